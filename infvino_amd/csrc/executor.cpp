@@ -1,0 +1,1465 @@
+// HIP-native plan executor (MI355X / gfx950).
+//
+// Mirrors src/PlanModel.cpp of the reference: parse (447-573), graph fusions (575-882),
+// activation memory plan (884-1210), per-node dispatch (run, 3127-4178), readOutput /
+// readTensor (4180-4200).  Designed for one GPU with a batch of B images:
+//   * every node describes one image; B is folded into the kernels' outer grid axis
+//     (implicit-GEMM convs fold it into M), inits are shared by all images;
+//   * conv-domain tensors are stored channels-last (NHWC, pixel stride rounded up to 8)
+//     so MFMA operands are 16-byte loads; tensors that feed reshape/softmax/permute/bmm
+//     or broadcasting stay NCHW, exactly the plan's layout;
+//   * concat along channels and channel splits are zero-copy: the producers of a
+//     concat's inputs write straight into the concat buffer at their channel offset
+//     (the conv "concat write-offset" epilogue); splits are views;
+//   * residual adds fold into the producing conv's epilogue (act first, then +res);
+//   * activations live in one arena, placed by liveness (best fit), sized per image;
+//   * the whole plan is replayed as one captured HIP graph per batch size.
+#include "executor.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <numeric>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+
+#include "../../include/ivh.h"
+#include "kernels.hpp"
+
+namespace ivh {
+
+#define HIPCHECK(expr)                                                                   \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e_) + " at " \
+                               + #expr);                                                 \
+  } while (0)
+
+namespace {
+
+long prod(const std::vector<int64_t> & d)
+{
+  long n = 1;
+  for (auto v : d) n *= (v < 0 ? 0 : v);
+  return n;
+}
+long round_up(long v, long m) { return (v + m - 1) / m * m; }
+
+std::vector<std::string> split_csv(const std::string & s)
+{
+  std::vector<std::string> out;
+  if (s == "-") return out;
+  std::stringstream ss(s);
+  std::string t;
+  while (std::getline(ss, t, ',')) out.push_back(t);
+  return out;
+}
+
+float h2f(uint16_t h)
+{
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu, f;
+  if (exp == 0) {
+    if (mant == 0) f = sign;
+    else {
+      int e = -14;
+      while (!(mant & 0x400u)) { mant <<= 1; --e; }
+      f = sign | ((uint32_t)(e + 127) << 23) | ((mant & 0x3ffu) << 13);
+    }
+  } else if (exp == 31) f = sign | 0x7f800000u | (mant << 13);
+  else f = sign | ((exp + 112u) << 23) | (mant << 13);
+  float o;
+  std::memcpy(&o, &f, 4);
+  return o;
+}
+
+int unary_to_act(int op)  // ew_unary table (kernels/ops.cl:50-63) -> canonical codes
+{
+  static const int m[5] = {kActSigmoid, kActSiLU, kActReLU, kActHSwish, kActHSigmoid};
+  return (op >= 0 && op < 5) ? m[op] : kActNone;
+}
+
+void check_batch(int batch, int maxb)
+{
+  if (batch < 1 || batch > maxb)
+    throw std::runtime_error("batch " + std::to_string(batch) + " out of range [1, " + std::to_string(maxb) + "]");
+}
+
+}  // namespace
+
+int PlanNode::i(const char * key, int def) const
+{
+  auto it = attr.find(key);
+  return it == attr.end() ? def : std::atoi(it->second.c_str());
+}
+std::string PlanNode::str(const char * key) const
+{
+  auto it = attr.find(key);
+  return it == attr.end() ? std::string() : it->second;
+}
+
+struct Model::Tensor {
+  std::string name;
+  std::vector<int64_t> dims;
+  enum Kind { kInput, kInit, kAct } kind = kAct;
+  std::string file;
+  int producer = -1;
+  std::vector<int> users;
+  int C = 1, H = 1, W = 1;  // per-image geometry (channel axis 1)
+  long numel = 1;
+  int root = -1;            // activation storage root
+  int coff = 0;             // channel offset in the root
+  long eoff = 0;            // element offset in the root when it is NCHW
+};
+
+struct Model::Root {
+  int C = 1, H = 1, W = 1;
+  long numel = 1;
+  int parent = -1;
+  int pcoff = 0;
+  bool reshaped = false, is_input = false, is_output = false, flat = false;
+  int layout = kNCHW;
+  int cs = 0;
+  long per_image = 0;
+  int first = INT_MAX, last = -1;
+  long off1 = 0;
+};
+
+// ================================================================ construction
+
+Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t flags)
+: plan_path_(plan_path), device_(device), max_batch_(max_batch), flags_(flags)
+{
+  if (max_batch < 1) throw std::runtime_error("max_batch must be >= 1");
+  dry_ = (flags_ & IVH_FLAG_DRY_RUN) != 0;
+  if (!dry_) {
+    int ndev = 0;
+    HIPCHECK(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev)
+      throw std::runtime_error("device index " + std::to_string(device) + " out of range (" +
+                               std::to_string(ndev) + " devices)");
+    HIPCHECK(hipSetDevice(device));
+  }
+  const auto pos = plan_path.find_last_of('/');
+  plan_dir_ = pos == std::string::npos ? std::string(".") : plan_path.substr(0, pos);
+  parse(plan_path);
+  if (!(flags_ & IVH_FLAG_NO_FUSE)) {
+    fuseResidual();
+    fuseActivation();
+  }
+  plan();
+  if (!dry_) HIPCHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  allocate();
+  uploadWeights();
+  buildStats();
+}
+
+Model::~Model()
+{
+  if (dry_) return;
+  (void)hipSetDevice(device_);
+  for (auto & g : graphs_) (void)hipGraphExecDestroy(g.second);
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (const auto & a : allocs_) (void)hipFree(reinterpret_cast<void *>(a.first));
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// ====================================================================== parse
+// Grammar of include/infvino/PlanModel.hpp:5-12; same errors as src/PlanModel.cpp:447-573.
+void Model::parse(const std::string & path)
+{
+  std::ifstream f(path);
+  if (!f) throw std::runtime_error("PlanModel: cannot open plan: " + path);
+  std::string line;
+  auto add = [&](const std::string & name, std::vector<int64_t> d, Tensor::Kind k) -> Tensor & {
+    auto t = std::make_unique<Tensor>();
+    t->name = name;
+    t->dims = std::move(d);
+    t->kind = k;
+    t->numel = prod(t->dims);
+    Tensor & ref = *t;
+    T_[name] = std::move(t);
+    return ref;
+  };
+  while (std::getline(f, line)) {
+    if (line.empty() || line[0] == '#') continue;
+    std::istringstream ls(line);
+    std::string kind;
+    ls >> kind;
+    if (kind == "input" || kind == "tensor") {
+      std::string name;
+      std::vector<int64_t> d;
+      ls >> name;
+      int64_t v;
+      while (ls >> v) d.push_back(v);
+      add(name, d, kind == "input" ? Tensor::kInput : Tensor::kAct);
+      if (kind == "input" && input_name_.empty()) {
+        input_name_ = name;
+        input_dims_ = d;
+      } else if (kind == "input") {
+        T_[name]->kind = Tensor::kAct;  // only the first input is the graph input
+      }
+    } else if (kind == "init") {
+      std::string name, file;
+      std::vector<int64_t> d;
+      ls >> name >> file;
+      int64_t v;
+      while (ls >> v) d.push_back(v);
+      Tensor & t = add(name, d, Tensor::kInit);
+      t.file = (file.empty() || file[0] == '/') ? file : (plan_dir_ + "/" + file);
+    } else if (kind == "node") {
+      PlanNode n;
+      std::string ins, outs;
+      ls >> n.op >> ins >> outs;
+      n.ins = split_csv(ins);
+      n.outs = split_csv(outs);
+      std::string kv;
+      while (ls >> kv) {
+        const auto p = kv.find('=');
+        if (p != std::string::npos) n.attr[kv.substr(0, p)] = kv.substr(p + 1);
+      }
+      if (n.outs.empty()) throw std::runtime_error("PlanModel: node without output: " + line);
+      nodes_.push_back(std::move(n));
+    } else if (kind == "output") {
+      std::string name;
+      ls >> name;
+      if (!name.empty()) outputs_.push_back(name);
+    }
+  }
+  if (input_name_.empty()) throw std::runtime_error("PlanModel: plan has no 'input' line");
+  if (outputs_.empty()) throw std::runtime_error("PlanModel: plan has no 'output' line");
+  for (const auto & o : outputs_)
+    if (!T_.count(o)) throw std::runtime_error("PlanModel: output tensor not declared: " + o);
+  for (const auto & n : nodes_) {
+    for (const auto & i : n.ins)
+      if (i != "-" && !T_.count(i)) throw std::runtime_error("PlanModel: missing tensor: " + i);
+    for (const auto & o : n.outs)
+      if (o != "-" && !T_.count(o)) throw std::runtime_error("PlanModel: missing tensor: " + o);
+  }
+  for (auto & kv : T_) {
+    Tensor & t = *kv.second;
+    const auto & d = t.dims;
+    if (d.size() >= 2) {
+      t.C = (int)d[1];
+      long hw = t.C > 0 ? t.numel / t.C : 0;
+      t.H = d.size() >= 4 ? (int)d[2] : 1;
+      t.W = t.H > 0 ? (int)(hw / t.H) : 0;
+    } else {
+      t.C = (int)t.numel;
+      t.H = t.W = 1;
+    }
+  }
+}
+
+// ====================================================================== fusions
+
+// conv + same-shape Add -> conv epilogue residual (act first, then +res), the reference's
+// fuseResidualAdd (src/PlanModel.cpp:667-740) extended to conv3x3.
+void Model::fuseResidual()
+{
+  std::map<std::string, int> producer, uses;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & o : nodes_[i].outs) producer[o] = (int)i;
+  for (const auto & n : nodes_)
+    for (const auto & in : n.ins)
+      if (in != "-") ++uses[in];
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  std::vector<char> remove(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    PlanNode & e = nodes_[i];
+    if (e.op != "ew_binary" || e.i("op") != 0 || e.ins.size() < 2) continue;
+    if (e.has("bdims") || e.i("b_scalar") != 0) continue;
+    const Tensor & yo = *T_[e.outs[0]];
+    for (int k = 0; k < 2; ++k) {
+      const std::string & pname = e.ins[k];
+      const std::string & rname = e.ins[1 - k];
+      auto pit = producer.find(pname);
+      if (pit == producer.end()) continue;
+      PlanNode & c = nodes_[pit->second];
+      if (c.op != "conv1x1" && c.op != "conv3x3") continue;
+      if (uses[pname] != 1 || outs.count(pname) || c.outs[0] != pname) continue;
+      const Tensor & pt = *T_[pname];
+      const Tensor & rt = *T_[rname];
+      if (rt.kind == Tensor::kInit || pt.numel != yo.numel || rt.numel != yo.numel) continue;
+      if (pt.dims != yo.dims || rt.dims != yo.dims) continue;
+      auto rit = producer.find(rname);
+      if (rt.kind != Tensor::kInput && (rit == producer.end() || rit->second >= pit->second)) continue;
+      if (c.ins.size() > 3 && c.ins[3] != "-") continue;
+      if (c.ins.size() < 4) c.ins.resize(4, "-");
+      c.ins[3] = rname;
+      c.outs[0] = e.outs[0];
+      producer.erase(pname);
+      producer[e.outs[0]] = pit->second;
+      remove[i] = 1;
+      break;
+    }
+  }
+  std::vector<PlanNode> kept;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if (!remove[i]) kept.push_back(std::move(nodes_[i]));
+  nodes_ = std::move(kept);
+}
+
+// conv3x3 / conv_general without act + sole ew_unary consumer -> folded activation.
+// (onnx2plan.py:135-147 can fold only HardSwish into conv3x3; ReLU/HardSigmoid/Sigmoid
+// after a 3x3 stay separate in the plan.)  Numerically the reference rounds the conv
+// output to fp16 before the activation; folding drops that intermediate rounding.
+void Model::fuseActivation()
+{
+  std::map<std::string, int> producer, uses;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & o : nodes_[i].outs) producer[o] = (int)i;
+  for (const auto & n : nodes_)
+    for (const auto & in : n.ins)
+      if (in != "-") ++uses[in];
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  std::vector<char> remove(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    PlanNode & u = nodes_[i];
+    if (u.op != "ew_unary" || u.ins.empty()) continue;
+    auto pit = producer.find(u.ins[0]);
+    if (pit == producer.end()) continue;
+    PlanNode & c = nodes_[pit->second];
+    const bool conv = c.op == "conv3x3" || c.op == "conv_general" || c.op == "conv1x1";
+    if (!conv || c.i("act") != 0 || uses[u.ins[0]] != 1 || outs.count(u.ins[0])) continue;
+    if (c.ins.size() > 3 && c.ins[3] != "-") continue;  // residual would be added before act
+    if (T_[u.ins[0]]->numel != T_[u.outs[0]]->numel) continue;
+    c.attr["act"] = std::to_string(unary_to_act(u.i("op")));
+    c.outs[0] = u.outs[0];
+    producer[u.outs[0]] = pit->second;
+    remove[i] = 1;
+  }
+  std::vector<PlanNode> kept;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if (!remove[i]) kept.push_back(std::move(nodes_[i]));
+  nodes_ = std::move(kept);
+}
+
+// ====================================================================== planning
+
+// ew_binary whose smaller operand is one value per output channel ([.., C, 1, 1]), the
+// reference's ew_binary_ch pattern (src/PlanModel.cpp:2603-2623).  Returns 1 if that
+// operand is `a`, 0 if it is `b`, -1 if the node is not such a broadcast.
+int Model::chanBroadcast(const PlanNode & n) const
+{
+  if (n.op != "ew_binary" || !n.has("bdims") || n.i("b_scalar") == 1 || n.ins.size() < 2) return -1;
+  const Tensor & at = *T_.at(n.ins[0]);
+  const Tensor & bt = *T_.at(n.ins[1]);
+  const Tensor & yt = *T_.at(n.outs[0]);
+  const Tensor * s = nullptr;
+  int a_is = 0;
+  if (at.numel != yt.numel && bt.numel == yt.numel) { s = &at; a_is = 1; }
+  else if (bt.numel != yt.numel && at.numel == yt.numel) s = &bt;
+  if (!s || s->numel != yt.C || yt.dims.size() < 3) return -1;
+  int nonunit = 0, pos = -1;
+  for (size_t i = 0; i < s->dims.size(); ++i)
+    if (s->dims[i] != 1) { ++nonunit; pos = (int)i; }
+  const int chidx = (int)s->dims.size() - 3;
+  if (nonunit == 1 && pos == chidx && s->dims.size() == yt.dims.size()) return a_is;
+  if (nonunit == 0 && yt.C == 1) return a_is;
+  return -1;
+}
+
+void Model::plan()
+{
+  for (auto & kv : T_) { kv.second->users.clear(); kv.second->producer = -1; }
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    for (const auto & in : nodes_[i].ins)
+      if (in != "-") T_[in]->users.push_back((int)i);
+    for (const auto & o : nodes_[i].outs)
+      if (o != "-") T_[o]->producer = (int)i;
+  }
+  skip_.assign(nodes_.size(), 0);
+  assignViews();
+  chooseLayouts();
+}
+
+// Views: every activation tensor gets a root; reshape/flatten alias, copy_c is a channel
+// view, channel concat redirects its inputs' roots into the concat root.
+void Model::assignViews()
+{
+  roots_.clear();
+  auto new_root = [&](Tensor & t) {
+    auto r = std::make_unique<Root>();
+    r->C = t.C; r->H = t.H; r->W = t.W; r->numel = t.numel;
+    r->flat = t.dims.size() != 4;
+    t.root = (int)roots_.size();
+    t.coff = 0;
+    t.eoff = 0;
+    roots_.push_back(std::move(r));
+  };
+  Tensor & in = *T_[input_name_];
+  new_root(in);
+  roots_[in.root]->is_input = true;
+  // resolve the current final root and offsets of a tensor through redirects
+  auto resolve = [&](const Tensor & t, int & coff, long & eoff) {
+    int r = t.root;
+    coff = t.coff;
+    eoff = t.eoff;
+    while (roots_[r]->parent >= 0) {
+      const Root & rr = *roots_[r];
+      const Root & pp = *roots_[rr.parent];
+      coff += rr.pcoff;
+      eoff += (long)rr.pcoff * pp.H * pp.W;
+      r = rr.parent;
+    }
+    return r;
+  };
+  const bool no_views = (flags_ & IVH_FLAG_NO_FUSE) != 0;
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    PlanNode & n = nodes_[ni];
+    Tensor & out = *T_[n.outs[0]];
+    if (n.op == "reshape" || n.op == "flatten") {
+      const Tensor & src = *T_[n.ins.at(0)];
+      if (src.numel != out.numel) throw std::runtime_error("reshape numel mismatch: " + out.name);
+      if (src.kind == Tensor::kInit) { new_root(out); continue; }  // materialised by a copy
+      out.root = src.root;
+      out.coff = src.coff;
+      out.eoff = src.eoff;
+      roots_[src.root]->reshaped = true;
+      skip_[ni] = 1;
+      continue;
+    }
+    if (n.op == "copy_c" && !no_views && n.i("dst_off") == 0) {
+      const Tensor & src = *T_[n.ins.at(0)];
+      const int HW = n.i("HW", 1), c0 = n.i("c0"), cnt = n.i("cnt");
+      if (src.kind == Tensor::kAct && (long)src.H * src.W == HW && c0 + cnt <= src.C &&
+          out.numel == (long)cnt * HW && out.H * out.W == HW) {
+        out.root = src.root;
+        out.coff = src.coff + c0;
+        out.eoff = src.eoff + (long)c0 * HW;
+        skip_[ni] = 1;
+        continue;
+      }
+    }
+    if (out.root < 0) new_root(out);
+    for (size_t k = 1; k < n.outs.size(); ++k)
+      if (T_[n.outs[k]]->root < 0) new_root(*T_[n.outs[k]]);
+    if (n.op == "concat4" && !no_views && n.i("outer", 1) == 1) {
+      const int cnt[4] = {n.i("ca"), n.i("cb"), n.i("cc"), n.i("cd")};
+      int off[4], tot = 0;
+      for (int j = 0; j < 4; ++j) { off[j] = tot; tot += cnt[j]; }
+      const int inner = n.i("inner", 1);
+      const Root & Q = *roots_[out.root];
+      const bool plain = tot == out.C && (long)Q.H * Q.W == inner;
+      for (int j = 0; plain && j < 4; ++j) {
+        if (cnt[j] <= 0) continue;
+        const Tensor & t = *T_[n.ins.at(j)];
+        int tc;
+        long te;
+        if (t.kind != Tensor::kAct) continue;
+        const int r = resolve(t, tc, te);
+        Root & R = *roots_[r];
+        const int qroot = out.root;
+        if (r == qroot) continue;  // already redirected into this concat (same root, earlier input)
+        const int base = off[j] - tc;
+        bool ok = R.parent < 0 && !R.is_input && !R.is_output && r != qroot &&
+                  (long)R.H * R.W == inner && base >= 0 && base + R.C <= tot && t.C == cnt[j];
+        for (const auto & o : outputs_)
+          if (T_[o]->root == r) ok = false;
+        // every concat input overlapping R's channel range must be the matching view of R
+        for (int k = 0; ok && k < 4; ++k) {
+          if (cnt[k] <= 0) continue;
+          const int lo = std::max(off[k], base), hi = std::min(off[k] + cnt[k], base + R.C);
+          if (lo >= hi) continue;
+          const Tensor & tk = *T_[n.ins.at(k)];
+          int kc;
+          long ke;
+          if (tk.kind != Tensor::kAct || resolve(tk, kc, ke) != r || off[k] - kc != base ||
+              off[k] < base || off[k] + cnt[k] > base + R.C)
+            ok = false;
+        }
+        if (!ok) continue;
+        R.parent = qroot;
+        R.pcoff = base;
+      }
+      // inputs that now resolve into the concat root at their own offset need no copy
+      bool done = true;
+      for (int j = 0; j < 4; ++j) {
+        if (cnt[j] <= 0) continue;
+        const Tensor & t = *T_[n.ins.at(j)];
+        int tc;
+        long te;
+        if (t.kind != Tensor::kAct || resolve(t, tc, te) != out.root || tc != off[j]) done = false;
+      }
+      if (done && plain) skip_[ni] = 1;
+    }
+  }
+  // every remaining activation without a root (e.g. declared but produced by nothing)
+  for (auto & kv : T_)
+    if (kv.second->kind == Tensor::kAct && kv.second->root < 0) new_root(*kv.second);
+  // collapse redirects: every tensor points at its final root
+  for (auto & kv : T_) {
+    Tensor & t = *kv.second;
+    if (t.root < 0) continue;
+    int c;
+    long e;
+    const int r = resolve(t, c, e);
+    t.root = r;
+    t.coff = c;
+    t.eoff = e;
+  }
+  for (const auto & o : outputs_) roots_[T_[o]->root]->is_output = true;
+  // reshape flags propagate to final roots
+  for (size_t i = 0; i < roots_.size(); ++i) {
+    if (!roots_[i]->reshaped) continue;
+    int r = (int)i;
+    while (roots_[r]->parent >= 0) r = roots_[r]->parent;
+    roots_[r]->reshaped = true;
+  }
+}
+
+// NHWC for conv-domain roots whose every reader and writer handles channels-last.
+void Model::chooseLayouts()
+{
+  // which (node, slot) reads accept NHWC
+  auto reader_ok = [&](const PlanNode & n, size_t slot, const Tensor & t) -> bool {
+    const std::string & op = n.op;
+    if (op == "conv3x3") return slot == 0 || slot == 3;
+    if (op == "conv1x1") return slot == 1 || slot == 3;
+    if (op == "conv_general") return slot == 0;
+    if (op == "maxpool" || op == "resize_nn" || op == "gap" || op == "ew_unary") return true;
+    if (op == "copy_c") return n.i("dst_off") == 0;
+    if (op == "concat4") return n.i("outer", 1) == 1;
+    if (op == "ew_binary") {
+      const Tensor & y = *T_[n.outs[0]];
+      if (!n.has("bdims") || n.i("b_scalar") == 1) return t.numel == y.numel;
+      return chanBroadcast(n) >= 0 && t.numel == y.numel;  // big operand of a per-channel broadcast
+    }
+    return false;
+  };
+  auto writer_ok = [&](const PlanNode & n) -> bool {
+    const std::string & op = n.op;
+    if (op == "conv3x3" || op == "conv1x1" || op == "conv_general" || op == "maxpool" ||
+        op == "resize_nn" || op == "ew_unary")
+      return true;
+    if (op == "copy_c") return n.i("dst_off") == 0;
+    if (op == "concat4") return n.i("outer", 1) == 1;
+    if (op == "ew_binary") return !n.has("bdims") || n.i("b_scalar") == 1 || chanBroadcast(n) >= 0;
+    return false;
+  };
+  std::vector<char> ok(roots_.size(), 1);
+  for (size_t i = 0; i < roots_.size(); ++i) {
+    const Root & r = *roots_[i];
+    if (r.parent >= 0 || r.reshaped || r.is_input || r.is_output || r.flat || (long)r.H * r.W <= 1)
+      ok[i] = 0;
+  }
+  if (flags_ & IVH_FLAG_NCHW_ONLY) std::fill(ok.begin(), ok.end(), 0);
+  for (auto & kv : T_) {
+    const Tensor & t = *kv.second;
+    if (t.kind != Tensor::kAct || t.root < 0) continue;
+    if (!ok[t.root]) continue;
+    if ((long)t.H * t.W != (long)roots_[t.root]->H * roots_[t.root]->W || t.dims.size() != 4) {
+      ok[t.root] = 0;
+      continue;
+    }
+    if (t.producer >= 0 && !writer_ok(nodes_[t.producer])) ok[t.root] = 0;
+    for (int u : t.users) {
+      const PlanNode & n = nodes_[u];
+      for (size_t s = 0; s < n.ins.size(); ++s)
+        if (n.ins[s] == t.name && !reader_ok(n, s, t)) ok[t.root] = 0;
+    }
+  }
+  for (size_t i = 0; i < roots_.size(); ++i) {
+    Root & r = *roots_[i];
+    r.layout = ok[i] ? kNHWC : kNCHW;
+    const long HW = (long)r.H * r.W;
+    if (r.layout == kNHWC) {
+      r.cs = (int)round_up(r.C, 8);
+      r.per_image = round_up(HW * r.cs, 64);
+    } else {
+      r.cs = (int)HW;
+      r.per_image = round_up(std::max<long>(r.numel, 8), 64);
+    }
+  }
+}
+
+// ============================================================ memory + weights
+
+// Device allocation; in a dry run (no GPU) a unique fake address is handed out instead so the
+// planner and the launch validator run on any host.  Every allocation is registered so each
+// launch's address range can be checked before it is enqueued.
+void * Model::devAlloc(size_t bytes, bool zero)
+{
+  bytes = (size_t)round_up((long)std::max<size_t>(bytes, 256), 256);
+  void * d = nullptr;
+  if (dry_) {
+    d = reinterpret_cast<void *>(fake_next_);
+    fake_next_ += round_up((long)bytes + 4096, 4096);
+  } else {
+    HIPCHECK(hipMalloc(&d, bytes));
+    if (zero) HIPCHECK(hipMemset(d, 0, bytes));
+  }
+  allocs_.push_back({reinterpret_cast<uintptr_t>(d), bytes});
+  return d;
+}
+
+void Model::devUpload(void * d, const void * src, size_t bytes)
+{
+  if (!dry_) HIPCHECK(hipMemcpy(d, src, bytes, hipMemcpyHostToDevice));
+}
+
+void Model::allocate()
+{
+  // liveness over final roots
+  for (auto & r : roots_) { r->first = INT_MAX; r->last = -1; }
+  const int N = (int)nodes_.size();
+  for (int ni = 0; ni < N; ++ni) {
+    for (const auto & in : nodes_[ni].ins) {
+      if (in == "-") continue;
+      const Tensor & t = *T_[in];
+      if (t.root < 0 || t.kind == Tensor::kInit) continue;
+      Root & r = *roots_[t.root];
+      r.last = std::max(r.last, ni);
+      r.first = std::min(r.first, ni);
+    }
+    for (const auto & o : nodes_[ni].outs) {
+      const Tensor & t = *T_[o];
+      if (t.root < 0) continue;
+      Root & r = *roots_[t.root];
+      r.first = std::min(r.first, ni);
+      r.last = std::max(r.last, ni);
+    }
+  }
+  for (const auto & o : outputs_) roots_[T_[o]->root]->last = N + 1;
+  // best-fit placement, largest first, on closed [first, last] intervals
+  std::vector<int> order;
+  for (size_t i = 0; i < roots_.size(); ++i) {
+    const Root & r = *roots_[i];
+    if (r.parent >= 0 || r.is_input || r.first == INT_MAX) continue;
+    order.push_back((int)i);
+  }
+  const bool no_reuse = (flags_ & IVH_FLAG_NO_REUSE) != 0;
+  std::sort(order.begin(), order.end(), [&](int a, int b) {
+    return roots_[a]->per_image != roots_[b]->per_image ? roots_[a]->per_image > roots_[b]->per_image : a < b;
+  });
+  std::vector<int> placed;
+  long total = 0;
+  for (int id : order) {
+    Root & r = *roots_[id];
+    std::vector<std::pair<long, long>> busy;
+    for (int pid : placed) {
+      const Root & p = *roots_[pid];
+      if (no_reuse || !(p.last < r.first || r.last < p.first)) busy.push_back({p.off1, p.off1 + p.per_image});
+    }
+    std::sort(busy.begin(), busy.end());
+    long best = -1, best_gap = LONG_MAX, cur = 0;
+    for (auto & iv : busy) {
+      if (iv.first - cur >= r.per_image && iv.first - cur < best_gap) { best = cur; best_gap = iv.first - cur; }
+      cur = std::max(cur, iv.second);
+    }
+    if (best < 0) best = cur;
+    r.off1 = best;
+    total = std::max(total, best + r.per_image);
+    placed.push_back(id);
+  }
+  arena_elems1_ = total;
+  arena_ = devAlloc((size_t)std::max<long>(total, 64) * max_batch_ * 2, true);
+  const Tensor & in = *T_[input_name_];
+  const long in_img = roots_[in.root]->per_image;
+  input_buf_ = devAlloc((size_t)in_img * max_batch_ * 2, true);
+}
+
+void Model::uploadWeights()
+{
+  // raw fp16 inits (used by small ops and as operand views)
+  std::map<std::string, std::vector<uint16_t>> host;
+  for (auto & kv : T_) {
+    Tensor & t = *kv.second;
+    if (t.kind != Tensor::kInit) continue;
+    std::vector<uint16_t> buf((size_t)t.numel);
+    std::ifstream f(t.file, std::ios::binary);
+    if (!f) throw std::runtime_error("PlanModel: cannot open init " + t.file);
+    f.read(reinterpret_cast<char *>(buf.data()), (std::streamsize)(buf.size() * 2));
+    if ((size_t)f.gcount() != buf.size() * 2)
+      throw std::runtime_error("PlanModel: init file too short: " + t.file);
+    const size_t bytes = round_up((long)buf.size() * 2 + 16, 256);
+    void * d = devAlloc(bytes, true);
+    devUpload(d, buf.data(), buf.size() * 2);
+    dev_allocs_.push_back(d);
+    weight_bytes_ += bytes;
+    init_dev_[t.name] = d;
+    host[t.name] = std::move(buf);
+  }
+  packed_.assign(nodes_.size(), Packed{});
+  auto upload = [&](const void * src, size_t bytes) -> void * {
+    void * d = devAlloc(bytes, false);
+    devUpload(d, src, bytes);
+    dev_allocs_.push_back(d);
+    weight_bytes_ += round_up((long)bytes, 256);
+    return d;
+  };
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    const PlanNode & n = nodes_[ni];
+    const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
+    if (!(is1 || is3 || isg) || skip_[ni]) continue;
+    const std::string wname = is1 ? n.ins.at(0) : n.ins.at(1);
+    const Tensor & wt = *T_[wname];
+    if (wt.kind != Tensor::kInit) throw std::runtime_error("conv weight is not an init: " + wname);
+    const std::vector<uint16_t> & W = host[wname];
+    const int Cout = (int)wt.dims.at(0);
+    const int K = is1 ? 1 : (is3 ? 3 : n.i("K", 3));
+    const int G = isg ? n.i("G", 1) : 1;
+    const int cin_g = (int)(wt.numel / ((long)Cout * K * K));
+    const std::string bname = n.ins.size() > 2 ? n.ins[2] : "-";
+    Packed pk;
+    if (bname != "-") {
+      const auto & B = host.at(bname);
+      if ((long)B.size() < Cout) throw std::runtime_error("bias too short: " + bname);
+      std::vector<float> bf(round_up(Cout, kIgemmRowPad) + 16, 0.0f);
+      for (int c = 0; c < Cout; ++c) bf[c] = h2f(B[c]);
+      pk.bias = static_cast<float *>(upload(bf.data(), bf.size() * 4));
+    }
+    // kernel family decided here (layouts are known): 0 igemm, 1 direct, 2 depthwise
+    const Tensor & x = *T_[is1 ? n.ins.at(1) : n.ins.at(0)];
+    const int Cin = is1 ? (int)wt.dims.at(1) : x.C;
+    const bool dw = isg && G == Cin && Cout == Cin && (K == 3 || K == 5);
+    const Root & xr = *roots_[x.root < 0 ? 0 : x.root];
+    const bool x_nhwc = x.kind == Tensor::kAct && xr.layout == kNHWC && (x.coff % 8) == 0;
+    long Nx = is1 ? x.numel / std::max(Cin, 1) : (long)x.H * x.W;
+    const bool x_vec1 = is1 && Nx == 1 && x.kind != Tensor::kInit && (x.eoff % 8) == 0 && xr.layout == kNCHW;
+    int kind;
+    if (dw) kind = 2;
+    else if (G == 1 && (x_nhwc || x_vec1)) kind = 0;
+    else kind = 1;
+    if (flags_ & IVH_FLAG_DIRECT_ONLY) kind = dw ? 2 : 1;
+    pk.kind = kind;
+    if (kind == 0) {
+      const int cin8 = (int)round_up(cin_g, 8);
+      const int kpad = (int)round_up((long)K * K * cin8, kIgemmBK);
+      const int rows = (int)round_up(Cout, kIgemmRowPad);
+      std::vector<uint16_t> P((size_t)rows * kpad, 0);
+      for (int co = 0; co < Cout; ++co)
+        for (int ci = 0; ci < cin_g; ++ci)
+          for (int ky = 0; ky < K; ++ky)
+            for (int kx = 0; kx < K; ++kx)
+              P[(size_t)co * kpad + (ky * K + kx) * cin8 + ci] = W[(((size_t)co * cin_g + ci) * K + ky) * K + kx];
+      pk.w = upload(P.data(), P.size() * 2);
+      pk.cin8 = cin8;
+      pk.kpad = kpad;
+    } else if (kind == 1) {
+      const int cout_g = Cout / G;
+      std::vector<float> P((size_t)G * cin_g * K * K * cout_g + 32, 0.0f);
+      for (int co = 0; co < Cout; ++co) {
+        const int g = co / cout_g, cl = co % cout_g;
+        for (int ci = 0; ci < cin_g; ++ci)
+          for (int t = 0; t < K * K; ++t)
+            P[(((size_t)g * cin_g + ci) * K * K + t) * cout_g + cl] = h2f(W[((size_t)co * cin_g + ci) * K * K + t]);
+      }
+      pk.w = upload(P.data(), P.size() * 4);
+    } else {
+      std::vector<float> P((size_t)K * K * Cout + 8, 0.0f);
+      for (int c = 0; c < Cout; ++c)
+        for (int t = 0; t < K * K; ++t) P[(size_t)t * Cout + c] = h2f(W[(size_t)c * K * K + t]);
+      pk.w = upload(P.data(), P.size() * 4);
+    }
+    packed_[ni] = pk;
+  }
+}
+
+// ==================================================================== dispatch
+
+View Model::view(const std::string & name, int batch) const
+{
+  const Tensor & t = *T_.at(name);
+  View v;
+  if (t.kind == Tensor::kInit) {
+    v.ptr = static_cast<__half *>(init_dev_.at(name));
+    v.img = 0;
+    v.layout = kNCHW;
+    v.cs = t.H * t.W;
+    return v;
+  }
+  const Root & r = *roots_.at(t.root);
+  __half * base;
+  if (r.is_input) base = static_cast<__half *>(input_buf_);
+  else base = static_cast<__half *>(arena_) + r.off1 * batch;
+  v.img = r.per_image;
+  v.layout = r.layout;
+  if (r.layout == kNHWC) {
+    v.ptr = base + t.coff;
+    v.cs = r.cs;
+  } else {
+    v.ptr = base + t.eoff;
+    v.cs = t.H * t.W;
+  }
+  return v;
+}
+
+void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
+{
+  const PlanNode & n = nodes_[ni];
+  const Tensor & yt = *T_[n.outs[0]];
+  auto has = [&](size_t i) { return i < n.ins.size() && n.ins[i] != "-"; };
+  auto fail = [&](const std::string & m) { throw std::runtime_error("node " + n.op + " -> " + yt.name + ": " + m); };
+  const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
+  if (is1 || is3 || isg) {
+    const Packed & pk = packed_[ni];
+    const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
+    const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
+    Launch L;
+    ConvParams & p = L.cp;
+    p.batch = batch;
+    p.Cout = (int)wt.dims[0];
+    if (is1) {
+      p.Cin = (int)wt.dims[1];
+      const long N = xt.numel / std::max(p.Cin, 1);
+      if (xt.numel != N * p.Cin) fail("x numel not a multiple of Cin");
+      if (xt.dims.size() == 4 && (long)xt.H * xt.W == N && xt.C == p.Cin) { p.H = xt.H; p.W = xt.W; }
+      else { p.H = (int)N; p.W = 1; }
+      p.K = 1; p.S = 1; p.P = 0; p.G = 1;
+      p.Ho = p.H; p.Wo = p.W;
+    } else {
+      p.Cin = xt.C; p.H = xt.H; p.W = xt.W;
+      p.K = is3 ? 3 : n.i("K", 3);
+      p.S = is3 ? n.i("stride", 1) : n.i("S", 1);
+      p.P = is3 ? n.i("pad", 1) : n.i("P", 1);
+      p.G = isg ? n.i("G", 1) : 1;
+      p.Ho = n.i("Hout"); p.Wo = n.i("Wout");
+      if (p.Ho != (p.H + 2 * p.P - p.K) / p.S + 1 || p.Wo != (p.W + 2 * p.P - p.K) / p.S + 1)
+        fail("Hout/Wout inconsistent with input geometry");
+      if (wt.numel != (long)p.Cout * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
+    }
+    if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
+    if (yt.numel != (long)p.Cout * p.Ho * p.Wo) fail("output numel mismatch");
+    p.act = n.i("act");
+    p.bias = pk.bias;
+    p.w = static_cast<const __half *>(pk.w);
+    p.x = view(xt.name, batch);
+    p.y = view(yt.name, batch);
+    if (has(3)) {
+      const Tensor & rt = *T_[n.ins[3]];
+      if (rt.numel != yt.numel) fail("residual numel mismatch");
+      p.r = view(rt.name, batch);
+    }
+    // single-pixel tensors: NCHW and NHWC coincide; present them channels-last
+    auto pix1 = [](View & v, int C) { v.layout = kNHWC; v.cs = (int)round_up(C, 8); };
+    if (p.H * p.W == 1) pix1(p.x, p.Cin);
+    if (p.Ho * p.Wo == 1) { pix1(p.y, p.Cout); if (p.r.ptr) pix1(p.r, p.Cout); }
+    if (pk.kind == 0) {
+      L.kind = Launch::kIgemm;
+      p.cin8 = pk.cin8;
+      p.kpad = pk.kpad;
+      if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) ||
+          (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
+        fail("implicit-GEMM input view not 16-byte aligned NHWC");
+      if (p.kpad < p.K * p.K * p.cin8 || p.cin8 < p.Cin) fail("packed weight geometry");
+    } else if (pk.kind == 1) {
+      L.kind = Launch::kDirect;
+    } else {
+      L.kind = Launch::kDw;
+    }
+    out.push_back(L);
+    return;
+  }
+
+  Launch L;
+  L.kind = Launch::kSmall;
+  SmallParams & q = L.sp;
+  q.batch = batch;
+  q.y = view(yt.name, batch);
+  q.C = yt.C; q.H = yt.H; q.W = yt.W;
+  const std::string & op = n.op;
+  if (op == "reshape" || op == "flatten") {  // init source: materialise by a copy
+    q.a = view(n.ins[0], batch);
+    q.C = 1; q.H = 1; q.W = (int)yt.numel;
+    q.a.layout = q.y.layout = kNCHW;
+    q.a.cs = q.y.cs = (int)yt.numel;
+    L.small = kCopy;
+    out.push_back(L);
+    return;
+  }
+  if (op == "ew_binary") {
+    const Tensor & at = *T_[n.ins.at(0)];
+    const Tensor & bt = *T_[n.ins.at(1)];
+    q.op = n.i("op");
+    q.a = view(at.name, batch);
+    q.b = view(bt.name, batch);
+    if (!n.has("bdims") || n.i("b_scalar") == 1) {
+      if (n.i("b_scalar") == 1) {
+        if (at.numel != yt.numel || bt.numel < 1) fail("scalar ew_binary shapes");
+        q.b.img = 0;
+        q.b.cs = 0;
+      } else if (at.numel != yt.numel || bt.numel != yt.numel) {
+        fail("ew_binary without bdims needs equal numel");
+      }
+      L.small = kEwSame;
+      out.push_back(L);
+      return;
+    }
+    // per-channel broadcast (ew_binary_ch) when one operand is [.., C, 1, 1]
+    const int a_is_chan = chanBroadcast(n);
+    if (a_is_chan >= 0) {
+      q.i0 = a_is_chan;
+      L.small = kEwChan;
+      out.push_back(L);
+      return;
+    }
+    // general broadcast: NCHW flat
+    std::vector<int> v;
+    {
+      std::stringstream ss(n.str("bdims"));
+      std::string tk;
+      while (std::getline(ss, tk, ',')) v.push_back(std::atoi(tk.c_str()));
+    }
+    const int rank = (int)v.size() / 3;
+    if (rank < 1 || rank > 6 || (int)v.size() != rank * 3) fail("bad bdims");
+    long no = 1, amax = 0, bmax = 0;
+    for (int r = 0; r < rank; ++r) {
+      no *= v[r];
+      amax += (long)(v[r] - 1) * v[rank + r];
+      bmax += (long)(v[r] - 1) * v[2 * rank + r];
+    }
+    if (no != yt.numel || amax >= at.numel || bmax >= bt.numel) fail("bdims out of operand bounds");
+    if (q.a.layout != kNCHW || q.b.layout != kNCHW || q.y.layout != kNCHW) fail("broadcast needs NCHW operands");
+    q.rank = rank;
+    for (int i = 0; i < rank * 3; ++i) q.dims[i] = v[i];
+    q.n = yt.numel;
+    L.small = kEwBcast;
+    out.push_back(L);
+    return;
+  }
+  if (op == "ew_unary") {
+    const Tensor & at = *T_[n.ins.at(0)];
+    if (at.numel != yt.numel) fail("ew_unary numel");
+    q.a = view(at.name, batch);
+    q.op = unary_to_act(n.i("op"));
+    L.small = kEwUnary;
+    out.push_back(L);
+    return;
+  }
+  if (op == "bias_add") {
+    const Tensor & at = *T_[n.ins.at(0)];
+    const Tensor & bt = *T_[n.ins.at(1)];
+    q.a = view(at.name, batch);
+    q.b = view(bt.name, batch);
+    q.i0 = std::max(1, n.i("HW", 1));
+    q.n = yt.numel;
+    if (at.numel != yt.numel || (yt.numel - 1) / q.i0 >= bt.numel) fail("bias_add shapes");
+    if (q.a.layout != kNCHW || q.y.layout != kNCHW) fail("bias_add needs NCHW");
+    L.small = kBiasAdd;
+    out.push_back(L);
+    return;
+  }
+  if (op == "copy_c") {  // not a view: copy `cnt` channels into y at dst_off
+    const Tensor & xt = *T_[n.ins.at(0)];
+    const int HW = n.i("HW", 1), c0 = n.i("c0"), cnt = n.i("cnt"), dst = n.i("dst_off");
+    if ((long)(c0 + cnt) * HW > xt.numel || dst + (long)cnt * HW > yt.numel) fail("copy_c bounds");
+    View xv = view(xt.name, batch), yv = view(yt.name, batch);
+    if (xv.layout == kNHWC) {
+      if ((long)xt.H * xt.W != HW || dst != 0) fail("copy_c on channels-last input");
+      q.a = xv;
+      q.a.ptr += c0;
+    } else {
+      q.a = xv;
+      q.a.ptr += (long)c0 * HW;
+      q.a.cs = HW;
+    }
+    if (yv.layout == kNHWC) {
+      if (dst != 0) fail("copy_c dst_off on channels-last output");
+      q.y = yv;
+    } else {
+      q.y = yv;
+      q.y.ptr += dst;
+      q.y.cs = HW;
+    }
+    q.C = cnt; q.H = 1; q.W = HW;
+    L.small = kCopy;
+    out.push_back(L);
+    return;
+  }
+  if (op == "slice_axis") {
+    const Tensor & xt = *T_[n.ins.at(0)];
+    q.a = view(xt.name, batch);
+    q.i0 = n.i("outer", 1); q.i1 = n.i("axdim"); q.i2 = n.i("inner", 1); q.i3 = n.i("start"); q.i4 = n.i("len");
+    if ((long)q.i0 * q.i1 * q.i2 > xt.numel || q.i3 + q.i4 > q.i1 || (long)q.i0 * q.i4 * q.i2 != yt.numel)
+      fail("slice_axis bounds");
+    if (q.a.layout != kNCHW || q.y.layout != kNCHW) fail("slice_axis needs NCHW");
+    L.small = kSliceAxis;
+    out.push_back(L);
+    return;
+  }
+  if (op == "concat4") {
+    const int cnt[4] = {n.i("ca"), n.i("cb"), n.i("cc"), n.i("cd")};
+    const int outer = n.i("outer", 1), inner = n.i("inner", 1);
+    const int tot = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+    if ((long)outer * tot * inner != yt.numel) fail("concat4 geometry");
+    int off = 0;
+    for (int j = 0; j < 4; ++j) {
+      if (cnt[j] <= 0) continue;
+      const Tensor & st = *T_[n.ins.at(j)];
+      if (st.numel != (long)outer * cnt[j] * inner) fail("concat4 input numel");
+      Launch Lj = L;
+      SmallParams & qj = Lj.sp;
+      qj.a = view(st.name, batch);
+      if (outer == 1) {
+        // skip inputs already written in place by their producer
+        if (st.kind == Tensor::kAct && st.root == yt.root && st.coff == yt.coff + off) { off += cnt[j]; continue; }
+        qj.y = view(yt.name, batch);
+        if (qj.y.layout == kNHWC) qj.y.ptr += off;
+        else { qj.y.ptr += (long)off * inner; qj.y.cs = inner; }
+        if (qj.a.layout == kNCHW) qj.a.cs = inner;
+        qj.C = cnt[j]; qj.H = 1; qj.W = inner;
+        if (qj.y.layout == kNHWC || qj.a.layout == kNHWC) {
+          if ((long)yt.H * yt.W != inner || (long)st.H * st.W != inner) fail("concat4 channels-last geometry");
+          qj.H = yt.H; qj.W = yt.W;
+        }
+        Lj.small = kCopy;
+      } else {
+        if (qj.a.layout != kNCHW || qj.y.layout != kNCHW) fail("concat4 outer>1 needs NCHW");
+        qj.i0 = outer; qj.i1 = cnt[j]; qj.i2 = inner; qj.i3 = tot; qj.i4 = off;
+        Lj.small = kConcatOuter;
+      }
+      out.push_back(Lj);
+      off += cnt[j];
+    }
+    return;
+  }
+  if (op == "maxpool" || op == "resize_nn") {
+    const Tensor & xt = *T_[n.ins.at(0)];
+    q.a = view(xt.name, batch);
+    q.C = n.i("C"); q.H = n.i("H"); q.W = n.i("W");
+    if (op == "maxpool") {
+      q.Ho = n.i("Hout"); q.Wo = n.i("Wout");
+      q.K = n.i("K", 5); q.S = n.i("S", 1); q.P = n.i("P", 2);
+      L.small = kMaxPool;
+    } else {
+      q.i0 = std::max(1, n.i("S", 2));
+      q.Ho = q.H * q.i0; q.Wo = q.W * q.i0;
+      L.small = kResizeNN;
+    }
+    if ((long)q.C * q.H * q.W != xt.numel || (long)q.C * q.Ho * q.Wo != yt.numel) fail("pool/resize geometry");
+    if ((q.a.layout == kNHWC && (long)xt.H * xt.W != (long)q.H * q.W) ||
+        (q.y.layout == kNHWC && (long)yt.H * yt.W != (long)q.Ho * q.Wo))
+      fail("pool/resize channels-last geometry");
+    if (q.a.layout == kNCHW) q.a.cs = q.H * q.W;
+    if (q.y.layout == kNCHW) q.y.cs = q.Ho * q.Wo;
+    out.push_back(L);
+    return;
+  }
+  if (op == "softmax_axis") {
+    const Tensor & xt = *T_[n.ins.at(0)];
+    q.a = view(xt.name, batch);
+    q.i0 = n.i("outer", 1); q.i1 = n.i("axdim"); q.i2 = n.i("inner", 1);
+    if ((long)q.i0 * q.i1 * q.i2 != xt.numel || xt.numel != yt.numel) fail("softmax geometry");
+    if (q.a.layout != kNCHW || q.y.layout != kNCHW) fail("softmax needs NCHW");
+    L.small = kSoftmax;
+    out.push_back(L);
+    return;
+  }
+  if (op == "permute_0213") {
+    const Tensor & xt = *T_[n.ins.at(0)];
+    q.a = view(xt.name, batch);
+    q.i0 = n.i("D1", 1); q.i1 = n.i("D2", 1); q.i2 = n.i("I", 1); q.op = n.i("mode");
+    if ((long)q.i0 * q.i1 * q.i2 != xt.numel || xt.numel != yt.numel) fail("permute geometry");
+    if (q.a.layout != kNCHW || q.y.layout != kNCHW) fail("permute needs NCHW");
+    L.small = kPermute;
+    out.push_back(L);
+    return;
+  }
+  if (op == "gap") {
+    const Tensor & xt = *T_[n.ins.at(0)];
+    q.a = view(xt.name, batch);
+    q.C = n.i("C");
+    const int HW = n.i("HW", 1);
+    q.H = 1; q.W = HW;
+    if ((long)q.C * HW != xt.numel || yt.numel != q.C) fail("gap geometry");
+    if (q.a.layout == kNHWC) { q.H = xt.H; q.W = xt.W; }
+    else q.a.cs = HW;
+    L.small = kGap;
+    out.push_back(L);
+    return;
+  }
+  if (op == "bmm" || op == "gemm") {
+    const Tensor & at = *T_[n.ins.at(0)];
+    const Tensor & bt = *T_[n.ins.at(1)];
+    q.a = view(at.name, batch);
+    q.b = view(bt.name, batch);
+    const auto & ad = at.dims;
+    const auto & bd = bt.dims;
+    if (ad.size() < 2 || bd.size() < 2) fail("matmul rank");
+    const int M = (int)ad[ad.size() - 2], K = (int)ad.back(), Nn = (int)bd.back();
+    const long BB = at.numel / ((long)M * K);
+    if ((long)K * Nn * BB != bt.numel && !((long)K * Nn == bt.numel && BB == 1)) fail("matmul operand shapes");
+    if (BB * M * Nn != yt.numel) fail("matmul output numel");
+    q.i0 = (int)BB; q.i1 = M; q.i2 = K; q.i3 = Nn;
+    if (q.a.layout != kNCHW || q.b.layout != kNCHW || q.y.layout != kNCHW) fail("matmul needs NCHW");
+    L.small = kBmm;
+    out.push_back(L);
+    return;
+  }
+  throw std::runtime_error("PlanModel: unknown op: " + op);
+}
+
+const std::vector<Launch> & Model::launches(int batch)
+{
+  auto it = launch_cache_.find(batch);
+  if (it != launch_cache_.end()) return it->second;
+  std::vector<Launch> L;
+  std::vector<size_t> beg(nodes_.size()), end(nodes_.size());
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    beg[ni] = L.size();
+    if (!skip_[ni]) emitNode(ni, batch, L);
+    end[ni] = L.size();
+  }
+  node_launch_begin_ = beg;
+  node_launch_end_ = end;
+  for (size_t ni = 0; ni < nodes_.size(); ++ni)
+    for (size_t i = beg[ni]; i < end[ni]; ++i) {
+      try {
+        validate(L[i]);
+      } catch (const std::exception & e) {
+        throw std::runtime_error("node " + nodes_[ni].op + " -> " + nodes_[ni].outs[0] + ": " + e.what());
+      }
+    }
+  return launch_cache_[batch] = std::move(L);
+}
+
+// Host-side bounds check of one launch: every element a kernel may touch (including the
+// 16-byte vector over-reads of the channels-last paths) must lie inside one allocation.
+void Model::validate(const Launch & l) const
+{
+  auto check = [&](const void * ptr, long first, long last, int elem, const char * what) {
+    if (!ptr) throw std::runtime_error(std::string("null operand ") + what);
+    if (last < first) return;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr) + first * elem;
+    const uintptr_t hi = reinterpret_cast<uintptr_t>(ptr) + (last + 1) * elem;
+    for (const auto & a : allocs_)
+      if (lo >= a.first && hi <= a.first + a.second) return;
+    throw std::runtime_error(std::string("launch would access outside its buffers: ") + what);
+  };
+  // last element of a view covering B images x C channels x HW pixels
+  auto vlast = [](const View & v, int B, long C, long HW) -> long {
+    if (C <= 0 || HW <= 0 || B <= 0) return -1;
+    return (long)(B - 1) * v.img + (v.layout == kNHWC ? (HW - 1) * v.cs + (C - 1) : (C - 1) * v.cs + (HW - 1));
+  };
+  if (l.kind != Launch::kSmall) {
+    const ConvParams & p = l.cp;
+    const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
+    if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout, HWo), 2, "conv y");
+    if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
+    if (p.bias) check(p.bias, 0, p.Cout - 1, 4, "conv bias");
+    if (l.kind == Launch::kIgemm) {
+      if (p.x.layout != kNHWC) throw std::runtime_error("igemm needs channels-last input");
+      check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
+      const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
+      check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
+      if (p.kpad % kIgemmBK) throw std::runtime_error("kpad not a multiple of the K tile");
+    } else if (l.kind == Launch::kDirect) {
+      check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "direct x");
+      check(p.w, 0, (long)p.Cin * p.K * p.K * (p.Cout / p.G) + 16 - 1, 4, "direct w");
+    } else {
+      check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "dw x");
+      check(p.w, 0, (long)p.K * p.K * p.Cin - 1, 4, "dw w");
+    }
+    return;
+  }
+  const SmallParams & q = l.sp;
+  const int B = q.batch;
+  if (B < 1 || B > 65535) throw std::runtime_error("batch out of grid range");
+  const long HW = (long)q.H * q.W;
+  auto flat = [&](const View & v, long n, const char * what) { check(v.ptr, 0, (long)(B - 1) * v.img + n - 1, 2, what); };
+  switch (l.small) {
+  case kEwSame:
+    check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "ew a");
+    if (q.b.img == 0 && q.b.cs == 0) check(q.b.ptr, 0, 0, 2, "ew scalar b");
+    else check(q.b.ptr, 0, vlast(q.b, B, q.C, HW), 2, "ew b");
+    check(q.y.ptr, 0, vlast(q.y, B, q.C, HW), 2, "ew y");
+    break;
+  case kEwUnary:
+  case kCopy:
+    check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "a");
+    check(q.y.ptr, 0, vlast(q.y, B, q.C, HW), 2, "y");
+    break;
+  case kEwChan:
+    if (q.i0) { flat(q.a, q.C, "chan a"); check(q.b.ptr, 0, vlast(q.b, B, q.C, HW), 2, "chan b"); }
+    else { check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "chan a"); flat(q.b, q.C, "chan b"); }
+    check(q.y.ptr, 0, vlast(q.y, B, q.C, HW), 2, "chan y");
+    break;
+  case kEwBcast: {
+    long amax = 0, bmax = 0;
+    for (int r = 0; r < q.rank; ++r) {
+      amax += (long)(q.dims[r] - 1) * q.dims[q.rank + r];
+      bmax += (long)(q.dims[r] - 1) * q.dims[2 * q.rank + r];
+    }
+    flat(q.a, amax + 1, "bcast a");
+    flat(q.b, bmax + 1, "bcast b");
+    flat(q.y, q.n, "bcast y");
+    break;
+  }
+  case kSliceAxis:
+    flat(q.a, (long)q.i0 * q.i1 * q.i2, "slice x");
+    flat(q.y, (long)q.i0 * q.i4 * q.i2, "slice y");
+    break;
+  case kConcatOuter:
+    flat(q.a, (long)q.i0 * q.i1 * q.i2, "concat x");
+    flat(q.y, (long)q.i0 * q.i3 * q.i2, "concat y");
+    if (q.i4 + q.i1 > q.i3) throw std::runtime_error("concat offset beyond axis");
+    break;
+  case kMaxPool:
+  case kResizeNN:
+    check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "pool x");
+    check(q.y.ptr, 0, vlast(q.y, B, q.C, (long)q.Ho * q.Wo), 2, "pool y");
+    break;
+  case kSoftmax:
+  case kPermute:
+    flat(q.a, (long)q.i0 * q.i1 * q.i2, "x");
+    flat(q.y, (long)q.i0 * q.i1 * q.i2, "y");
+    break;
+  case kGap:
+    check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "gap x");
+    flat(q.y, q.C, "gap y");
+    break;
+  case kBmm:
+    flat(q.a, (long)q.i0 * q.i1 * q.i2, "bmm a");
+    flat(q.b, (long)q.i0 * q.i2 * q.i3, "bmm b");
+    flat(q.y, (long)q.i0 * q.i1 * q.i3, "bmm y");
+    break;
+  case kBiasAdd:
+    flat(q.a, q.n, "bias x");
+    check(q.b.ptr, 0, (q.n - 1) / q.i0, 2, "bias b");
+    flat(q.y, q.n, "bias y");
+    break;
+  default:
+    throw std::runtime_error("unknown small op");
+  }
+}
+
+void Model::dryRun(int batch)
+{
+  check_batch(batch, max_batch_);
+  (void)launches(batch);
+}
+
+void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
+{
+  for (size_t i = b; i < e; ++i) {
+    const Launch & l = L[i];
+    switch (l.kind) {
+    case Launch::kIgemm: launch_conv_igemm(l.cp, stream_); break;
+    case Launch::kDirect: launch_conv_direct(l.cp, stream_); break;
+    case Launch::kDw: launch_dwconv(l.cp, stream_); break;
+    default: launch_small(l.small, l.sp, stream_); break;
+    }
+  }
+  HIPCHECK(hipGetLastError());
+}
+
+// ==================================================================== running
+
+size_t Model::inputNumel() const { return (size_t)prod(input_dims_); }
+const std::vector<int64_t> & Model::outputDims(int i) const { return T_.at(outputs_.at(i))->dims; }
+size_t Model::outputNumel(int i) const { return (size_t)T_.at(outputs_.at(i))->numel; }
+
+
+void Model::setInputF16(const uint16_t * host, int batch)
+{
+  check_batch(batch, max_batch_);
+  HIPCHECK(hipSetDevice(device_));
+  const long n = (long)inputNumel();
+  const long img = roots_[T_[input_name_]->root]->per_image;
+  HIPCHECK(hipMemcpy2DAsync(input_buf_, img * 2, host, n * 2, n * 2, batch, hipMemcpyHostToDevice, stream_));
+  HIPCHECK(hipStreamSynchronize(stream_));
+}
+
+void Model::setInputDeviceF16(const void * dev, int batch)
+{
+  check_batch(batch, max_batch_);
+  HIPCHECK(hipSetDevice(device_));
+  const long n = (long)inputNumel();
+  const long img = roots_[T_[input_name_]->root]->per_image;
+  HIPCHECK(hipMemcpy2DAsync(input_buf_, img * 2, dev, n * 2, n * 2, batch, hipMemcpyDeviceToDevice, stream_));
+}
+
+void Model::setInputF32Trunc(const float * host, int batch)
+{
+  check_batch(batch, max_batch_);
+  HIPCHECK(hipSetDevice(device_));
+  const long n = (long)inputNumel();
+  const long img = roots_[T_[input_name_]->root]->per_image;
+  if (!stage_f32_) stage_f32_ = devAlloc((size_t)n * max_batch_ * 4, false);
+  HIPCHECK(hipMemcpyAsync(stage_f32_, host, (size_t)n * batch * 4, hipMemcpyHostToDevice, stream_));
+  for (int b = 0; b < batch; ++b)
+    launch_f32_to_f16_trunc(static_cast<const float *>(stage_f32_) + (long)b * n,
+                            static_cast<__half *>(input_buf_) + (long)b * img, n, stream_);
+  HIPCHECK(hipGetLastError());
+  HIPCHECK(hipStreamSynchronize(stream_));
+}
+
+void Model::run(int batch)
+{
+  check_batch(batch, max_batch_);
+  if (dry_) { dryRun(batch); return; }
+  HIPCHECK(hipSetDevice(device_));
+  const auto t0 = std::chrono::steady_clock::now();
+  const auto & L = launches(batch);
+  if (flags_ & IVH_FLAG_NO_GRAPH) {
+    enqueue(L, 0, L.size());
+  } else {
+    auto it = graphs_.find(batch);
+    if (it == graphs_.end()) {
+      hipGraph_t g = nullptr;
+      HIPCHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+      try {
+        enqueue(L, 0, L.size());
+      } catch (...) {
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HIPCHECK(hipStreamEndCapture(stream_, &g));
+      hipGraphExec_t ge = nullptr;
+      HIPCHECK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      HIPCHECK(hipGraphDestroy(g));
+      it = graphs_.emplace(batch, ge).first;
+    }
+    HIPCHECK(hipGraphLaunch(it->second, stream_));
+  }
+  if (!(flags_ & IVH_FLAG_ASYNC)) {
+    HIPCHECK(hipStreamSynchronize(stream_));
+    last_run_ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+}
+
+void Model::sync()
+{
+  HIPCHECK(hipSetDevice(device_));
+  HIPCHECK(hipStreamSynchronize(stream_));
+}
+
+void Model::readOutputF16(int i, uint16_t * host, int batch)
+{
+  check_batch(batch, max_batch_);
+  if (i < 0 || i >= outputCount()) throw std::runtime_error("output index out of range");
+  HIPCHECK(hipSetDevice(device_));
+  const Tensor & t = *T_[outputs_[i]];
+  const View v = view(t.name, batch);
+  if (v.layout != kNCHW) throw std::runtime_error("output stored channels-last");
+  HIPCHECK(hipMemcpy2DAsync(host, t.numel * 2, v.ptr, v.img * 2, t.numel * 2, batch, hipMemcpyDeviceToHost, stream_));
+  HIPCHECK(hipStreamSynchronize(stream_));
+}
+
+void Model::readOutputF32(int i, float * host, int batch)
+{
+  const long n = (long)outputNumel(i);
+  std::vector<uint16_t> h((size_t)n * batch);
+  readOutputF16(i, h.data(), batch);
+  for (size_t k = 0; k < h.size(); ++k) host[k] = h2f(h[k]);
+}
+
+size_t Model::tensorNumel(const std::string & name) const
+{
+  auto it = T_.find(name);
+  return it == T_.end() ? 0 : (size_t)it->second->numel;
+}
+
+bool Model::readTensorF16(const std::string & name, uint16_t * host, int batch)
+{
+  auto it = T_.find(name);
+  if (it == T_.end()) return false;
+  check_batch(batch, max_batch_);
+  HIPCHECK(hipSetDevice(device_));
+  HIPCHECK(hipStreamSynchronize(stream_));
+  const Tensor & t = *it->second;
+  const View v = view(name, batch);
+  const long img = std::max<long>(v.img, 0);
+  // pull the whole root span of each image, then gather NCHW on the host
+  const long span = t.kind == Tensor::kInit ? t.numel : roots_[t.root]->per_image;
+  const __half * base = v.ptr;
+  long lo = 0;
+  if (t.kind != Tensor::kInit) {
+    const Root & r = *roots_[t.root];
+    lo = r.layout == kNHWC ? t.coff : t.eoff;
+  }
+  std::vector<uint16_t> buf((size_t)span);
+  const long HW = (long)t.H * t.W;
+  for (int b = 0; b < batch; ++b) {
+    HIPCHECK(hipMemcpy(buf.data(), base - lo + (long)b * img, span * 2, hipMemcpyDeviceToHost));
+    uint16_t * dst = host + (long)b * t.numel;
+    if (v.layout == kNHWC) {
+      for (int c = 0; c < t.C; ++c)
+        for (long p = 0; p < HW; ++p) dst[c * HW + p] = buf[(size_t)(lo + p * v.cs + c)];
+    } else {
+      std::memcpy(dst, buf.data() + lo, (size_t)t.numel * 2);
+    }
+  }
+  return true;
+}
+
+std::vector<double> Model::profileNodes(int batch, int iters)
+{
+  check_batch(batch, max_batch_);
+  HIPCHECK(hipSetDevice(device_));
+  const auto & L = launches(batch);
+  std::vector<double> ms(nodes_.size(), 0.0);
+  std::vector<hipEvent_t> ev(nodes_.size() + 1);
+  for (auto & e : ev) HIPCHECK(hipEventCreate(&e));
+  for (int it = 0; it < iters; ++it) {
+    HIPCHECK(hipEventRecord(ev[0], stream_));
+    for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+      enqueue(L, node_launch_begin_[ni], node_launch_end_[ni]);
+      HIPCHECK(hipEventRecord(ev[ni + 1], stream_));
+    }
+    HIPCHECK(hipStreamSynchronize(stream_));
+    for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+      float t = 0;
+      HIPCHECK(hipEventElapsedTime(&t, ev[ni], ev[ni + 1]));
+      ms[ni] += t;
+    }
+  }
+  for (auto & e : ev) (void)hipEventDestroy(e);
+  for (auto & m : ms) m /= std::max(iters, 1);
+  return ms;
+}
+
+// ================================================================= statistics
+// Algorithmic FLOPs / compulsory fp16 bytes per image, for roofline reports.
+void Model::buildStats()
+{
+  stats_.assign(nodes_.size(), NodeStat{});
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    const PlanNode & n = nodes_[ni];
+    NodeStat & s = stats_[ni];
+    s.op = n.op;
+    const Tensor & y = *T_[n.outs[0]];
+    double in_b = 0;
+    for (size_t k = 0; k < n.ins.size(); ++k) {
+      if (n.ins[k] == "-") continue;
+      const Tensor & t = *T_[n.ins[k]];
+      if (t.kind == Tensor::kInit) continue;
+      in_b += 2.0 * t.numel;
+    }
+    s.bytes = skip_[ni] ? 0 : in_b + 2.0 * y.numel;
+    char buf[256];
+    if (n.op == "conv1x1" || n.op == "conv3x3" || n.op == "conv_general") {
+      const bool is1 = n.op == "conv1x1";
+      const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
+      const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
+      s.flops = 2.0 * wt.numel * (double)y.numel / std::max<int64_t>(wt.dims[0], 1);
+      const int kind = packed_[ni].kind;
+      s.kernel = kind == 0 ? "conv_igemm" : (kind == 1 ? "conv_direct" : "dwconv");
+      std::snprintf(buf, sizeof(buf), "%s %dx%dx%d->%dx%dx%d k%d s%d g%d act%d%s", n.op.c_str(), xt.C, xt.H, xt.W,
+                    y.C, y.H, y.W, is1 ? 1 : (n.op == "conv3x3" ? 3 : n.i("K", 3)),
+                    is1 ? 1 : (n.op == "conv3x3" ? n.i("stride", 1) : n.i("S", 1)), n.i("G", 1), n.i("act"),
+                    (n.ins.size() > 3 && n.ins[3] != "-") ? " +res" : "");
+      s.desc = buf;
+    } else {
+      s.kernel = skip_[ni] ? "(view)" : n.op;
+      if (n.op == "bmm" || n.op == "gemm") {
+        const Tensor & at = *T_[n.ins[0]];
+        const Tensor & bt = *T_[n.ins[1]];
+        s.flops = 2.0 * at.numel * (double)bt.dims.back();
+      }
+      std::snprintf(buf, sizeof(buf), "%s -> %s [%ld]", n.op.c_str(), y.name.c_str(), (long)y.numel);
+      s.desc = buf;
+    }
+  }
+}
+
+}  // namespace ivh

@@ -1,0 +1,133 @@
+// HIP-native plan executor: the MI355X counterpart of infvino::PlanModel
+// (include/infvino/PlanModel.hpp:57-234, src/PlanModel.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "ivh_internal.hpp"
+
+namespace ivh {
+
+struct PlanNode {
+  std::string op;
+  std::vector<std::string> ins, outs;
+  std::map<std::string, std::string> attr;
+  int i(const char * key, int def = 0) const;
+  bool has(const char * key) const { return attr.count(key) != 0; }
+  std::string str(const char * key) const;
+};
+
+// One kernel launch with everything resolved for a given batch size.
+struct Launch {
+  enum Kind { kIgemm, kDirect, kDw, kSmall } kind = kSmall;
+  int small = 0;
+  ConvParams cp;
+  SmallParams sp;
+};
+
+struct NodeStat {
+  std::string op, kernel, desc;
+  double flops = 0, bytes = 0;  // algorithmic, per image
+};
+
+class Model {
+ public:
+  Model(const std::string & plan_path, int device, int max_batch, uint32_t flags);
+  ~Model();
+  Model(const Model &) = delete;
+  Model & operator=(const Model &) = delete;
+
+  const std::vector<int64_t> & inputDims() const { return input_dims_; }
+  size_t inputNumel() const;
+  int outputCount() const { return (int)outputs_.size(); }
+  const std::vector<int64_t> & outputDims(int i) const;
+  size_t outputNumel(int i) const;
+  int maxBatch() const { return max_batch_; }
+  int device() const { return device_; }
+  hipStream_t stream() const { return stream_; }
+
+  void setInputF16(const uint16_t * host, int batch);
+  void setInputF32Trunc(const float * host, int batch);
+  void setInputDeviceF16(const void * dev, int batch);
+  void run(int batch);
+  void sync();
+  void readOutputF16(int i, uint16_t * host, int batch);
+  void readOutputF32(int i, float * host, int batch);
+  bool readTensorF16(const std::string & name, uint16_t * host, int batch);
+  size_t tensorNumel(const std::string & name) const;
+  double lastRunMs() const { return last_run_ms_; }
+  // Builds and bounds-checks the launches for `batch` without touching a device.
+  void dryRun(int batch);
+  bool isDry() const { return dry_; }
+
+  // Per-node device time (ms, averaged over iters) measured with HIP events on the
+  // model's stream around each node's launches.
+  std::vector<double> profileNodes(int batch, int iters);
+  int nodeCount() const { return (int)nodes_.size(); }
+  const NodeStat & nodeStat(int i) const { return stats_.at(i); }
+  size_t arenaBytes(int batch) const { return (size_t)arena_elems1_ * batch * 2; }
+  size_t weightBytes() const { return weight_bytes_; }
+
+ private:
+  struct Tensor;
+  struct Root;
+  void parse(const std::string & path);
+  void fuseResidual();
+  void fuseActivation();
+  void plan();
+  int chanBroadcast(const PlanNode & n) const;
+  void assignViews();
+  void chooseLayouts();
+  void allocate();
+  void uploadWeights();
+  void buildStats();
+  const std::vector<Launch> & launches(int batch);
+  View view(const std::string & name, int batch) const;
+  void enqueue(const std::vector<Launch> & L, size_t b, size_t e);
+  void emitNode(size_t ni, int batch, std::vector<Launch> & out);
+  void validate(const Launch & l) const;
+  void * devAlloc(size_t bytes, bool zero);
+  void devUpload(void * d, const void * src, size_t bytes);
+
+  std::string plan_path_, plan_dir_;
+  int device_ = 0, max_batch_ = 1;
+  uint32_t flags_ = 0;
+  hipStream_t stream_ = nullptr;
+
+  std::vector<PlanNode> nodes_;
+  std::vector<char> skip_;                  // node needs no launch (pure alias)
+  std::map<std::string, std::unique_ptr<Tensor>> T_;
+  std::vector<std::unique_ptr<Root>> roots_;
+  std::string input_name_;
+  std::vector<int64_t> input_dims_;
+  std::vector<std::string> outputs_;
+
+  // device memory
+  void * arena_ = nullptr;                  // activations, max_batch images
+  long arena_elems1_ = 0;                   // elements per image-unit
+  void * input_buf_ = nullptr;              // graph input, max_batch images (fp16)
+  void * stage_f32_ = nullptr;              // f32 staging for the truncating conversion
+  std::vector<void *> dev_allocs_;          // weights etc.
+  size_t weight_bytes_ = 0;
+  std::map<std::string, void *> init_dev_;  // raw fp16 inits
+  struct Packed { void * w = nullptr; float * bias = nullptr; int kind = 0; int kpad = 0, cin8 = 0; };
+  std::vector<Packed> packed_;              // per node
+
+  std::map<int, std::vector<Launch>> launch_cache_;
+  std::vector<size_t> node_launch_begin_;   // per node: [begin, end) into launches(batch)
+  std::vector<size_t> node_launch_end_;
+  std::map<int, hipGraphExec_t> graphs_;
+  std::vector<NodeStat> stats_;
+  double last_run_ms_ = 0.0;
+  bool dry_ = false;
+  uintptr_t fake_next_ = (uintptr_t)1 << 44;
+  std::vector<std::pair<uintptr_t, size_t>> allocs_;
+};
+
+}  // namespace ivh

@@ -1,0 +1,62 @@
+// Internal types shared by the host executor and the gfx950 kernels.
+//
+// Activation storage model (one GPU, batch B as the outer axis):
+//   Every activation tensor of the plan describes ONE image (src/PlanModel.cpp:3561-3564
+//   read C,H,W from the last three dims and ignore dim 0).  On the device a tensor is a
+//   *view* into a root buffer that holds B images back to back:
+//     element (b, c, p)  with p = h*W + w  lives at
+//        base + b*img + (layout == NHWC ? p*cs + c : c*cs + p)
+//   NHWC (channels-last) is the layout the MFMA implicit-GEMM convs read and write: the
+//   GEMM K axis (input channels) is contiguous, so operand fragments are 16-byte loads.
+//   A channel range of a root (concat write-offset, split) is the same root with base
+//   moved by the channel offset; nothing is copied.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+
+namespace ivh {
+
+enum Layout : int { kNCHW = 0, kNHWC = 1 };
+
+// Canonical activation codes (include/infvino/KernelFamily.hpp:70-73).
+enum Act : int { kActNone = 0, kActSiLU = 1, kActReLU = 2, kActHSwish = 3, kActHSigmoid = 4, kActSigmoid = 5 };
+
+struct View {
+  __half * ptr = nullptr;  // image 0, channel 0 of this view
+  long img = 0;            // elements between consecutive images (0 = shared by all images)
+  int layout = kNCHW;
+  int cs = 0;              // NCHW: elements between channels; NHWC: elements between pixels
+};
+
+// One convolution launch.  Output pixels of all images form the GEMM M axis.
+struct ConvParams {
+  View x, y, r;              // input, output, residual (r.ptr == nullptr: none)
+  const __half * w = nullptr;  // packed weights (layout depends on the kernel family)
+  const float * bias = nullptr;
+  int batch = 1;
+  int Cin = 0, H = 0, W = 0;
+  int Cout = 0, Ho = 0, Wo = 0;
+  int K = 1, S = 1, P = 0, G = 1;  // square kernel, stride, pad, groups
+  int act = 0;
+  int cin8 = 0;   // input channels rounded up to 8 (im2col K chunking)
+  int kpad = 0;   // packed K per output channel, multiple of the K tile
+};
+
+// Generic small-op descriptor (elementwise / pooling / data movement).
+struct SmallParams {
+  View a, b, y;
+  int batch = 1;
+  int C = 0, H = 0, W = 0;     // per-image geometry of the iteration space
+  int Ho = 0, Wo = 0;
+  int K = 0, S = 1, P = 0;
+  int op = 0;
+  long n = 0;                  // per-image element count (flat ops)
+  int i0 = 0, i1 = 0, i2 = 0, i3 = 0, i4 = 0;  // op-specific integers
+  int rank = 0;
+  int dims[18] = {0};          // ew_binary broadcast spec (rank <= 6)
+};
+
+}  // namespace ivh

@@ -1,0 +1,42 @@
+// Host-side launchers of the gfx950 kernels.  Each takes fully resolved device views
+// (batch-B pointers) and a stream; all shape checks happen in the executor before launch.
+#pragma once
+
+#include "ivh_internal.hpp"
+
+namespace ivh {
+
+// conv_mfma.hip
+int igemm_bn(int cout);                    // N tile of the implicit GEMM for a Cout
+constexpr int kIgemmBK = 32;               // K tile (packed weight rows are a multiple)
+constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
+void launch_conv_igemm(const ConvParams & p, hipStream_t s);
+
+// kernels_misc.hip
+void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout
+void launch_dwconv(const ConvParams & p, hipStream_t s);        // depthwise, any layout
+bool dwconv_vectorizable(const ConvParams & p);
+
+enum SmallOp : int {
+  kEwSame = 0,     // y = op(a, b), same geometry; b.img == 0 && b.cs == 0 -> scalar
+  kEwBcast,        // NCHW flat broadcast, dims = bdims spec
+  kEwChan,         // per-channel broadcast: i0 = 1 if a is the [C] operand
+  kEwUnary,        // y = act(a), op = canonical activation code
+  kCopy,           // y(c,p) = a(c,p) (any layouts): split / concat parts / layout change
+  kSliceAxis,      // NCHW flat: i0 outer, i1 axdim, i2 inner, i3 start, i4 len
+  kConcatOuter,    // NCHW flat 4-source concat along an inner axis (see executor)
+  kMaxPool,
+  kResizeNN,
+  kSoftmax,        // NCHW flat: i0 outer, i1 axdim, i2 inner
+  kPermute,        // NCHW flat: i0 D1, i1 D2, i2 I, op = mode
+  kGap,            // a view [C,H,W] -> y flat [C]
+  kBmm,            // NCHW flat: i0 BB, i1 M, i2 K, i3 N  (a: [BB][M][K], b: [BB][K][N])
+  kBiasAdd,        // NCHW flat: i0 HW
+};
+void launch_small(int kind, const SmallParams & p, hipStream_t s);
+
+// boundary conversions (include/infvino/Half.hpp semantics for the truncating one)
+void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t s);
+void launch_f16_to_f32(const __half * in, float * out, long n, hipStream_t s);
+
+}  // namespace ivh

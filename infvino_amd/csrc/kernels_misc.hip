@@ -1,0 +1,530 @@
+// Bandwidth-bound gfx950 kernels: direct conv (stem Cin<8, grouped, NCHW-input convs),
+// depthwise conv, the small ops of kernels/ops.cl, and the boundary conversions.
+// None of these use MFMA; they are written for coalesced HBM access with batch B as an
+// outer grid axis.  Element addressing goes through ivh::View (NCHW or NHWC, strided).
+#include "ivh_internal.hpp"
+#include "kernels.hpp"
+
+namespace ivh {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float actf(float v, int act)
+{
+  switch (act) {
+  case kActSiLU: return v / (1.0f + __expf(-v));
+  case kActReLU: return fmaxf(v, 0.0f);
+  case kActHSwish: return v * fminf(fmaxf(v + 3.0f, 0.0f), 6.0f) / 6.0f;
+  case kActHSigmoid: return fminf(fmaxf(v + 3.0f, 0.0f), 6.0f) / 6.0f;
+  case kActSigmoid: return 1.0f / (1.0f + __expf(-v));
+  default: return v;
+  }
+}
+
+__device__ __forceinline__ long vidx(const View & v, int b, int c, long p)
+{
+  return (long)b * v.img + (v.layout == kNHWC ? p * v.cs + c : (long)c * v.cs + p);
+}
+__device__ __forceinline__ float vld(const View & v, int b, int c, long p)
+{
+  return (float)reinterpret_cast<const _Float16 *>(v.ptr)[vidx(v, b, c, p)];
+}
+__device__ __forceinline__ void vst(const View & v, int b, int c, long p, float x)
+{
+  reinterpret_cast<_Float16 *>(v.ptr)[vidx(v, b, c, p)] = (_Float16)x;
+}
+
+static inline unsigned nblk(long n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// ------------------------------------------------------------------ direct conv
+// Restates conv_general (kernels/conv_general.cl:7-48) / conv3x3_cin3 (conv_cin3.cl:67-118):
+// one lane = one output pixel x COB output channels of one group, fp32 accumulation.
+// Weights packed fp32 [G][cin_g][K][K][cout_g] so every lane of a wave reads the same
+// weight addresses (uniform, scalar-cache friendly).
+template <int COB>
+__global__ void __launch_bounds__(256) conv_direct_kernel(const ConvParams p)
+{
+  const int HWo = p.Ho * p.Wo;
+  const long Mt = (long)p.batch * HWo;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cout_g = p.Cout / p.G, cin_g = p.Cin / p.G;
+  const int ncb = (cout_g + COB - 1) / COB;
+  if (idx >= Mt * ncb * p.G) return;
+  const long pix = idx % Mt;
+  const int cbg = (int)(idx / Mt);
+  const int g = cbg / ncb, cb = cbg % ncb;
+  const int b = (int)(pix / HWo), hw = (int)(pix % HWo);
+  const int oy = hw / p.Wo, ox = hw % p.Wo;
+  const int col = cb * COB;  // first channel within the group
+  const float * W = reinterpret_cast<const float *>(p.w);
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = 0.0f;
+  for (int cl = 0; cl < cin_g; ++cl) {
+    const int c = g * cin_g + cl;
+    for (int ky = 0; ky < p.K; ++ky) {
+      const int iy = oy * p.S - p.P + ky;
+      if ((unsigned)iy >= (unsigned)p.H) continue;
+      for (int kx = 0; kx < p.K; ++kx) {
+        const int ix = ox * p.S - p.P + kx;
+        if ((unsigned)ix >= (unsigned)p.W) continue;
+        const float xv = vld(p.x, b, c, (long)iy * p.W + ix);
+        const float * wp = W + (((long)(g * cin_g + cl) * p.K + ky) * p.K + kx) * cout_g + col;
+#pragma unroll
+        for (int j = 0; j < COB; ++j) acc[j] += xv * wp[j];
+      }
+    }
+  }
+  float out[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) {
+    const int co = g * cout_g + col + j;
+    float v = acc[j] + ((p.bias && col + j < cout_g) ? p.bias[co] : 0.0f);
+    v = actf(v, p.act);
+    if (p.r.ptr && col + j < cout_g) v += vld(p.r, b, co, hw);
+    out[j] = v;
+  }
+  const int co0 = g * cout_g + col;
+  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr);
+  if (COB % 8 == 0 && p.y.layout == kNHWC && col + COB <= cout_g &&
+      (((p.y.cs | (int)p.y.img | co0 | (int)(reinterpret_cast<uintptr_t>(yb) >> 1)) & 7) == 0)) {
+#pragma unroll
+    for (int j = 0; j < COB; j += 8) {
+      h8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (_Float16)out[j + e];
+      *reinterpret_cast<h8 *>(yb + (long)b * p.y.img + (long)hw * p.y.cs + co0 + j) = v;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < COB; ++j)
+      if (col + j < cout_g) vst(p.y, b, co0 + j, hw, out[j]);
+  }
+}
+
+void launch_conv_direct(const ConvParams & p, hipStream_t s)
+{
+  const int cout_g = p.Cout / p.G;
+  const long Mt = (long)p.batch * p.Ho * p.Wo;
+  if (cout_g % 16 == 0 || (p.G == 1 && cout_g > 8)) {
+    const long n = Mt * ((cout_g + 15) / 16) * p.G;
+    hipLaunchKernelGGL(conv_direct_kernel<16>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+  } else if (cout_g % 8 == 0 || p.G == 1) {
+    const long n = Mt * ((cout_g + 7) / 8) * p.G;
+    hipLaunchKernelGGL(conv_direct_kernel<8>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+  } else {
+    const long n = Mt * cout_g * p.G;
+    hipLaunchKernelGGL(conv_direct_kernel<1>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+  }
+}
+
+// ------------------------------------------------------------------- depthwise
+// Restates depthwise_f16 / depthwise_v / depthwise_blk (kernels/conv_general.cl:85-187,
+// depthwise_blk.cl:118-228): y[c] = act(sum_k x[c]*w[c] + b[c]), K in {3,5}, S in {1,2}.
+// NHWC vector path: one lane = one output pixel x 8 channels, 16-byte loads/stores,
+// fp32 accumulation.  Weights packed fp32 [K][K][C].
+template <int K>
+__global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p)
+{
+  const int C8 = p.Cin >> 3;
+  const int HWo = p.Ho * p.Wo;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)p.batch * HWo * C8) return;
+  const int c8 = (int)(idx % C8);
+  const long pix = idx / C8;
+  const int b = (int)(pix / HWo), hw = (int)(pix % HWo);
+  const int oy = hw / p.Wo, ox = hw % p.Wo;
+  const int c = c8 * 8;
+  const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img + c;
+  const float * W = reinterpret_cast<const float *>(p.w) + c;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int ky = 0; ky < K; ++ky) {
+    const int iy = oy * p.S - p.P + ky;
+    if ((unsigned)iy >= (unsigned)p.H) continue;
+#pragma unroll
+    for (int kx = 0; kx < K; ++kx) {
+      const int ix = ox * p.S - p.P + kx;
+      if ((unsigned)ix >= (unsigned)p.W) continue;
+      const h8 xv = *reinterpret_cast<const h8 *>(xb + ((long)iy * p.W + ix) * p.x.cs);
+      const float4 w0 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin);
+      const float4 w1 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin + 4);
+      acc[0] += (float)xv[0] * w0.x; acc[1] += (float)xv[1] * w0.y;
+      acc[2] += (float)xv[2] * w0.z; acc[3] += (float)xv[3] * w0.w;
+      acc[4] += (float)xv[4] * w1.x; acc[5] += (float)xv[5] * w1.y;
+      acc[6] += (float)xv[6] * w1.z; acc[7] += (float)xv[7] * w1.w;
+    }
+  }
+  h8 out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = acc[e] + (p.bias ? p.bias[c + e] : 0.0f);
+    v = actf(v, p.act);
+    if (p.r.ptr) v += vld(p.r, b, c + e, hw);
+    out[e] = (_Float16)v;
+  }
+  *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + (long)hw * p.y.cs + c) = out;
+}
+
+// Any-layout depthwise: one lane = one output element.
+__global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p)
+{
+  const int HWo = p.Ho * p.Wo;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)p.batch * HWo * p.Cin) return;
+  const int hw = (int)(idx % HWo);
+  const long t = idx / HWo;
+  const int c = (int)(t % p.Cin), b = (int)(t / p.Cin);
+  const int oy = hw / p.Wo, ox = hw % p.Wo;
+  const float * W = reinterpret_cast<const float *>(p.w);
+  float acc = 0.0f;
+  for (int ky = 0; ky < p.K; ++ky) {
+    const int iy = oy * p.S - p.P + ky;
+    if ((unsigned)iy >= (unsigned)p.H) continue;
+    for (int kx = 0; kx < p.K; ++kx) {
+      const int ix = ox * p.S - p.P + kx;
+      if ((unsigned)ix >= (unsigned)p.W) continue;
+      acc += vld(p.x, b, c, (long)iy * p.W + ix) * W[(ky * p.K + kx) * p.Cin + c];
+    }
+  }
+  float v = actf(acc + (p.bias ? p.bias[c] : 0.0f), p.act);
+  if (p.r.ptr) v += vld(p.r, b, c, hw);
+  vst(p.y, b, c, hw, v);
+}
+
+bool dwconv_vectorizable(const ConvParams & p)
+{
+  auto al = [](const View & v) {
+    return v.layout == kNHWC && ((v.cs | (int)v.img | (int)(reinterpret_cast<uintptr_t>(v.ptr) >> 1)) & 7) == 0;
+  };
+  return (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) && al(p.x) && al(p.y) &&
+         (!p.r.ptr || p.r.layout == kNHWC);
+}
+
+void launch_dwconv(const ConvParams & p, hipStream_t s)
+{
+  const long M = (long)p.batch * p.Ho * p.Wo;
+  if (dwconv_vectorizable(p)) {
+    const long n = M * (p.Cin / 8);
+    if (p.K == 3) hipLaunchKernelGGL(dw_nhwc_kernel<3>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(dw_nhwc_kernel<5>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL(dw_generic_kernel, dim3(nblk(M * p.Cin, 256)), dim3(256), 0, s, p);
+  }
+}
+
+// ------------------------------------------------------------------ small ops
+// Semantics of kernels/ops.cl (fp32 compute, fp16 store), batch on grid axis y.
+
+__device__ __forceinline__ float binop(float a, float b, int op)
+{
+  switch (op) {
+  case 0: return a + b;
+  case 1: return a - b;
+  case 2: return a * b;
+  default: return a / b;
+  }
+}
+
+// iteration index -> (c, p) in the output's physical order (coalesced stores)
+__device__ __forceinline__ void cp_of(const SmallParams & q, long i, int & c, long & p)
+{
+  const long HW = (long)q.H * q.W;
+  if (q.y.layout == kNHWC) { p = i / q.C; c = (int)(i - p * q.C); }
+  else { c = (int)(i / HW); p = i - (long)c * HW; }
+}
+
+__global__ void ew_same_kernel(const SmallParams q)  // ew_binary / ew_binary_v (ops.cl:34-48,373-391)
+{
+  const long n = (long)q.C * q.H * q.W;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  cp_of(q, i, c, p);
+  const float av = vld(q.a, b, c, p);
+  const float bv = (q.b.img == 0 && q.b.cs == 0) ? (float)reinterpret_cast<const _Float16 *>(q.b.ptr)[0]
+                                                 : vld(q.b, b, c, p);
+  vst(q.y, b, c, p, binop(av, bv, q.op));
+}
+
+__global__ void ew_unary_kernel(const SmallParams q)  // ew_unary (ops.cl:50-63), canonical code in op
+{
+  const long n = (long)q.C * q.H * q.W;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  cp_of(q, i, c, p);
+  vst(q.y, b, c, p, actf(vld(q.a, b, c, p), q.op));
+}
+
+__global__ void copy_kernel(const SmallParams q)  // copy_c / concat part / layout change
+{
+  const long n = (long)q.C * q.H * q.W;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  cp_of(q, i, c, p);
+  const long si = vidx(q.a, b, c, p), di = vidx(q.y, b, c, p);
+  reinterpret_cast<_Float16 *>(q.y.ptr)[di] = reinterpret_cast<const _Float16 *>(q.a.ptr)[si];
+}
+
+// ew_binary_ch (ops.cl:311-341): one operand is per-channel [C]; i0 = 1 if that is `a`.
+__global__ void ew_chan_kernel(const SmallParams q)
+{
+  const long n = (long)q.C * q.H * q.W;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  cp_of(q, i, c, p);
+  const _Float16 * ap = reinterpret_cast<const _Float16 *>(q.a.ptr);
+  const _Float16 * bp = reinterpret_cast<const _Float16 *>(q.b.ptr);
+  float av, bv;
+  if (q.i0) { av = (float)ap[(long)b * q.a.img + c]; bv = vld(q.b, b, c, p); }
+  else { av = vld(q.a, b, c, p); bv = (float)bp[(long)b * q.b.img + c]; }
+  vst(q.y, b, c, p, binop(av, bv, q.op));
+}
+
+// ew_binary_bcast (ops.cl:10-32): flat NCHW, dims = [out, a_strides, b_strides].
+__global__ void ew_bcast_kernel(const SmallParams q)
+{
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= q.n) return;
+  long rem = i, ai = 0, bi = 0;
+  for (int r = q.rank - 1; r >= 0; --r) {
+    const long od = q.dims[r];
+    const long coord = rem % od;
+    rem /= od;
+    ai += coord * q.dims[q.rank + r];
+    bi += coord * q.dims[2 * q.rank + r];
+  }
+  const float av = (float)reinterpret_cast<const _Float16 *>(q.a.ptr)[(long)b * q.a.img + ai];
+  const float bv = (float)reinterpret_cast<const _Float16 *>(q.b.ptr)[(long)b * q.b.img + bi];
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = (_Float16)binop(av, bv, q.op);
+}
+
+__global__ void slice_axis_kernel(const SmallParams q)  // ops.cl:74-91
+{
+  const long total = (long)q.i0 * q.i4 * q.i2;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  const long li = (long)q.i4 * q.i2;
+  const long o = i / li, rem = i - o * li;
+  const _Float16 * x = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img;
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = x[(o * q.i1 + q.i3) * q.i2 + rem];
+}
+
+// One source of concat4 (ops.cl:93-119) with outer > 1:
+// y[o][off + ax][r] = x[o][ax][r], i0 outer, i1 src axis len, i2 inner, i3 dst axis len, i4 off.
+__global__ void concat_outer_kernel(const SmallParams q)
+{
+  const long total = (long)q.i0 * q.i1 * q.i2;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  const long r = i % q.i2, t = i / q.i2;
+  const long ax = t % q.i1, o = t / q.i1;
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + (o * q.i3 + q.i4 + ax) * q.i2 + r] =
+    reinterpret_cast<const _Float16 *>(q.a.ptr)[(long)b * q.a.img + i];
+}
+
+__global__ void maxpool_kernel(const SmallParams q)  // ops.cl:148-166, OOB taps ignored
+{
+  const long n = (long)q.C * q.Ho * q.Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  SmallParams o = q;
+  o.H = q.Ho; o.W = q.Wo;
+  cp_of(o, i, c, p);
+  const int oh = (int)(p / q.Wo), ow = (int)(p % q.Wo);
+  float m = -3.4e38f;
+  for (int kh = 0; kh < q.K; ++kh) {
+    const int yy = oh * q.S - q.P + kh;
+    if ((unsigned)yy >= (unsigned)q.H) continue;
+    for (int kw = 0; kw < q.K; ++kw) {
+      const int xx = ow * q.S - q.P + kw;
+      if ((unsigned)xx >= (unsigned)q.W) continue;
+      m = fmaxf(m, vld(q.a, b, c, (long)yy * q.W + xx));
+    }
+  }
+  vst(q.y, b, c, p, m);
+}
+
+__global__ void resize_nn_kernel(const SmallParams q)  // ops.cl:168-179, i0 = scale
+{
+  const long n = (long)q.C * q.Ho * q.Wo;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= n) return;
+  int c; long p;
+  SmallParams o = q;
+  o.H = q.Ho; o.W = q.Wo;
+  cp_of(o, i, c, p);
+  const int oh = (int)(p / q.Wo), ow = (int)(p % q.Wo);
+  const long si = vidx(q.a, b, c, (long)(oh / q.i0) * q.W + ow / q.i0);
+  reinterpret_cast<_Float16 *>(q.y.ptr)[vidx(q.y, b, c, p)] = reinterpret_cast<const _Float16 *>(q.a.ptr)[si];
+}
+
+__global__ void softmax_kernel(const SmallParams q)  // ops.cl:181-197
+{
+  const long total = (long)q.i0 * q.i2;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  const long o = i / q.i2, r = i - o * q.i2;
+  const _Float16 * x = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img + o * q.i1 * q.i2 + r;
+  _Float16 * y = reinterpret_cast<_Float16 *>(q.y.ptr) + (long)b * q.y.img + o * q.i1 * q.i2 + r;
+  float m = -3.4e38f;
+  for (int a = 0; a < q.i1; ++a) m = fmaxf(m, (float)x[(long)a * q.i2]);
+  float s = 0.0f;
+  for (int a = 0; a < q.i1; ++a) s += __expf((float)x[(long)a * q.i2] - m);
+  const float inv = 1.0f / s;
+  for (int a = 0; a < q.i1; ++a) y[(long)a * q.i2] = (_Float16)(__expf((float)x[(long)a * q.i2] - m) * inv);
+}
+
+__global__ void permute_kernel(const SmallParams q)  // ops.cl:199-222
+{
+  const long total = (long)q.i0 * q.i1 * q.i2;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  // i enumerates the OUTPUT (coalesced stores)
+  long src;
+  if (q.op == 0) {  // out [D2][D1][I]
+    const long r = i % q.i2, t = i / q.i2;
+    const long d1 = t % q.i0, d2 = t / q.i0;
+    src = (d1 * q.i1 + d2) * q.i2 + r;
+  } else {          // out [D1][I][D2]
+    const long d2 = i % q.i1, t = i / q.i1;
+    const long r = t % q.i2, d1 = t / q.i2;
+    src = (d1 * q.i1 + d2) * q.i2 + r;
+  }
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] =
+    reinterpret_cast<const _Float16 *>(q.a.ptr)[(long)b * q.a.img + src];
+}
+
+// gap / gap_r (ops.cl:224-266): one 64-lane wave per (image, channel), fp32 tree reduction.
+__global__ void __launch_bounds__(256) gap_kernel(const SmallParams q)
+{
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + wave;
+  const int b = blockIdx.y;
+  if (c >= q.C) return;
+  const long HW = (long)q.H * q.W;
+  float s = 0.0f;
+  for (long p = lane; p < HW; p += 64) s += vld(q.a, b, c, p);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0)
+    reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + c] = (_Float16)(s / (float)HW);
+}
+
+// bmm (ops.cl:276-294): fp32 accumulation, one lane per output.
+__global__ void bmm_kernel(const SmallParams q)
+{
+  const long total = (long)q.i0 * q.i1 * q.i3;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  const long n = i % q.i3, t = i / q.i3;
+  const long m = t % q.i1, bb = t / q.i1;
+  const _Float16 * A = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img + (bb * q.i1 + m) * q.i2;
+  const _Float16 * B = reinterpret_cast<const _Float16 *>(q.b.ptr) + (long)b * q.b.img + bb * q.i2 * q.i3 + n;
+  float acc = 0.0f;
+  for (int k = 0; k < q.i2; ++k) acc += (float)A[k] * (float)B[(long)k * q.i3];
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = (_Float16)acc;
+}
+
+__global__ void bias_add_kernel(const SmallParams q)  // ops.cl:268-274
+{
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= q.n) return;
+  const float x = (float)reinterpret_cast<const _Float16 *>(q.a.ptr)[(long)b * q.a.img + i];
+  const float bb = (float)reinterpret_cast<const _Float16 *>(q.b.ptr)[i / q.i0];
+  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = (_Float16)(x + bb);
+}
+
+void launch_small(int kind, const SmallParams & q, hipStream_t s)
+{
+  const dim3 blk(256);
+  const unsigned B = (unsigned)q.batch;
+  const long nchw = (long)q.C * q.H * q.W;
+  switch (kind) {
+  case kEwSame: hipLaunchKernelGGL(ew_same_kernel, dim3(nblk(nchw, 256), B), blk, 0, s, q); break;
+  case kEwUnary: hipLaunchKernelGGL(ew_unary_kernel, dim3(nblk(nchw, 256), B), blk, 0, s, q); break;
+  case kCopy: hipLaunchKernelGGL(copy_kernel, dim3(nblk(nchw, 256), B), blk, 0, s, q); break;
+  case kEwChan: hipLaunchKernelGGL(ew_chan_kernel, dim3(nblk(nchw, 256), B), blk, 0, s, q); break;
+  case kEwBcast: hipLaunchKernelGGL(ew_bcast_kernel, dim3(nblk(q.n, 256), B), blk, 0, s, q); break;
+  case kSliceAxis:
+    hipLaunchKernelGGL(slice_axis_kernel, dim3(nblk((long)q.i0 * q.i4 * q.i2, 256), B), blk, 0, s, q);
+    break;
+  case kConcatOuter:
+    hipLaunchKernelGGL(concat_outer_kernel, dim3(nblk((long)q.i0 * q.i1 * q.i2, 256), B), blk, 0, s, q);
+    break;
+  case kMaxPool:
+    hipLaunchKernelGGL(maxpool_kernel, dim3(nblk((long)q.C * q.Ho * q.Wo, 256), B), blk, 0, s, q);
+    break;
+  case kResizeNN:
+    hipLaunchKernelGGL(resize_nn_kernel, dim3(nblk((long)q.C * q.Ho * q.Wo, 256), B), blk, 0, s, q);
+    break;
+  case kSoftmax:
+    hipLaunchKernelGGL(softmax_kernel, dim3(nblk((long)q.i0 * q.i2, 256), B), blk, 0, s, q);
+    break;
+  case kPermute:
+    hipLaunchKernelGGL(permute_kernel, dim3(nblk((long)q.i0 * q.i1 * q.i2, 256), B), blk, 0, s, q);
+    break;
+  case kGap: hipLaunchKernelGGL(gap_kernel, dim3((unsigned)((q.C + 3) / 4), B), blk, 0, s, q); break;
+  case kBmm:
+    hipLaunchKernelGGL(bmm_kernel, dim3(nblk((long)q.i0 * q.i1 * q.i3, 256), B), blk, 0, s, q);
+    break;
+  case kBiasAdd: hipLaunchKernelGGL(bias_add_kernel, dim3(nblk(q.n, 256), B), blk, 0, s, q); break;
+  default: break;
+  }
+}
+
+// ------------------------------------------------------------- boundary conversions
+// f32 -> f16 exactly as include/infvino/Half.hpp:14-24: truncate the mantissa, flush
+// results with exponent <= 0 to signed zero, saturate exponent >= 31 (NaN too) to inf.
+__global__ void f32_to_f16_trunc_kernel(const float * in, uint16_t * out, long n)
+{
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t x = __float_as_uint(in[i]);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const int exp = (int)((x >> 23) & 0xffu) - 112;
+  uint32_t h;
+  if (exp <= 0) h = sign;
+  else if (exp >= 31) h = sign | 0x7c00u;
+  else h = sign | ((uint32_t)exp << 10) | ((x & 0x7fffffu) >> 13);
+  out[i] = (uint16_t)h;
+}
+
+__global__ void f16_to_f32_kernel(const __half * in, float * out, long n)
+{
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[i] = (float)reinterpret_cast<const _Float16 *>(in)[i];
+}
+
+void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t s)
+{
+  hipLaunchKernelGGL(f32_to_f16_trunc_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, in,
+                     reinterpret_cast<uint16_t *>(out), n);
+}
+
+void launch_f16_to_f32(const __half * in, float * out, long n, hipStream_t s)
+{
+  hipLaunchKernelGGL(f16_to_f32_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, in, out, n);
+}
+
+}  // namespace ivh

@@ -1,0 +1,85 @@
+"""Whole-model parity on the GPU through the C ABI (scripts/model_check.py protocol):
+raw head tensors vs the CPU oracle run on the same plan and inputs; pass bar
+mean_rel < 2e-2 and max_rel < 5e-2, or scale_rel < 5e-3 (model_check.py:25,196-201).
+Two different inputs, the second compared (README.md:153-155), batch consistency,
+graph replay vs eager launches."""
+import numpy as np
+import pytest
+
+import infvino_amd as ia
+from infvino_amd import planwriter as pw
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+M_MEAN, M_MAX, M_SCALE = 2e-2, 5e-2, 5e-3
+
+
+def _inputs(p, batch, seed):
+    rng = np.random.default_rng(seed)
+    return O.f2h(rng.random(p.numel(p.input_name) * batch).astype(np.float32))
+
+
+def _model_ok(got, ref, label):
+    mean_rel, max_rel, max_abs, scale_rel = O.rel_errors(O.h2f(got), O.h2f(ref))
+    print(f"{label}: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e} max_abs={max_abs:.2e} scale_rel={scale_rel:.2e}")
+    return (mean_rel < M_MEAN and max_rel < M_MAX) or scale_rel < M_SCALE
+
+
+@pytest.mark.parametrize("name,imgsz,batch", [("mobilenetv3-small", 224, 3), ("yolov8n-pose", 640, 2),
+                                              ("yolo11n-pose", 640, 1), ("yolov8n-pose", 320, 3)])
+def test_model_parity(tmp_path, name, imgsz, batch):
+    path, _ = pw.MODELS[name](str(tmp_path), seed=0, imgsz=imgsz)
+    p = O.Plan.load(path)
+    m = ia.PlanModel(path, 0, batch)
+    # frame 1: input A, frame 2: input B (staleness protocol); compare frame 2
+    m.setInput(_inputs(p, batch, 1), batch)
+    m.run(batch)
+    xb = _inputs(p, batch, 2)
+    m.setInput(xb, batch)
+    m.run(batch)
+    got = m.readOutput(0, batch)
+    ref = O.run_plan(p, xb, batch)[0].ravel()
+    assert _model_ok(got, ref, f"{name}@{imgsz} b{batch}")
+    m.close()
+
+
+def test_batch_and_replay_consistency(tmp_path):
+    """Image i of a batch equals the same image run alone; graph replay equals eager launches;
+    a fresh model on input B equals a model that ran A first (bit-exact)."""
+    path, _ = pw.yolov8n_pose(str(tmp_path), seed=0, imgsz=256)
+    p = O.Plan.load(path)
+    x = _inputs(p, 3, 5)
+    n = p.numel(p.input_name)
+    m = ia.PlanModel(path, 0, 3)
+    m.setInput(x, 3)
+    m.run(3)
+    full = m.readOutput(0, 3)
+    per = full.size // 3
+    for i in range(3):
+        m.setInput(x[i * n:(i + 1) * n], 1)
+        m.run(1)
+        assert np.array_equal(m.readOutput(0, 1), full[i * per:(i + 1) * per]), f"image {i}"
+    m.close()
+    e = ia.PlanModel(path, 0, 3, ia.IVH_FLAG_NO_GRAPH)
+    e.setInput(x, 3)
+    e.run(3)
+    assert np.array_equal(e.readOutput(0, 3), full)
+    e.close()
+
+
+def test_backend_f32_boundary(tmp_path):
+    """HipBackend.infer: f32 in (reference truncation to fp16), f32 Tensors out."""
+    path, _ = pw.mobilenetv3_small(str(tmp_path), seed=0)
+    be = ia.HipBackend(path, max_batch=2)
+    assert be.inputDims() == [1, 3, 224, 224]
+    assert be.outputShapes() == [[1, 1000]]
+    rng = np.random.default_rng(7)
+    xf = rng.random(2 * 3 * 224 * 224).astype(np.float32)
+    outs = be.infer(xf)
+    assert outs[0].shape == [2, 1000]
+    p = O.Plan.load(path)
+    ref = O.h2f(O.run_plan(p, O.f2h_trunc(xf), 2)[0].ravel())
+    assert _model_ok(O.f2h(outs[0].data.ravel()), O.f2h(ref), "backend mbv3 b2")
+    with pytest.raises(RuntimeError, match="numel mismatch"):
+        be.infer(xf[:100])

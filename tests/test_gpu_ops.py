@@ -1,0 +1,160 @@
+"""Op-level parity on the GPU: single-node plans through the C ABI vs the CPU oracle.
+
+Protocol of scripts/kernel_check.py (reference): seeded inputs, relative errors
+mean|d|/mean|ref| and max|d|/max|ref|; contract mean_rel < 1e-2, max_rel < 5e-2 against
+the reference-rounding oracle (IVO_REF, fp16 accumulation as the reference kernels do).
+Against the fp32 oracle (one fp16 rounding, the HIP kernels' own semantics) the bar is
+tighter: mean_rel < 2e-3, max_rel < 1e-2.  Data-movement ops must be bit-exact.
+"""
+import numpy as np
+import pytest
+
+import infvino_amd as ia
+from infvino_amd import planwriter as pw
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+OP_MEAN, OP_MAX = 1e-2, 5e-2          # scripts/kernel_check.py:20-22
+F32_MEAN, F32_MAX = 2e-3, 1e-2
+
+
+def _run(path, batch, seed=0, lo=0.0, hi=1.0, flags=0):
+    p = O.Plan.load(path)
+    rng = np.random.default_rng(seed)
+    x = O.f2h((lo + (hi - lo) * rng.random(p.numel(p.input_name) * batch)).astype(np.float32))
+    m = ia.PlanModel(path, 0, batch, flags)
+    m.setInput(x, batch)
+    m.run(batch)
+    got = [m.readOutput(i, batch) for i in range(m.outputCount())]
+    m.close()
+    return p, x, got
+
+
+def _check_f32(path, batch, seed=0, ref_mode=True, **kw):
+    p, x, got = _run(path, batch, seed, **kw)
+    ref = O.run_plan(p, x, batch)
+    for g, r in zip(got, ref):
+        mean_rel, max_rel, max_abs, _ = O.rel_errors(O.h2f(g), O.h2f(r.ravel()))
+        print(f"{path}: vs f32 oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e} max_abs={max_abs:.2e}")
+        assert mean_rel < F32_MEAN and max_rel < F32_MAX
+    if ref_mode:
+        refr = O.run_plan(p, x, batch, mode=O.REF)
+        for g, r in zip(got, refr):
+            mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(g), O.h2f(r.ravel()))
+            print(f"   vs reference-rounding oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+            assert mean_rel < OP_MEAN and max_rel < OP_MAX
+    return got
+
+
+def test_conv1x1_config(tmp_path):
+    """Single pointwise conv via the plan's conv1x1 op: 64->128 @ 80x80, SiLU."""
+    path, _ = pw.conv1x1_config(str(tmp_path))
+    for b in (1, 3):
+        _check_f32(path, b)
+
+
+@pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
+def test_conv_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act)
+    _check_f32(path, 2, ref_mode=(H * W * cin <= 160 * 160 * 32))
+
+
+@pytest.mark.parametrize("cin,cout,hw,k,s,act", [
+    (48, 32, 20, 1, 1, 1),     # ragged tiles: M not a multiple of 128
+    (51, 51, 20, 3, 1, 1),     # Cin not a multiple of 8 (pose keypoint branch)
+    (24, 40, 9, 3, 2, 3),      # odd spatial, stride 2, HardSwish
+    (16, 1, 12, 1, 1, 0),      # Cout = 1
+    (256, 256, 5, 3, 1, 1),    # Cout > BN (two N tiles)
+    (40, 72, 7, 5, 1, 2),      # 5x5 dense conv via conv_general
+    (64, 64, 6, 3, 1, 4),      # HardSigmoid after 3x3 (unfused in the plan, folded at load)
+])
+def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act)
+    _check_f32(path, 3, lo=-1.0)
+
+
+@pytest.mark.parametrize("c,hw,k,s,act", [(16, 112, 3, 2, 3), (96, 14, 5, 1, 3), (72, 28, 5, 2, 3),
+                                          (20, 9, 3, 1, 2), (24, 10, 5, 2, 4)])
+def test_depthwise(tmp_path, c, hw, k, s, act):
+    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=act)
+    _check_f32(path, 2, lo=-1.0)
+
+
+def _small_plan(d, build):
+    pb = pw.PlanBuilder(str(d), seed=3)
+    out = build(pb)
+    pb.output(out)
+    return pb.write()
+
+
+SMALL = {
+    "maxpool5": lambda pb: pb.maxpool(pb.input("x", [1, 24, 13, 17]), 5, 1, 2),
+    "maxpool3s2": lambda pb: pb.maxpool(pb.input("x", [1, 8, 15, 15]), 3, 2, 1),
+    "resize2": lambda pb: pb.upsample(pb.input("x", [1, 40, 7, 9]), 2),
+    "softmax_inner": lambda pb: pb.softmax(pb.input("x", [1, 4, 16, 300]), 2),
+    "softmax_last": lambda pb: pb.softmax(pb.input("x", [1, 2, 40, 40]), 3),
+    "permute0213": lambda pb: pb.permute(pb.input("x", [1, 4, 16, 50]), [0, 2, 1, 3]),
+    "permute0132": lambda pb: pb.permute(pb.input("x", [1, 3, 7, 11]), [0, 1, 3, 2]),
+    "slice_axis2": lambda pb: pb.slice(pb.input("x", [1, 17, 3, 40]), 2, 1, 2),
+    "concat_ch": lambda pb: pb.concat([pb.input("x", [1, 5, 6, 7]),
+                                       pb.unary(pb.const(np.ones((1, 3, 6, 7)), "k"), 2)]),
+    "concat_axis2": lambda pb: pb.concat([pb.reshape(pb.input("x", [1, 6, 4, 5]), [1, 6, 20]),
+                                          pb.const(np.arange(60).reshape(1, 6, 10) / 7.0, "k")], axis=2),
+    "ew_add_bcast": lambda pb: pb.binary(pb.input("x", [1, 17, 2, 30]), pb.const(np.linspace(-1, 1, 60).reshape(2, 30), "k"), 0),
+    "ew_mul_stride": lambda pb: pb.binary(pb.input("x", [1, 4, 30]), pb.const(np.linspace(1, 3, 30).reshape(1, 30), "k"), 2),
+    "ew_div_scalar": lambda pb: pb.binary(pb.input("x", [1, 3, 9, 9]), pb.const(np.array([2.0]), "k"), 3),
+    "ew_sub_same": lambda pb: pb.binary(pb.const(np.linspace(0, 5, 2 * 33).reshape(1, 2, 33), "k"), pb.input("x", [1, 2, 33]), 1),
+    "unary_sigmoid": lambda pb: pb.unary(pb.input("x", [1, 5, 40]), 0),
+    "unary_hswish": lambda pb: pb.unary(pb.input("x", [1, 6, 8, 8]), 3),
+    "gap": lambda pb: pb.gap(pb.input("x", [1, 24, 11, 13])),
+    "bmm": lambda pb: pb.matmul(pb.reshape(pb.input("x", [1, 2, 40, 32]), [1, 2, 40, 32]),
+                                pb.const(np.random.default_rng(0).normal(0, 0.2, (1, 2, 32, 24)), "k")),
+}
+
+
+EXACT = {"maxpool5", "maxpool3s2", "resize2", "permute0213", "permute0132", "slice_axis2",
+         "concat_ch", "concat_axis2"}
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+def test_small_ops(tmp_path, name):
+    path = _small_plan(tmp_path, SMALL[name])
+    p, x, got = _run(path, 3, lo=-3.0, hi=3.0)
+    ref = O.run_plan(p, x, 3)[0].ravel()
+    g = got[0]
+    exact = name in EXACT
+    if exact:
+        assert np.array_equal(g, ref), f"{name}: data movement must be bit-exact"
+    else:
+        mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(g), O.h2f(ref))
+        print(f"{name}: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+        assert mean_rel < F32_MEAN and max_rel < F32_MAX
+
+
+def test_se_block_channel_broadcast(tmp_path):
+    """SE: gap -> 1x1 ReLU -> 1x1 HardSigmoid -> channel-broadcast Mul on a channels-last tensor."""
+    def build(pb):
+        x = pb.input("x", [1, 16, 12, 12])
+        t = pb.conv(x, 32, 3, 1, act=pw.ACT_HSWISH)
+        t = pb.conv(t, 32, 3, 1, groups=32, act=pw.ACT_HSWISH)
+        t = pw._se(pb, t, 8)
+        return pb.conv(t, 16, 1, act=pw.ACT_NONE)
+    path = _small_plan(tmp_path, build)
+    _check_f32(path, 3, lo=-1.0)
+
+
+def test_c2f_zero_copy_concat(tmp_path):
+    """C2f (split views + bottleneck residual + 4-way concat written in place) and SPPF."""
+    def build(pb):
+        x = pb.input("x", [1, 32, 20, 20])
+        y = pw._c2f(pb, x, 64, 2, True)
+        return pw._sppf(pb, y, 64)
+    path = _small_plan(tmp_path, build)
+    _check_f32(path, 2, lo=-1.0)
+    # same result with every view/fusion switched off and with NCHW everywhere
+    p, x, base = _run(path, 2, lo=-1.0)
+    for flags in (ia.IVH_FLAG_NO_FUSE, ia.IVH_FLAG_NCHW_ONLY | ia.IVH_FLAG_NO_REUSE, ia.IVH_FLAG_DIRECT_ONLY):
+        _, _, alt = _run(path, 2, lo=-1.0, flags=flags)
+        mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(alt[0]), O.h2f(base[0]))
+        assert mean_rel < F32_MEAN and max_rel < F32_MAX, flags
