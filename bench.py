@@ -1,0 +1,167 @@
+"""Benchmark: YOLOv8n-pose 3x640x640 fp16 on one MI355X through the HIP backend.
+
+One step = one pass of the plan over one batch of 64 synthetic images already resident in
+HBM (the captured HIP graph of the whole plan).  Prints ONE JSON line on stdout; a per-node
+table goes to stderr.
+
+  value          images/s at batch 64 (whole job, one GPU)
+  latency_b1_ms  wall time of one synchronous batch-1 inference (graph replay)
+  roofline       dominant kernel (largest device time per batch-64 step): algorithmic FLOPs
+                 (or bytes) per launch / its mean launch time, HIP events on the model stream
+  conv_mfma_frac all conv FLOPs of a step / conv device time / dense fp16 MFMA peak
+  cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
+                 workload on this host's cores -- a reported baseline, not a target
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--imgsz", type=int, default=640)
+    ap.add_argument("--model", default="yolov8n-pose")
+    ap.add_argument("--profile-iters", type=int, default=5)
+    ap.add_argument("--cpu-images", type=int, default=-1, help="oracle sample size (-1: ~15 s worth)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the batch axis would shard as independent replicas, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import infvino_amd as ia
+    from infvino_amd import planwriter as pw
+
+    tmp = tempfile.TemporaryDirectory()
+    path, flops_img = pw.MODELS[args.model](tmp.name, seed=0, imgsz=args.imgsz)
+    B = args.batch
+    rng = np.random.default_rng(0)
+    n_in = 3 * args.imgsz * args.imgsz
+    x = rng.random(n_in * B, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+    # ---- throughput: K graph replays queued back to back, synchronised at both ends
+    m = ia.PlanModel(path, 0, B, ia.IVH_FLAG_ASYNC)
+    m.setInput(x, B)
+    for _ in range(args.warmup):
+        m.run(B)
+    m.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.run(B)
+    m.sync()
+    dt = time.perf_counter() - t0
+    ms_step = dt * 1e3 / args.steps
+    ips = B * args.steps / dt
+    log(f"[bench] {args.model}@{args.imgsz} batch {B}: {ms_step:.3f} ms/step, {ips:.0f} images/s")
+
+    # ---- per-node device time at batch B (HIP events on the model stream)
+    prof = m.profileNodes(B, args.profile_iters)
+    infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
+    conv_t = sum(t for t, inf in zip(prof, infos) if inf["op"].startswith("conv"))
+    conv_f = sum(inf["flops"] * B for inf in infos if inf["op"].startswith("conv"))
+    order = np.argsort(-prof)
+    log(f"[bench] per-node device time, batch {B} (sum {prof.sum():.3f} ms; graph step {ms_step:.3f} ms)")
+    for i in order[:25]:
+        inf = infos[i]
+        t = prof[i]
+        tf = inf["flops"] * B / (t * 1e-3) / 1e12 if t > 0 else 0
+        gbs = inf["bytes"] * B / (t * 1e-3) / 1e9 if t > 0 else 0
+        log(f"  {t:8.4f} ms  {tf:7.1f} TFLOP/s  {gbs:7.1f} GB/s  {inf['kernel']:12s} {inf['desc']}")
+    dom = int(order[0])
+    d = infos[dom]
+    t_dom = prof[dom] * 1e-3
+    ai = d["flops"] / d["bytes"] if d["bytes"] else float("inf")
+    ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if d["flops"] > 0 and ai >= ridge:
+        achieved = d["flops"] * B / t_dom / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4)}
+    else:
+        achieved = d["bytes"] * B / t_dom / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    roof.update({"traffic": None, "kernel": d["kernel"], "node": d["desc"],
+                 "launch_ms": round(t_dom * 1e3, 4),
+                 "flops_per_launch": d["flops"] * B, "bytes_per_launch": d["bytes"] * B})
+    conv_frac = conv_f / (conv_t * 1e-3) / 1e12 / PEAK_FP16_TFLOPS if conv_t > 0 else 0.0
+    m.close()
+
+    # ---- batch-1 latency: synchronous runs (graph replay), mean wall time
+    m1 = ia.PlanModel(path, 0, 1)
+    m1.setInput(x[:n_in], 1)
+    for _ in range(max(args.warmup, 5)):
+        m1.run(1)
+    lat = []
+    for _ in range(max(args.steps, 20)):
+        t = time.perf_counter()
+        m1.run(1)
+        lat.append(time.perf_counter() - t)
+    lat_ms = float(np.mean(lat) * 1e3)
+    log(f"[bench] batch 1 latency: mean {lat_ms:.3f} ms, p50 {np.median(lat) * 1e3:.3f} ms")
+    m1.close()
+
+    # ---- CPU baseline: the oracle on a bounded sample of the same workload
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        p = O.Plan.load(path)
+        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        t = time.perf_counter()
+        O.run_plan(p, x[:n_in], 1)
+        one = time.perf_counter() - t
+        k = args.cpu_images if args.cpu_images > 0 else max(1, min(64, int(15.0 / max(one, 1e-3))))
+        t = time.perf_counter()
+        O.run_plan(p, x[:n_in * k], k)
+        el = time.perf_counter() - t
+        cpu = {"value": round(k / el, 3), "unit": "images/s", "cores": cores, "kind": "port",
+               "sample": f"{k} images of {args.model} 3x{args.imgsz}x{args.imgsz} through the C oracle "
+                         f"(fp32 accumulate, OpenMP over output channels), {el:.1f} s"}
+        log(f"[bench] cpu oracle: {k / el:.3f} images/s on {cores} threads")
+
+    out = {
+        "metric": "images/sec at batch 1 & 64 (yolov8n-pose 640, fp16); conv MFMA % peak",
+        "value": round(ips, 1),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (uniform[0,1) frames, random-init He-normal weights, BN folded)",
+        "config": {"workload": f"{args.model} 3x{args.imgsz}x{args.imgsz} batch {B}, one plan pass per step",
+                   "batch": B, "imgsz": args.imgsz, "gflop_per_image": round(flops_img / 1e9, 3)},
+        "latency_b1_ms": round(lat_ms, 4),
+        "conv_mfma_frac": round(conv_frac, 4),
+        "tflops_effective": round(flops_img * ips / 1e12, 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    tmp.cleanup()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+"""Host-side tests (no GPU): the plan writer, the C ABI surface, the planner and its
+host bounds check (dry run), and the error behaviour of the boundary."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import infvino_amd as ia
+from infvino_amd import planwriter as pw
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRY = ia.IVH_FLAG_DRY_RUN
+
+
+def test_model_flops_match_reference_accounting(plans):
+    # conv+gemm GFLOP per image as the reference reports them (docs/benchmark.md:78-80)
+    assert abs(plans("yolov8n-pose")[1] / 1e9 - 9.178) < 0.005
+    assert abs(plans("mobilenetv3-small")[1] / 1e9 - 0.110) < 0.005
+    assert abs(plans("yolo11n-pose")[1] / 1e9 - 7.406) / 7.406 < 0.02
+
+
+def test_yolov8_node_census(plans):
+    p = O.Plan.load(plans("yolov8n-pose")[0])
+    ops = [n.op for n in p.nodes]
+    # 45 conv3x3 + 28 conv1x1 per frame, as the reference's y8 budget counts them
+    assert ops.count("conv3x3") == 45 and ops.count("conv1x1") == 28
+    assert p.dims[p.outputs[0]] == [1, 56, 8400]
+
+
+def test_header_symbols_exported():
+    hdr = open(os.path.join(ROOT, "include", "ivh.h")).read()
+    declared = set(re.findall(r"^\s*(?:int|const char \*)\s+(ivh_\w+)\s*\(", hdr, re.M))
+    assert declared == set(ia.SIGNATURES), declared ^ set(ia.SIGNATURES)
+    L = ia.lib()
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+@pytest.mark.parametrize("name", ["yolov8n-pose", "mobilenetv3-small", "yolo11n-pose"])
+def test_dry_run_plans_and_bounds(plans, name):
+    path = plans(name)[0]
+    m = ia.PlanModel(path, 0, 64, DRY)
+    for b in (1, 5, 64):
+        m.run(b)          # builds every launch and bounds-checks it on the host
+    arena, weights = m.memoryInfo(64)
+    assert arena > 0 and weights > 0
+    kinds = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    assert kinds.count("conv_igemm") > 0
+    m.close()
+
+
+def test_zero_copy_views_in_c2f(plans):
+    """C2f: cv1 output is split by views, the bottleneck outputs and both halves land in the
+    concat buffer in place, so no copy_c/concat node launches anything."""
+    path = plans("yolov8n-pose")[0]
+    m = ia.PlanModel(path, 0, 1, DRY)
+    m.run(1)
+    info = [m.nodeInfo(i) for i in range(m.nodeCount())]
+    assert all(i["kernel"] == "(view)" for i in info if i["op"] == "copy_c")
+    chan_concats = [i for i in info if i["op"] == "concat4"]
+    assert sum(i["kernel"] == "(view)" for i in chan_concats) >= 12
+    # residual adds of the bottlenecks are folded into the conv epilogue
+    assert not any(i["op"] == "ew_binary" and "+res" in i["desc"] for i in info)
+    assert sum("+res" in i["desc"] for i in info) == 6
+    m.close()
+
+
+@pytest.mark.parametrize("flags", [ia.IVH_FLAG_NO_FUSE, ia.IVH_FLAG_NCHW_ONLY, ia.IVH_FLAG_DIRECT_ONLY,
+                                   ia.IVH_FLAG_NO_REUSE])
+def test_dry_run_variants(plans, flags):
+    m = ia.PlanModel(plans("yolov8n-pose", imgsz=320)[0], 0, 4, DRY | flags)
+    m.run(4)
+    m.close()
+
+
+def _write(tmp_path, text, bins=()):
+    for name, n in bins:
+        np.zeros(n, np.float16).tofile(tmp_path / name)
+    p = tmp_path / "model.plan"
+    p.write_text(text)
+    return str(p)
+
+
+@pytest.mark.parametrize("text,bins,msg", [
+    ("tensor y 1 4\nnode ew_unary x y op=1 n=4\noutput y\n", (), "plan has no 'input' line"),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary x y op=1 n=4\n", (), "plan has no 'output' line"),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary x y op=1 n=4\noutput z\n", (), "output tensor not declared: z"),
+    ("input x 1 4\ntensor y 1 4\nnode frobnicate x y\noutput y\n", (), "unknown op: frobnicate"),
+    ("input x 1 4\ninit w w.bin 4 4\ntensor y 1 4\nnode conv1x1 w,x,-,- y\noutput y\n", (), "cannot open init"),
+    ("input x 1 4\ninit w w.bin 4 4\ntensor y 1 4\nnode conv1x1 w,x,-,- y\noutput y\n", [("w.bin", 7)], "too short"),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary q y op=1 n=4\noutput y\n", (), "missing tensor: q"),
+    ("input x 1 8 4 4\ninit w w.bin 8 8 3 3\ntensor y 1 8 4 4\nnode conv3x3 x,w,-,- y stride=1 pad=1 Hout=5 Wout=4\noutput y\n",
+     [("w.bin", 576)], "Hout/Wout inconsistent"),
+])
+def test_malformed_plans_raise(tmp_path, text, bins, msg):
+    path = _write(tmp_path, text, bins)
+    with pytest.raises(RuntimeError, match=re.escape(msg)):
+        m = ia.PlanModel(path, 0, 1, DRY)
+        m.run(1)
+
+
+def test_batch_range_checked(plans):
+    m = ia.PlanModel(plans("mobilenetv3-small")[0], 0, 2, DRY)
+    with pytest.raises(RuntimeError, match="out of range"):
+        m.run(3)
+    with pytest.raises(RuntimeError, match="out of range"):
+        m.run(0)
+    m.close()
+
+
+def test_missing_plan_file():
+    with pytest.raises(RuntimeError, match="cannot open plan"):
+        ia.PlanModel("/nonexistent/model.plan", 0, 1, DRY)
+
+
+def test_no_device_fails_loudly(plans):
+    """Without the dry-run flag and without a GPU the boundary raises (no CPU fallback)."""
+    if ia.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="HIP error"):
+        ia.PlanModel(plans("mobilenetv3-small")[0], 0, 1)
+
+
+def test_rel_errors_definition():
+    ref = np.array([1.0, -2.0, 4.0, 0.5])
+    got = ref + np.array([0.01, 0.0, -0.04, 0.0])
+    mean_rel, max_rel, max_abs, scale_rel = O.rel_errors(got, ref)
+    assert np.isclose(mean_rel, 0.0125 / 1.875) and np.isclose(max_rel, 0.01)
+    assert np.isclose(max_abs, 0.04) and np.isclose(scale_rel, 0.0125 / 4)
