@@ -118,6 +118,12 @@ def main():
         lat.append(time.perf_counter() - t)
     lat_ms = float(np.mean(lat) * 1e3)
     log(f"[bench] batch 1 latency: mean {lat_ms:.3f} ms, p50 {np.median(lat) * 1e3:.3f} ms")
+    prof1 = m1.profileNodes(1, args.profile_iters)
+    inf1 = [m1.nodeInfo(i) for i in range(m1.nodeCount())]
+    launched = sum(1 for i in inf1 if i["kernel"] != "(view)")
+    log(f"[bench] per-node device time, batch 1 (sum {prof1.sum():.3f} ms over {launched} launching nodes)")
+    for i in np.argsort(-prof1)[:15]:
+        log(f"  {prof1[i]:8.4f} ms  {inf1[i]['kernel']:12s} {inf1[i]['desc']}")
     m1.close()
 
     # ---- CPU baseline: the oracle on a bounded sample of the same workload

@@ -50,6 +50,7 @@ extern "C" {
 #define IVH_FLAG_NCHW_ONLY 0x8u   /* keep every activation in the plan's NCHW layout */
 #define IVH_FLAG_DIRECT_ONLY 0x10u /* no MFMA implicit GEMM: direct convolution kernels */
 #define IVH_FLAG_ASYNC 0x20u      /* ivh_run returns without waiting for the device */
+#define IVH_FLAG_NO_SPLITK 0x80u  /* never split the K loop of an implicit-GEMM conv */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 

@@ -91,9 +91,14 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
       aix[i] = -100000;
     }
   }
+  // K range of this work-group (split-K: blockIdx.z-th slice of the K tiles)
+  const int nk_all = p.kpad / BK;
+  const int per = (nk_all + p.ksplit - 1) / p.ksplit;
+  const int kt0 = blockIdx.z * per;
+  const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
   // K position of this thread's chunk: tap (ky,kx) and channel ci, advanced by BK per step.
   const int taps = p.K * p.K;
-  int ci = kc * 8, tap = 0, ky = 0, kx = 0;
+  int ci = kt0 * BK + kc * 8, tap = 0, ky = 0, kx = 0;
   auto norm_k = [&]() {
     while (ci >= p.cin8) {
       ci -= p.cin8;
@@ -153,13 +158,15 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
-  const int nk = p.kpad / BK;
-  load_tile(0);
-  store_tile(0);
+  const int nk = kt1 - kt0;
+  if (nk > 0) {
+    load_tile(kt0);
+    store_tile(0);
+  }
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) load_tile(kt + 1);
+    if (kt + 1 < nk) load_tile(kt0 + kt + 1);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       h8 fa[TN], fb[TM];
@@ -179,6 +186,25 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
     }
     if (kt + 1 < nk) store_tile(cur ^ 1);
     __syncthreads();
+  }
+
+  // ---- split-K: fp32 partials to the workspace [z][co][pixel]; the reduce kernel finishes
+  if (p.ksplit > 1) {
+    const int Npad = gridDim.y * BN;
+    float * wsz = p.ws + (long)blockIdx.z * Npad * M;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        const long pm = m0 + wm * TM * 32 + tm * 32 + (lane & 31);
+        if (pm >= M) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int co = n0 + wn * TN * 32 + tn * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          wsz[(long)co * M + pm] = acc[tn][tm][v];
+        }
+      }
+    return;
   }
 
   // ---- epilogue phase 1: bias + activation in fp32, one rounding, tile into LDS.
@@ -274,6 +300,31 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   }
 }
 
+// Split-K finish: y = act(sum_z ws[z] + b) (+ r), partials summed in fixed z order so the
+// result does not depend on scheduling.  One lane per (channel, pixel), pixels fastest.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const ConvParams p, int npad)
+{
+  const int HWo = p.Ho * p.Wo;
+  const long M = (long)p.batch * HWo;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * p.Cout) return;
+  const int co = (int)(i / M);
+  const long pm = i - (long)co * M;
+  float v = 0.0f;
+  for (int z = 0; z < p.ksplit; ++z) v += p.ws[((long)z * npad + co) * M + pm];
+  if (p.bias) v += p.bias[co];
+  v = act_f(v, p.act);
+  const int b = (int)(pm / HWo), hw = (int)(pm - (long)b * HWo);
+  const _Float16 hv = (_Float16)v;  // one rounding before the residual, as the fused epilogue
+  float o = (float)hv;
+  if (p.r.ptr) {
+    const long ri = p.r.layout == kNHWC ? (long)hw * p.r.cs + co : (long)co * p.r.cs + hw;
+    o += (float)reinterpret_cast<const _Float16 *>(p.r.ptr)[(long)b * p.r.img + ri];
+  }
+  const long yi = p.y.layout == kNHWC ? (long)hw * p.y.cs + co : (long)co * p.y.cs + hw;
+  reinterpret_cast<_Float16 *>(p.y.ptr)[(long)b * p.y.img + yi] = (_Float16)o;
+}
+
 // ---------------------------------------------------------------- host side
 
 // Tile table: a small CDNA4 choice per op (BN from Cout; BM = 128 pixels).
@@ -285,8 +336,28 @@ static void launch_t(const ConvParams & p, hipStream_t s)
 {
   using Sh = IgemmShape<WGM, WGN, TM, TN, 32>;
   const long M = (long)p.batch * p.Ho * p.Wo;
-  dim3 grid((unsigned)((M + Sh::BM - 1) / Sh::BM), (unsigned)((p.Cout + Sh::BN - 1) / Sh::BN));
+  dim3 grid((unsigned)((M + Sh::BM - 1) / Sh::BM), (unsigned)((p.Cout + Sh::BN - 1) / Sh::BN),
+            (unsigned)p.ksplit);
   hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, 32>), grid, dim3(256), 0, s, p);
+  if (p.ksplit > 1) {
+    const long n = M * p.Cout;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
+                       (int)grid.y * Sh::BN);
+  }
+}
+
+// Split-K factor: convs whose output tiles cannot fill the chip (batch 1, 20x20 / 40x40
+// feature maps) and whose K loop is long get their K range split across work-groups.
+int igemm_ksplit(long M, int cout, int kpad)
+{
+  const int bn = igemm_bn(cout);
+  const long tiles = ((M + 127) / 128) * ((cout + bn - 1) / bn);
+  const int nk = kpad / kIgemmBK;
+  if (tiles >= 192 || nk < 8) return 1;
+  int s = (int)((384 + tiles - 1) / tiles);
+  s = s < nk / 4 ? s : nk / 4;
+  s = s < 16 ? s : 16;
+  return s < 2 ? 1 : s;
 }
 
 void launch_conv_igemm(const ConvParams & p, hipStream_t s)

@@ -742,6 +742,14 @@ void Model::uploadWeights()
       pk.w = upload(P.data(), P.size() * 2);
       pk.cin8 = cin8;
       pk.kpad = kpad;
+    } else if (kind == 1 && G == 1 && cin_g <= 3 && K == 3 && Cout <= 32) {
+      // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened
+      const int rows = (Cout + 15) / 16 * 16;
+      std::vector<uint16_t> P((size_t)rows * 32, 0);
+      for (int co = 0; co < Cout; ++co)
+        for (int k = 0; k < cin_g * 9; ++k) P[(size_t)co * 32 + k] = W[(size_t)co * cin_g * 9 + k];
+      pk.w = upload(P.data(), P.size() * 2);
+      pk.stem = true;
     } else if (kind == 1) {
       const int cout_g = Cout / G;
       std::vector<float> P((size_t)G * cin_g * K * K * cout_g + 32, 0.0f);
@@ -759,6 +767,27 @@ void Model::uploadWeights()
       pk.w = upload(P.data(), P.size() * 4);
     }
     packed_[ni] = pk;
+  }
+  // split-K workspace: the largest need over every node and every batch size, so launch
+  // lists and captured graphs of different batch sizes share one fixed buffer
+  size_t need = 0;
+  if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
+    for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+      if (packed_[ni].kind != 0 || !packed_[ni].w) continue;
+      const Tensor & y = *T_[nodes_[ni].outs[0]];
+      const int cout = y.numel > 0 ? (int)T_[nodes_[ni].op == "conv1x1" ? nodes_[ni].ins[0] : nodes_[ni].ins[1]]->dims[0] : 0;
+      const long hwo = cout > 0 ? y.numel / cout : 0;
+      const int bn = igemm_bn(cout);
+      const long npad = (long)(cout + bn - 1) / bn * bn;
+      for (int b = 1; b <= max_batch_; ++b) {
+        const int ks = igemm_ksplit((long)b * hwo, cout, packed_[ni].kpad);
+        if (ks > 1) need = std::max(need, (size_t)ks * npad * b * hwo);
+      }
+    }
+  }
+  if (need) {
+    ws_ = static_cast<float *>(devAlloc(need * 4, false));
+    ws_floats_ = need;
   }
 }
 
@@ -845,12 +874,17 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
       L.kind = Launch::kIgemm;
       p.cin8 = pk.cin8;
       p.kpad = pk.kpad;
+      if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
+        p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
+        if (p.ksplit > 1) p.ws = ws_;
+      }
       if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) ||
           (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
         fail("implicit-GEMM input view not 16-byte aligned NHWC");
       if (p.kpad < p.K * p.K * p.cin8 || p.cin8 < p.Cin) fail("packed weight geometry");
     } else if (pk.kind == 1) {
       L.kind = Launch::kDirect;
+      p.stem_mfma = pk.stem ? 1 : 0;
     } else {
       L.kind = Launch::kDw;
     }
@@ -888,6 +922,9 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
       } else if (at.numel != yt.numel || bt.numel != yt.numel) {
         fail("ew_binary without bdims needs equal numel");
       }
+      // dense NCHW operands of equal numel are walked in the output's (C, H*W) order
+      if (q.a.layout == kNCHW) q.a.cs = yt.H * yt.W;
+      if (q.b.layout == kNCHW && q.b.img | q.b.cs) q.b.cs = yt.H * yt.W;
       L.small = kEwSame;
       out.push_back(L);
       return;
@@ -928,6 +965,7 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     const Tensor & at = *T_[n.ins.at(0)];
     if (at.numel != yt.numel) fail("ew_unary numel");
     q.a = view(at.name, batch);
+    if (q.a.layout == kNCHW) q.a.cs = yt.H * yt.W;
     q.op = unary_to_act(n.i("op"));
     L.small = kEwUnary;
     out.push_back(L);
@@ -1150,7 +1188,16 @@ void Model::validate(const Launch & l) const
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
       const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
+      if (p.ksplit > 1) {
+        const long M = (long)p.batch * HWo;
+        if ((size_t)p.ksplit * rows * M > ws_floats_) throw std::runtime_error("split-K workspace too small");
+        check(p.ws, 0, (long)p.ksplit * rows * M - 1, 4, "igemm split-K workspace");
+      }
       if (p.kpad % kIgemmBK) throw std::runtime_error("kpad not a multiple of the K tile");
+    } else if (l.kind == Launch::kDirect && p.stem_mfma) {
+      check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
+      check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");
+      if (p.Cin * 9 > 32 || p.Cout > 32) throw std::runtime_error("stem geometry");
     } else if (l.kind == Launch::kDirect) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "direct x");
       check(p.w, 0, (long)p.Cin * p.K * p.K * (p.Cout / p.G) + 16 - 1, 4, "direct w");

@@ -116,8 +116,16 @@ class Model {
   std::vector<void *> dev_allocs_;          // weights etc.
   size_t weight_bytes_ = 0;
   std::map<std::string, void *> init_dev_;  // raw fp16 inits
-  struct Packed { void * w = nullptr; float * bias = nullptr; int kind = 0; int kpad = 0, cin8 = 0; };
+  struct Packed {
+    void * w = nullptr;
+    float * bias = nullptr;
+    int kind = 0;
+    int kpad = 0, cin8 = 0;
+    bool stem = false;  // direct conv with Cin <= 3, 3x3: fp16 MFMA stem packing
+  };
   std::vector<Packed> packed_;              // per node
+  float * ws_ = nullptr;                    // split-K partials
+  size_t ws_floats_ = 0;
 
   std::map<int, std::vector<Launch>> launch_cache_;
   std::vector<size_t> node_launch_begin_;   // per node: [begin, end) into launches(batch)

@@ -43,6 +43,12 @@ struct ConvParams {
   int act = 0;
   int cin8 = 0;   // input channels rounded up to 8 (im2col K chunking)
   int kpad = 0;   // packed K per output channel, multiple of the K tile
+  // split-K (implicit GEMM): ksplit > 1 writes fp32 partials [ksplit][Npad][M] to ws and a
+  // second kernel reduces them in fixed order and applies the epilogue
+  int ksplit = 1;
+  float * ws = nullptr;
+  // stem MFMA path: w holds fp16 [ceil(Cout/16)*16][32] (k = ci*9 + ky*3 + kx, zero padded)
+  int stem_mfma = 0;
 };
 
 // Generic small-op descriptor (elementwise / pooling / data movement).

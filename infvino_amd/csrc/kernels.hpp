@@ -11,6 +11,7 @@ int igemm_bn(int cout);                    // N tile of the implicit GEMM for a 
 constexpr int kIgemmBK = 32;               // K tile (packed weight rows are a multiple)
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
 void launch_conv_igemm(const ConvParams & p, hipStream_t s);
+int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
 
 // kernels_misc.hip
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout

@@ -5,6 +5,8 @@
 #include "ivh_internal.hpp"
 #include "kernels.hpp"
 
+#include <initializer_list>
+
 namespace ivh {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -102,11 +104,108 @@ __global__ void __launch_bounds__(256) conv_direct_kernel(const ConvParams p)
   }
 }
 
+
+// Stem convolution with few input channels (conv3x3_cin3, kernels/conv_cin3.cl:67-118) on
+// fp16 MFMA: K = Cin*9 taps padded to 32, one v_mfma_f32_16x16x32_f16 per 16 output pixels
+// and 16 output channels.  Operand A (weights, [co][k], k = ci*9 + ky*3 + kx exactly the
+// plan's [Cout][Cin][3][3] order) is loaded once per lane; operand B is gathered straight
+// from the input (im2col in registers).  D layout: lane holds pixel lane%16 and channels
+// 4*(lane/16) + 0..3, so a wave stores 16 pixels x 32 bytes contiguously (channels-last).
+typedef _Float16 h8s __attribute__((ext_vector_type(8)));
+typedef float f4s __attribute__((ext_vector_type(4)));
+typedef _Float16 h4s __attribute__((ext_vector_type(4)));
+
+template <int NT, bool NCHW_IN>
+__global__ void __launch_bounds__(256) conv_stem_mfma_kernel(const ConvParams p)
+{
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.y;
+  const int HWo = p.Ho * p.Wo;
+  const int taps = p.Cin * 9;
+  const _Float16 * W = reinterpret_cast<const _Float16 *>(p.w);  // [NT*16][32]
+  h8s afrag[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    afrag[t] = *reinterpret_cast<const h8s *>(W + (t * 16 + (lane & 15)) * 32 + (lane >> 4) * 8);
+  const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img;
+  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr);
+  const bool vec = p.y.layout == kNHWC && ((p.y.cs | (int)p.y.img | (int)(reinterpret_cast<uintptr_t>(yb) >> 1)) & 3) == 0;
+  // this wave: 4 groups of 16 consecutive output pixels
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int pix = (blockIdx.x * 4 + wave) * 64 + g * 16 + (lane & 15);
+    const bool pvalid = pix < HWo;
+    const int oy = pix / p.Wo, ox = pix - oy * p.Wo;
+    const int iy0 = oy * p.S - p.P, ix0 = ox * p.S - p.P;
+    h8s bfrag;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = (lane >> 4) * 8 + e;
+      float v = 0.0f;
+      if (pvalid && k < taps) {
+        const int ci = k / 9, r = k - ci * 9, ky = r / 3, kx = r - ky * 3;
+        const int iy = iy0 + ky, ix = ix0 + kx;
+        if ((unsigned)iy < (unsigned)p.H && (unsigned)ix < (unsigned)p.W) {
+          const int q = iy * p.W + ix;
+          v = (float)xb[NCHW_IN ? (long)ci * p.x.cs + q : (long)q * p.x.cs + ci];
+        }
+      }
+      bfrag[e] = (_Float16)v;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f4s acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag[t], bfrag, acc, 0, 0, 0);
+      if (!pvalid) continue;
+      const int co0 = t * 16 + (lane >> 4) * 4;
+      float o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int co = co0 + v;
+        float x = acc[v] + (co < p.Cout && p.bias ? p.bias[co] : 0.0f);
+        x = actf(x, p.act);
+        if (p.r.ptr && co < p.Cout) x += vld(p.r, b, co, pix);
+        o[v] = x;
+      }
+      if (vec && co0 + 4 <= p.Cout) {
+        h4s hv;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) hv[v] = (_Float16)o[v];
+        *reinterpret_cast<h4s *>(yb + (long)b * p.y.img + (long)pix * p.y.cs + co0) = hv;
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (co0 + v < p.Cout) vst(p.y, b, co0 + v, pix, o[v]);
+      }
+    }
+  }
+}
+
+bool stem_supported(const ConvParams & p)
+{
+  return p.K == 3 && p.G == 1 && p.Cin >= 1 && p.Cin <= 3 && p.Cout <= 32 && p.stem_mfma;
+}
+
 void launch_conv_direct(const ConvParams & p, hipStream_t s)
 {
+  if (stem_supported(p)) {
+    const dim3 grid(nblk((long)p.Ho * p.Wo, 256), (unsigned)p.batch);
+    const bool nchw = p.x.layout == kNCHW;
+    if (p.Cout <= 16) {
+      if (nchw) hipLaunchKernelGGL((conv_stem_mfma_kernel<1, true>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((conv_stem_mfma_kernel<1, false>), grid, dim3(256), 0, s, p);
+    } else {
+      if (nchw) hipLaunchKernelGGL((conv_stem_mfma_kernel<2, true>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((conv_stem_mfma_kernel<2, false>), grid, dim3(256), 0, s, p);
+    }
+    return;
+  }
   const int cout_g = p.Cout / p.G;
   const long Mt = (long)p.batch * p.Ho * p.Wo;
-  if (cout_g % 16 == 0 || (p.G == 1 && cout_g > 8)) {
+  if (cout_g < 4) {
+    const long n = Mt * cout_g * p.G;
+    hipLaunchKernelGGL(conv_direct_kernel<1>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+  } else if (cout_g % 16 == 0 || (p.G == 1 && cout_g > 8)) {
     const long n = Mt * ((cout_g + 15) / 16) * p.G;
     hipLaunchKernelGGL(conv_direct_kernel<16>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
   } else if (cout_g % 8 == 0 || p.G == 1) {
@@ -454,8 +553,287 @@ __global__ void bias_add_kernel(const SmallParams q)  // ops.cl:268-274
   reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = (_Float16)(x + bb);
 }
 
+
+// ---------------------------------------------------------- 16-byte vector paths
+// Used when every operand of an op is channels-last with C % 8 == 0 (one lane = one pixel x
+// 8 channels) or dense NCHW with 8 | C*H*W (one lane = 8 consecutive elements).  The
+// per-channel operand of ew_binary_ch is a plain [C] vector per image.
+
+__device__ __forceinline__ h8 ld8(const __half * p, long off) { return *reinterpret_cast<const h8 *>(reinterpret_cast<const _Float16 *>(p) + off); }
+__device__ __forceinline__ void st8(__half * p, long off, h8 v) { *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p) + off) = v; }
+
+// mode: 0 binary, 1 binary with scalar b, 2 unary (op = act), 3 copy, 4 chan (a = [C]), 5 chan (b = [C])
+__global__ void __launch_bounds__(256) ew_vec8_kernel(const SmallParams q, int mode)
+{
+  const int HW = q.H * q.W;
+  const int C8 = q.C >> 3;
+  const int total8 = (int)(((long)q.C * HW) >> 3);
+  const int i8 = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i8 >= total8) return;
+  const bool nhwc = q.y.layout == kNHWC;
+  int c;
+  long pa, pb, py;
+  if (nhwc) {
+    const int p = i8 / C8;
+    c = (i8 - p * C8) * 8;
+    pa = (long)p * q.a.cs + c;
+    pb = (long)p * q.b.cs + c;
+    py = (long)p * q.y.cs + c;
+  } else {
+    const long e = (long)i8 * 8;
+    c = (int)(e / HW);
+    pa = pb = py = e;
+  }
+  pa += (long)b * q.a.img;
+  pb += (long)b * q.b.img;
+  py += (long)b * q.y.img;
+  h8 out;
+  if (mode == 3) {
+    out = ld8(q.a.ptr, pa);
+  } else if (mode == 2) {
+    const h8 x = ld8(q.a.ptr, pa);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)actf((float)x[e], q.op);
+  } else {
+    const _Float16 * ap = reinterpret_cast<const _Float16 *>(q.a.ptr);
+    const _Float16 * bp = reinterpret_cast<const _Float16 *>(q.b.ptr);
+    float av[8], bv[8];
+    if (mode == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[e] = (float)ap[(long)b * q.a.img + c + (nhwc ? e : 0)];
+    } else {
+      const h8 x = ld8(q.a.ptr, pa);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[e] = (float)x[e];
+    }
+    if (mode == 5) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bv[e] = (float)bp[(long)b * q.b.img + c + (nhwc ? e : 0)];
+    } else if (mode == 1) {
+      const float s0 = (float)bp[0];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bv[e] = s0;
+    } else {
+      const h8 x = ld8(q.b.ptr, pb);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bv[e] = (float)x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)binop(av[e], bv[e], q.op);
+  }
+  st8(q.y.ptr, py, out);
+}
+
+// nearest resize / max pool, channels-last, one lane = one output pixel x 8 channels
+__global__ void __launch_bounds__(256) pool_vec8_kernel(const SmallParams q, int is_max)
+{
+  const int C8 = q.C >> 3;
+  const int HWo = q.Ho * q.Wo;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= HWo * C8) return;
+  const int p = i / C8, c = (i - p * C8) * 8;
+  const int oh = p / q.Wo, ow = p - oh * q.Wo;
+  const long abase = (long)b * q.a.img + c;
+  h8 out;
+  if (!is_max) {
+    out = ld8(q.a.ptr, abase + (long)((oh / q.i0) * q.W + ow / q.i0) * q.a.cs);
+  } else {
+    float m[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m[e] = -3.4e38f;
+    for (int kh = 0; kh < q.K; ++kh) {
+      const int yy = oh * q.S - q.P + kh;
+      if ((unsigned)yy >= (unsigned)q.H) continue;
+      for (int kw = 0; kw < q.K; ++kw) {
+        const int xx = ow * q.S - q.P + kw;
+        if ((unsigned)xx >= (unsigned)q.W) continue;
+        const h8 v = ld8(q.a.ptr, abase + (long)(yy * q.W + xx) * q.a.cs);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], (float)v[e]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)m[e];
+  }
+  st8(q.y.ptr, (long)b * q.y.img + (long)p * q.y.cs + c, out);
+}
+
+// Row copies of `L` contiguous elements (L % 8 == 0): slice_axis, concat along an inner
+// axis, permute mode 0.  kind 0 slice, 1 concat part, 2 permute.
+__global__ void __launch_bounds__(256) rows_vec8_kernel(const SmallParams q, int kind, int L, int rows)
+{
+  const int L8 = L >> 3;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (t >= rows * L8) return;
+  const int r = t / L8, j = (t - r * L8) * 8;
+  int src, dst;
+  if (kind == 0) {        // y row r = (o, l) <- x row o*axdim + start + l
+    const int o = r / q.i4, l = r - o * q.i4;
+    dst = r;
+    src = o * q.i1 + q.i3 + l;
+  } else if (kind == 1) { // x row r = (o, ax) -> y row o*tot + off + ax
+    const int o = r / q.i1, ax = r - o * q.i1;
+    src = r;
+    dst = o * q.i3 + q.i4 + ax;
+  } else {                // y row r = (d2, d1) <- x row d1*D2 + d2
+    const int d2 = r / q.i0, d1 = r - d2 * q.i0;
+    dst = r;
+    src = d1 * q.i1 + d2;
+  }
+  st8(q.y.ptr, (long)b * q.y.img + (long)dst * L + j, ld8(q.a.ptr, (long)b * q.a.img + (long)src * L + j));
+}
+
+// ew_binary_bcast with 8 consecutive outputs per lane (output innermost extent % 8 == 0).
+__global__ void __launch_bounds__(256) ew_bcast8_kernel(const SmallParams q)
+{
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  const int n8 = (int)(q.n >> 3);
+  if (t >= n8) return;
+  int rem = t * 8, ai = 0, bi = 0;
+  for (int r = q.rank - 1; r >= 0; --r) {
+    const int od = q.dims[r];
+    const int coord = rem % od;
+    rem /= od;
+    ai += coord * q.dims[q.rank + r];
+    bi += coord * q.dims[2 * q.rank + r];
+  }
+  const int sa = q.dims[2 * q.rank - 1], sb = q.dims[3 * q.rank - 1];
+  const _Float16 * ap = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img;
+  const _Float16 * bp = reinterpret_cast<const _Float16 *>(q.b.ptr) + (long)b * q.b.img;
+  h8 out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = (_Float16)binop((float)ap[ai + e * sa], (float)bp[bi + e * sb], q.op);
+  st8(q.y.ptr, (long)b * q.y.img + (long)t * 8, out);
+}
+
+// softmax over an axis with stride `inner` > 1: values cached in registers (axdim <= 32).
+__global__ void __launch_bounds__(256) softmax_reg_kernel(const SmallParams q)
+{
+  const int total = q.i0 * q.i2;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= total) return;
+  const int o = i / q.i2, r = i - o * q.i2;
+  const long base = (long)o * q.i1 * q.i2 + r;
+  const _Float16 * x = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img + base;
+  _Float16 * y = reinterpret_cast<_Float16 *>(q.y.ptr) + (long)b * q.y.img + base;
+  float v[32];
+  float m = -3.4e38f;
+#pragma unroll
+  for (int a = 0; a < 32; ++a)
+    if (a < q.i1) { v[a] = (float)x[(long)a * q.i2]; m = fmaxf(m, v[a]); }
+  float s = 0.0f;
+#pragma unroll
+  for (int a = 0; a < 32; ++a)
+    if (a < q.i1) { v[a] = __expf(v[a] - m); s += v[a]; }
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int a = 0; a < 32; ++a)
+    if (a < q.i1) y[(long)a * q.i2] = (_Float16)(v[a] * inv);
+}
+
+// softmax over the contiguous last axis (inner == 1): one wave per row, shuffle reductions.
+__global__ void __launch_bounds__(256) softmax_row_kernel(const SmallParams q)
+{
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int b = blockIdx.y;
+  if (row >= q.i0) return;
+  const _Float16 * x = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img + (long)row * q.i1;
+  _Float16 * y = reinterpret_cast<_Float16 *>(q.y.ptr) + (long)b * q.y.img + (long)row * q.i1;
+  float m = -3.4e38f;
+  for (int a = lane; a < q.i1; a += 64) m = fmaxf(m, (float)x[a]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  float s = 0.0f;
+  for (int a = lane; a < q.i1; a += 64) s += __expf((float)x[a] - m);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  const float inv = 1.0f / s;
+  for (int a = lane; a < q.i1; a += 64) y[a] = (_Float16)(__expf((float)x[a] - m) * inv);
+}
+
+namespace {
+bool al8(const View & v) { return ((v.img | (long)(reinterpret_cast<uintptr_t>(v.ptr) >> 1)) & 7) == 0; }
+// every listed view channels-last, 8-channel aligned
+bool nhwc8(const SmallParams & q, std::initializer_list<const View *> vs)
+{
+  if (q.C % 8) return false;
+  for (const View * v : vs)
+    if (v->layout != kNHWC || (v->cs % 8) || !al8(*v)) return false;
+  return true;
+}
+// every listed view dense NCHW (channel stride == H*W), 8 | C*H*W
+bool dense8(const SmallParams & q, std::initializer_list<const View *> vs, bool chan)
+{
+  const long HW = (long)q.H * q.W;
+  if (((long)q.C * HW) % 8 || (chan && HW % 8)) return false;
+  for (const View * v : vs)
+    if (v->layout != kNCHW || (q.C > 1 && v->cs != HW) || !al8(*v)) return false;
+  return true;
+}
+}  // namespace
+
+// Picks the vector kernel for a small op when its operands allow it; returns false to
+// fall back to the scalar kernel.
+bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
+{
+  const dim3 blk(256);
+  const unsigned B = (unsigned)q.batch;
+  const long n8 = (long)q.C * q.H * q.W / 8;
+  auto ew = [&](int mode, std::initializer_list<const View *> vs, bool chan) {
+    if (!(nhwc8(q, vs) || dense8(q, vs, chan))) return false;
+    hipLaunchKernelGGL(ew_vec8_kernel, dim3(nblk(n8, 256), B), blk, 0, s, q, mode);
+    return true;
+  };
+  switch (kind) {
+  case kEwSame:
+    if (q.b.img == 0 && q.b.cs == 0) return ew(1, {&q.a, &q.y}, false);
+    return ew(0, {&q.a, &q.b, &q.y}, false);
+  case kEwUnary: return ew(2, {&q.a, &q.y}, false);
+  case kCopy: return ew(3, {&q.a, &q.y}, false);
+  case kEwChan: return q.i0 ? ew(4, {&q.b, &q.y}, true) : ew(5, {&q.a, &q.y}, true);
+  case kMaxPool:
+  case kResizeNN:
+    if (!nhwc8(q, {&q.a, &q.y})) return false;
+    hipLaunchKernelGGL(pool_vec8_kernel, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q,
+                       kind == kMaxPool ? 1 : 0);
+    return true;
+  case kSliceAxis:
+  case kConcatOuter:
+  case kPermute: {
+    const int L = q.i2;
+    if (L % 8 || !al8(q.a) || !al8(q.y)) return false;
+    if (kind == kPermute && q.op != 0) return false;
+    const int rows = kind == kSliceAxis ? q.i0 * q.i4 : (kind == kConcatOuter ? q.i0 * q.i1 : q.i0 * q.i1);
+    const int k = kind == kSliceAxis ? 0 : (kind == kConcatOuter ? 1 : 2);
+    hipLaunchKernelGGL(rows_vec8_kernel, dim3(nblk((long)rows * (L / 8), 256), B), blk, 0, s, q, k, L, rows);
+    return true;
+  }
+  case kEwBcast:
+    if (q.n % 8 || q.dims[q.rank - 1] % 8 || !al8(q.y)) return false;
+    hipLaunchKernelGGL(ew_bcast8_kernel, dim3(nblk(q.n / 8, 256), B), blk, 0, s, q);
+    return true;
+  case kSoftmax:
+    if (q.i2 > 1 && q.i1 <= 32) {
+      hipLaunchKernelGGL(softmax_reg_kernel, dim3(nblk((long)q.i0 * q.i2, 256), B), blk, 0, s, q);
+      return true;
+    }
+    if (q.i2 == 1) {
+      hipLaunchKernelGGL(softmax_row_kernel, dim3((unsigned)((q.i0 + 3) / 4), B), blk, 0, s, q);
+      return true;
+    }
+    return false;
+  default: return false;
+  }
+}
+
 void launch_small(int kind, const SmallParams & q, hipStream_t s)
 {
+  if (launch_small_vec(kind, q, s)) return;
   const dim3 blk(256);
   const unsigned B = (unsigned)q.batch;
   const long nchw = (long)q.C * q.H * q.W;

@@ -68,10 +68,29 @@ def test_conv_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     (256, 256, 5, 3, 1, 1),    # Cout > BN (two N tiles)
     (40, 72, 7, 5, 1, 2),      # 5x5 dense conv via conv_general
     (64, 64, 6, 3, 1, 4),      # HardSigmoid after 3x3 (unfused in the plan, folded at load)
+    (3, 32, 17, 3, 1, 1),      # stem MFMA path, two 16-channel tiles, ragged pixel groups
+    (3, 8, 15, 3, 2, 3),       # stem MFMA path, Cout < 16
+    (2, 16, 9, 3, 1, 1),       # stem MFMA path, Cin = 2
 ])
 def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act)
     _check_f32(path, 3, lo=-1.0)
+
+
+@pytest.mark.parametrize("cin,cout,hw,k,s,batch", [
+    (256, 256, 20, 3, 1, 1),   # batch 1: 8 output tiles, 72 K tiles -> split-K
+    (128, 51, 40, 3, 1, 1),
+    (512, 256, 20, 1, 1, 1),
+    (384, 128, 40, 1, 1, 2),
+    (128, 256, 40, 3, 2, 3),
+])
+def test_split_k(tmp_path, cin, cout, hw, k, s, batch):
+    """Small-M / long-K convs take the split-K path (partials + fixed-order reduce)."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=pw.ACT_SILU)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, nosplit = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(nosplit[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
 @pytest.mark.parametrize("c,hw,k,s,act", [(16, 112, 3, 2, 3), (96, 14, 5, 1, 3), (72, 28, 5, 2, 3),
