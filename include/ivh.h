@@ -51,6 +51,7 @@ extern "C" {
 #define IVH_FLAG_DIRECT_ONLY 0x10u /* no MFMA implicit GEMM: direct convolution kernels */
 #define IVH_FLAG_ASYNC 0x20u      /* ivh_run returns without waiting for the device */
 #define IVH_FLAG_NO_SPLITK 0x80u  /* never split the K loop of an implicit-GEMM conv */
+#define IVH_FLAG_NO_HALO 0x100u   /* 3x3 convs use the im2col path, never the LDS halo tile */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 

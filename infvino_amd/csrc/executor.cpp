@@ -742,6 +742,26 @@ void Model::uploadWeights()
       pk.w = upload(P.data(), P.size() * 2);
       pk.cin8 = cin8;
       pk.kpad = kpad;
+      // 3x3 stride 1 with a well-filled tile grid: also pack for the LDS halo kernel
+      const int S = is3 ? n.i("stride", 1) : n.i("S", 1);
+      const Tensor & yo = *T_[n.outs[0]];
+      const int Ho = yo.H, Wo = yo.W;
+      if (K == 3 && S == 1 && x_nhwc && !(flags_ & IVH_FLAG_NO_HALO) && Ho >= 8 && Wo >= 8) {
+        const int tw = halo_tw(Ho, Wo), th = 128 / tw;
+        const long slots = (long)((Wo + tw - 1) / tw) * tw * ((Ho + th - 1) / th) * th;
+        if (slots * 4 <= (long)Ho * Wo * 5) {
+          const int nch = (cin_g + 31) / 32;
+          const int kh = nch * 9 * 32;
+          std::vector<uint16_t> Q((size_t)rows * kh, 0);
+          for (int co = 0; co < Cout; ++co)
+            for (int ci = 0; ci < cin_g; ++ci)
+              for (int t = 0; t < 9; ++t)
+                Q[(size_t)co * kh + ((ci / 32) * 9 + t) * 32 + (ci % 32)] = W[((size_t)co * cin_g + ci) * 9 + t];
+          pk.w_halo = upload(Q.data(), Q.size() * 2);
+          pk.kpad_halo = kh;
+          pk.halo = tw;
+        }
+      }
     } else if (kind == 1 && G == 1 && cin_g <= 3 && K == 3 && Cout <= 32) {
       // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened
       const int rows = (Cout + 15) / 16 * 16;
@@ -877,6 +897,11 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
       if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
         p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
         if (p.ksplit > 1) p.ws = ws_;
+      }
+      if (p.ksplit == 1 && pk.halo && p.K == 3 && p.S == 1) {
+        p.halo = pk.halo;
+        p.w = static_cast<const __half *>(pk.w_halo);
+        p.kpad = pk.kpad_halo;
       }
       if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) ||
           (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
@@ -1188,6 +1213,10 @@ void Model::validate(const Launch & l) const
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
       const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
+      if (p.halo) {
+        if (p.K != 3 || p.S != 1 || p.ksplit != 1 || (p.halo != 8 && p.halo != 16)) throw std::runtime_error("halo geometry");
+        if (p.kpad != (p.Cin + 31) / 32 * 9 * 32) throw std::runtime_error("halo weight packing");
+      }
       if (p.ksplit > 1) {
         const long M = (long)p.batch * HWo;
         if ((size_t)p.ksplit * rows * M > ws_floats_) throw std::runtime_error("split-K workspace too small");

@@ -122,6 +122,9 @@ class Model {
     int kind = 0;
     int kpad = 0, cin8 = 0;
     bool stem = false;  // direct conv with Cin <= 3, 3x3: fp16 MFMA stem packing
+    void * w_halo = nullptr;  // 3x3 s1: [co][chunk][tap][32] packing for the halo kernel
+    int kpad_halo = 0;
+    int halo = 0;             // tile choice (16 / 8), 0 = not eligible
   };
   std::vector<Packed> packed_;              // per node
   float * ws_ = nullptr;                    // split-K partials

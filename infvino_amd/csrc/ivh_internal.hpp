@@ -49,6 +49,9 @@ struct ConvParams {
   float * ws = nullptr;
   // stem MFMA path: w holds fp16 [ceil(Cout/16)*16][32] (k = ci*9 + ky*3 + kx, zero padded)
   int stem_mfma = 0;
+  // 3x3 stride-1 halo kernel: 16 -> 8x16 output tiles, 8 -> 16x8 tiles, 0 -> im2col kernel;
+  // w is then packed [co][32-channel chunk][tap][32]
+  int halo = 0;
 };
 
 // Generic small-op descriptor (elementwise / pooling / data movement).

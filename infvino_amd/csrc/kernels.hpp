@@ -12,6 +12,7 @@ constexpr int kIgemmBK = 32;               // K tile (packed weight rows are a m
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
 void launch_conv_igemm(const ConvParams & p, hipStream_t s);
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
+int halo_tw(int Ho, int Wo);                    // 16: 8x16 tiles, 8: 16x8 tiles
 
 // kernels_misc.hip
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout

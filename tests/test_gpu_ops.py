@@ -77,6 +77,33 @@ def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
     _check_f32(path, 3, lo=-1.0)
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch", [
+    (64, 64, 80, 80, 2),       # the YOLOv8 80x80 bottleneck shape
+    (48, 40, 33, 35, 2),       # ragged 8x16 tiles on both axes
+    (24, 16, 40, 24, 3),       # Cin < 32: one zero-filled chunk
+    (51, 51, 48, 48, 1),       # Cin not a multiple of 8 (pose keypoint branch)
+    (96, 136, 24, 40, 2),      # Cout > 128: two N tiles, 16x8 tiles
+])
+def test_halo_conv3x3(tmp_path, cin, cout, H, W, batch):
+    """3x3 stride-1 convs through the LDS halo kernel vs the oracle and vs the im2col path."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=pw.ACT_SILU)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_SPLITK)
+    _, _, im2col = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_HALO | ia.IVH_FLAG_NO_SPLITK)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(im2col[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def test_halo_residual_chain(tmp_path):
+    """Bottleneck chain (3x3, 3x3 + residual) on 48x48: halo kernel with the fused residual."""
+    def build(pb):
+        x = pb.input("x", [1, 32, 48, 48])
+        t = pb.conv(x, 32, 3)
+        t = pb.conv(t, 32, 3)
+        return pb.binary(x, t, 0)
+    path = _small_plan(tmp_path, build)
+    _check_f32(path, 2, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
+
+
 @pytest.mark.parametrize("cin,cout,hw,k,s,batch", [
     (256, 256, 20, 3, 1, 1),   # batch 1: 8 output tiles, 72 K tiles -> split-K
     (128, 51, 40, 3, 1, 1),
