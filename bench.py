@@ -32,6 +32,39 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def calibrate(ia, pw):
+    """A plain streaming kernel of known size: ReLU over 8 images x 8 x 1024 x 1024 fp16
+    (128 MiB read, 128 MiB written per launch).  Its FETCH_SIZE / WRITE_SIZE per dispatch,
+    over the known byte counts, give the counter-to-bytes factors."""
+    with tempfile.TemporaryDirectory() as d:
+        pb = pw.PlanBuilder(d, seed=0)
+        y = pb.unary(pb.input("x", [1, 8, 1024, 1024]), pw.UN_RELU)
+        pb.output(y)
+        m = ia.PlanModel(pb.write(), 0, 8, ia.IVH_FLAG_NO_GRAPH)
+        m.setInput(np.zeros(8 * 8 * 1024 * 1024, np.uint16), 8)
+        for _ in range(5):
+            m.run(8)
+        m.close()
+    log("[bench] calibration pass: 5 x (128 MiB read + 128 MiB write)")
+
+
+def measured_traffic(node_desc, batch):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
+    summary (profiles/traffic_dominant_kernel.md), when it was measured on this node."""
+    path = os.path.join(ROOT, "profiles", "traffic_dominant_kernel.md")
+    if not os.path.exists(path):
+        return None
+    node = bytes_ = b = None
+    for line in open(path):
+        if line.startswith("node:"):
+            node = line.split(":", 1)[1].strip()
+        elif line.startswith("batch:"):
+            b = int(line.split(":", 1)[1])
+        elif line.startswith("hbm_bytes_per_launch:"):
+            bytes_ = float(line.split(":", 1)[1])
+    return bytes_ if (node == node_desc and b == batch) else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -43,6 +76,11 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=5)
     ap.add_argument("--cpu-images", type=int, default=-1, help="oracle sample size (-1: ~15 s worth)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch node by node instead of replaying the captured HIP graph")
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib"],
+                    help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
+                         "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -52,6 +90,9 @@ def main():
     import infvino_amd as ia
     from infvino_amd import planwriter as pw
 
+    if args.phase == "calib":
+        calibrate(ia, pw)
+        return
     tmp = tempfile.TemporaryDirectory()
     path, flops_img = pw.MODELS[args.model](tmp.name, seed=0, imgsz=args.imgsz)
     B = args.batch
@@ -60,7 +101,8 @@ def main():
     x = rng.random(n_in * B, dtype=np.float32).astype(np.float16).view(np.uint16)
 
     # ---- throughput: K graph replays queued back to back, synchronised at both ends
-    m = ia.PlanModel(path, 0, B, ia.IVH_FLAG_ASYNC)
+    gflag = ia.IVH_FLAG_NO_GRAPH if args.no_graph else 0
+    m = ia.PlanModel(path, 0, B, ia.IVH_FLAG_ASYNC | gflag)
     m.setInput(x, B)
     for _ in range(args.warmup):
         m.run(B)
@@ -74,6 +116,10 @@ def main():
     ips = B * args.steps / dt
     log(f"[bench] {args.model}@{args.imgsz} batch {B}: {ms_step:.3f} ms/step, {ips:.0f} images/s")
 
+    if args.phase == "throughput":
+        m.close()
+        log(json.dumps({"phase": "throughput", "images_per_s": round(ips, 1), "ms_per_step": round(ms_step, 4)}))
+        return
     # ---- per-node device time at batch B (HIP events on the model stream)
     prof = m.profileNodes(B, args.profile_iters)
     infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
@@ -100,14 +146,14 @@ def main():
         achieved = d["bytes"] * B / t_dom / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    roof.update({"traffic": None, "kernel": d["kernel"], "node": d["desc"],
+    roof.update({"traffic": measured_traffic(d["desc"], B), "kernel": d["kernel"], "node": d["desc"],
                  "launch_ms": round(t_dom * 1e3, 4),
                  "flops_per_launch": d["flops"] * B, "bytes_per_launch": d["bytes"] * B})
     conv_frac = conv_f / (conv_t * 1e-3) / 1e12 / PEAK_FP16_TFLOPS if conv_t > 0 else 0.0
     m.close()
 
     # ---- batch-1 latency: synchronous runs (graph replay), mean wall time
-    m1 = ia.PlanModel(path, 0, 1)
+    m1 = ia.PlanModel(path, 0, 1, gflag)
     m1.setInput(x[:n_in], 1)
     for _ in range(max(args.warmup, 5)):
         m1.run(1)
@@ -160,6 +206,7 @@ def main():
         "config": {"workload": f"{args.model} 3x{args.imgsz}x{args.imgsz} batch {B}, one plan pass per step",
                    "batch": B, "imgsz": args.imgsz, "gflop_per_image": round(flops_img / 1e9, 3)},
         "latency_b1_ms": round(lat_ms, 4),
+        "launch": "eager" if args.no_graph else "hip_graph",
         "conv_mfma_frac": round(conv_frac, 4),
         "tflops_effective": round(flops_img * ips / 1e12, 2),
         "roofline": roof,

@@ -1,0 +1,113 @@
+// HipBackend: drop-in for infvino::ClBackend (include/infvino/ClBackend.hpp:29-53,
+// src/ClBackend.cpp:13-65 of the reference) on one MI355X.
+//   * constructed from the same ModelInfo (any type with a `plan` string member; its
+//     `device` string "GPU.<n>" picks the HIP device), or from a plan path;
+//   * infer(const float* input, size_t numel) -> std::vector<Tensor>: f32 NCHW in, the
+//     reference's truncating f32 -> f16 conversion (done on the device), fp16 compute,
+//     f32 Tensors out; numel must equal prod(inputDims()) (throws "input numel mismatch"
+//     otherwise), or a multiple B <= maxBatch of it, in which case the outputs carry B
+//     images along dim 0;
+//   * infer serialised by a mutex so Sessions can share one backend (ClBackend.cpp:33).
+#ifndef INFVINO_HIP_BACKEND_HPP_
+#define INFVINO_HIP_BACKEND_HPP_
+
+#include <chrono>
+#include <cstdlib>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "infvino_hip/HipPlanModel.hpp"
+#include "infvino_hip/Tensor.hpp"
+
+namespace infvino_hip
+{
+
+struct HipDeviceInfo
+{
+  std::string requested;  ///< the ModelInfo device string ("AUTO", "GPU", "GPU.1", ...)
+  std::string resolved;   ///< device actually used, e.g. "GPU.0"
+  std::string full_name;  ///< HIP device name
+  unsigned compute_units = 0;
+  unsigned clock_mhz = 0;
+};
+
+class HipBackend
+{
+public:
+  explicit HipBackend(const std::string & plan, int device = 0, int max_batch = 1, uint32_t flags = 0,
+                      const std::string & requested = "AUTO")
+  {
+    if (plan.empty())
+      throw std::runtime_error("HipBackend: ModelInfo.plan is empty. Generate it first with "
+                               "scripts/onnx2plan.py --onnx <model.onnx> --out-dir models");
+    model_ = std::make_unique<HipPlanModel>(plan, device, max_batch, flags);
+    input_dims_ = model_->inputDims();
+    for (size_t i = 0; i < model_->outputCount(); ++i) output_shapes_.push_back(model_->outputDims(i));
+    char name[256] = {0};
+    int cu = 0, mhz = 0;
+    check(ivh_device_info(device, name, sizeof name, &cu, &mhz));
+    device_.requested = requested;
+    device_.resolved = "GPU." + std::to_string(device);
+    device_.full_name = name;
+    device_.compute_units = static_cast<unsigned>(cu);
+    device_.clock_mhz = static_cast<unsigned>(mhz);
+  }
+
+  /** From a ModelInfo-like object: uses info.plan and info.device ("GPU.<n>" -> device n). */
+  template <class Info, class = decltype(std::declval<const Info &>().plan)>
+  explicit HipBackend(const Info & info, int max_batch = 1, uint32_t flags = 0)
+  : HipBackend(info.plan, deviceIndex(info.device), max_batch, flags, info.device)
+  {
+  }
+
+  const std::vector<int64_t> & inputDims() const { return input_dims_; }
+  const std::vector<std::vector<int64_t>> & outputShapes() const { return output_shapes_; }
+  const HipDeviceInfo & device() const { return device_; }
+  double lastInferMs() const { return last_infer_ms_; }
+  HipPlanModel & model() { return *model_; }
+
+  std::vector<Tensor> infer(const float * input_f32, size_t numel)
+  {
+    std::lock_guard<std::mutex> lock(mutex_);
+    const size_t per = model_->inputNumel();
+    if (numel == 0 || numel % per != 0 || numel / per > static_cast<size_t>(model_->maxBatch()))
+      throw std::runtime_error("HipBackend: input numel mismatch: got " + std::to_string(numel) +
+                               ", expected " + std::to_string(per));
+    const int batch = static_cast<int>(numel / per);
+    const auto t0 = std::chrono::steady_clock::now();
+    model_->setInputF32(input_f32, batch);
+    model_->run(batch);
+    last_infer_ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    std::vector<Tensor> outputs;
+    outputs.reserve(model_->outputCount());
+    for (size_t i = 0; i < model_->outputCount(); ++i) {
+      Tensor t;
+      t.shape = model_->outputDims(i);
+      if (batch > 1 && !t.shape.empty()) t.shape[0] *= batch;
+      t.data.resize(model_->outputNumel(i) * batch);
+      model_->readOutputF32(i, t.data.data(), batch);
+      outputs.push_back(std::move(t));
+    }
+    return outputs;
+  }
+
+private:
+  static int deviceIndex(const std::string & dev)
+  {
+    const auto p = dev.find('.');
+    return p == std::string::npos ? 0 : std::atoi(dev.c_str() + p + 1);
+  }
+
+  std::unique_ptr<HipPlanModel> model_;
+  std::vector<int64_t> input_dims_;
+  std::vector<std::vector<int64_t>> output_shapes_;
+  HipDeviceInfo device_;
+  double last_infer_ms_ = 0.0;
+  std::mutex mutex_;
+};
+
+}  // namespace infvino_hip
+
+#endif  // INFVINO_HIP_BACKEND_HPP_

@@ -24,6 +24,7 @@
  *   ivh_last_run_ms       PlanModel::lastRunMs / ClBackend::lastInferMs, PlanModel.hpp:176, ClBackend.hpp:47
  *   ivh_profile_nodes     PlanModel::profile() per-node GPU time, PlanModel.hpp:201-224
  *   ivh_node_info         PlanModel::PlanProfile::NodeRow (op, tag, signature), PlanModel.hpp:203-211
+ *   ivh_device_info       ClBackend::device() / describeDevice, ClBackend.hpp:46, include/infvino/Device.hpp
  * The batch argument is new: the reference runs one image per call (src/PlanModel.cpp:3561-3564
  * read C,H,W from the last three dims).  Here a call processes `batch` images stored back to
  * back (image stride = the plan's per-image numel); batch == 1 is the reference behaviour.
@@ -60,6 +61,8 @@ typedef struct ivh_model ivh_model;
 const char * ivh_last_error(void);
 int ivh_version(int * major, int * minor);
 int ivh_device_count(int * n);
+/* name / compute units / peak clock of a device (ClBackend::device(), src/Device.cpp) */
+int ivh_device_info(int device, char * name, size_t name_len, int * compute_units, int * clock_mhz);
 
 int ivh_create(const char * plan_path, int device, int max_batch, uint32_t flags, ivh_model ** out);
 int ivh_destroy(ivh_model * m);

@@ -39,6 +39,7 @@ SIGNATURES = {
     "ivh_last_error": (C.c_char_p, []),
     "ivh_version": (_i, [_ip, _ip]),
     "ivh_device_count": (_i, [_ip]),
+    "ivh_device_info": (_i, [_i, C.c_char_p, _sz, _ip, _ip]),
     "ivh_create": (_i, [C.c_char_p, _i, _i, _u32, C.POINTER(_vp)]),
     "ivh_destroy": (_i, [_vp]),
     "ivh_input_dims": (_i, [_vp, _i64p, _ip]),
@@ -90,6 +91,13 @@ def device_count() -> int:
     n = C.c_int(0)
     _check(lib().ivh_device_count(C.byref(n)))
     return n.value
+
+
+def device_info(device: int = 0) -> dict:
+    name = C.create_string_buffer(256)
+    cu, mhz = C.c_int(), C.c_int()
+    _check(lib().ivh_device_info(device, name, 256, C.byref(cu), C.byref(mhz)))
+    return {"name": name.value.decode(), "compute_units": cu.value, "clock_mhz": mhz.value}
 
 
 def _dims(fn, *args):

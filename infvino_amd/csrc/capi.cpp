@@ -78,6 +78,31 @@ int ivh_device_count(int * n)
   });
 }
 
+int ivh_device_info(int device, char * name, size_t name_len, int * compute_units, int * clock_mhz)
+{
+  return guard([&] {
+    auto chk = [](hipError_t e) {
+      if (e != hipSuccess) throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e));
+    };
+    int cu = 0, clk = 0;
+    chk(hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, device));
+    chk(hipDeviceGetAttribute(&clk, hipDeviceAttributeClockRate, device));
+    if (compute_units) *compute_units = cu;
+    if (clock_mhz) *clock_mhz = clk / 1000;
+    if (name && name_len) {
+      char buf[256] = {0};
+      chk(hipDeviceGetName(buf, sizeof buf, device));
+      if (!buf[0]) {
+        hipDeviceProp_t prop;
+        chk(hipGetDeviceProperties(&prop, device));
+        std::strncpy(buf, prop.gcnArchName, sizeof buf - 1);
+      }
+      std::strncpy(name, buf, name_len - 1);
+      name[name_len - 1] = 0;
+    }
+  });
+}
+
 int ivh_create(const char * plan_path, int device, int max_batch, uint32_t flags, ivh_model ** out)
 {
   return guard([&] {

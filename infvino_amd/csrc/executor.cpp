@@ -163,8 +163,8 @@ Model::~Model()
 {
   if (dry_) return;
   (void)hipSetDevice(device_);
-  for (auto & g : graphs_) (void)hipGraphExecDestroy(g.second);
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (auto & g : graphs_) (void)hipGraphExecDestroy(g.second);
   for (const auto & a : allocs_) (void)hipFree(reinterpret_cast<void *>(a.first));
   if (stream_) (void)hipStreamDestroy(stream_);
 }

@@ -101,3 +101,27 @@ def test_backend_f32_boundary(tmp_path):
     assert _model_ok(O.f2h(outs[0].data.ravel()), O.f2h(ref), "backend mbv3 b2")
     with pytest.raises(RuntimeError, match="numel mismatch"):
         be.infer(xf[:100])
+
+
+def test_cpp_backend_dropin(tmp_path):
+    """The C++ HipBackend / HipPlanModel (include/infvino_hip/) used as ClBackend is used:
+    f32 in, f32 Tensors out, batch 2, error messages; outputs vs the oracle."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "_build", "test_backend")
+    if not os.path.exists(exe):
+        pytest.skip("tests/cpp/_build/test_backend not built (__graft_entry__.build())")
+    path, _ = pw.mobilenetv3_small(str(tmp_path / "m"), seed=0)
+    bad = tmp_path / "bad.plan"
+    bad.write_text("input x 1 4\ntensor y 1 4\nnode ew_unary x y op=1 n=4\n")
+    out = tmp_path / "out.bin"
+    r = subprocess.run([exe, path, str(out), str(bad)], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "test_backend OK" in r.stdout
+    got = np.fromfile(out, np.float32)
+    p = O.Plan.load(path)
+    n = p.numel(p.input_name)
+    i = np.arange(2 * n, dtype=np.uint64)
+    xf = ((i * np.uint64(2654435761)) % np.uint64(1000)).astype(np.float32) / np.float32(1000.0)
+    ref = O.h2f(O.run_plan(p, O.f2h_trunc(xf), 2)[0].ravel())
+    assert _model_ok(O.f2h(got), O.f2h(ref), "C++ HipBackend mbv3 b2")

@@ -129,3 +129,16 @@ def test_rel_errors_definition():
     mean_rel, max_rel, max_abs, scale_rel = O.rel_errors(got, ref)
     assert np.isclose(mean_rel, 0.0125 / 1.875) and np.isclose(max_rel, 0.01)
     assert np.isclose(max_abs, 0.04) and np.isclose(scale_rel, 0.0125 / 4)
+
+
+def test_cpp_headers_compile(tmp_path):
+    """include/infvino_hip/*.hpp compile as a C++17 translation unit against include/ivh.h."""
+    import subprocess
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "infvino_hip/HipBackend.hpp"\n'
+                   'struct MI { std::string plan, device; };\n'
+                   'int main() { MI m{"x.plan", "GPU.0"}; (void)sizeof(infvino_hip::HipBackend); '
+                   'if (0) { infvino_hip::HipBackend b(m); } return 0; }\n')
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
