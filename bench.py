@@ -9,6 +9,8 @@ table goes to stderr.
   roofline       dominant kernel (largest device time per batch-64 step): algorithmic FLOPs
                  (or bytes) per launch / its mean launch time, HIP events on the model stream
   conv_mfma_frac all conv FLOPs of a step / conv device time / dense fp16 MFMA peak
+  conv_sweep     the conv operator sweep (stem, strided / stride-1 3x3, depthwise) at the
+                 same batch: per layer time, TFLOP/s, GB/s and fraction of its binding roof
   cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
                  workload on this host's cores -- a reported baseline, not a target
 """
@@ -48,6 +50,43 @@ def calibrate(ia, pw):
     log("[bench] calibration pass: 5 x (128 MiB read + 128 MiB write)")
 
 
+def conv_sweep(ia, pw, batch, iters):
+    """The conv operator sweep (stem, strided and stride-1 3x3, depthwise) at `batch`, each
+    conv measured in the layout it has inside a model: the stem reads the NCHW graph input,
+    every other conv sits between two ReLUs so its input and output are internal
+    (channels-last) tensors.  Per layer: HIP-event time of the conv node, algorithmic
+    TFLOP/s and GB/s, and the fraction of the roof that binds it (MFMA when its arithmetic
+    intensity is above the ridge, HBM otherwise)."""
+    ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    rows = []
+    for name, cin, cout, H, W, k, s, g, act in pw.CONV_SWEEP:
+        with tempfile.TemporaryDirectory() as d:
+            pb = pw.PlanBuilder(d, seed=0)
+            x = pb.input("x", [1, cin, H, W])
+            if not name.startswith("stem"):
+                x = pb.unary(x, pw.UN_RELU)
+            y = pb.unary(pb.conv(x, cout, k, s, groups=g, act=act), pw.UN_RELU)
+            pb.output(y)
+            m = ia.PlanModel(pb.write(), 0, batch, ia.IVH_FLAG_NO_GRAPH)
+            x0 = np.random.default_rng(0).random(m.inputNumel() * batch, dtype=np.float32)
+            m.setInput(x0.astype(np.float16).view(np.uint16), batch)
+            m.run(batch)
+            ci = next(i for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
+            inf = m.nodeInfo(ci)
+            t = float(m.profileNodes(batch, iters)[ci]) * 1e-3
+            m.close()
+        fl, by = inf["flops"] * batch, inf["bytes"] * batch
+        tf, gbs = fl / t / 1e12, by / t / 1e9
+        mfma = fl / by >= ridge
+        rows.append({"layer": name, "kernel": inf["kernel"], "us": round(t * 1e6, 2),
+                     "tflops": round(tf, 1), "gbs": round(gbs, 1),
+                     "bound": "mfma" if mfma else "hbm",
+                     "frac": round(tf / PEAK_FP16_TFLOPS if mfma else gbs / PEAK_HBM_GBS, 4)})
+        log(f"[sweep] {name:24s} b{batch} {inf['kernel']:12s} {t * 1e6:8.2f} us {tf:7.1f} TFLOP/s "
+            f"{gbs:7.1f} GB/s -> {rows[-1]['bound']} {rows[-1]['frac'] * 100:.1f}%")
+    return rows
+
+
 def measured_traffic(node_desc, batch):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
     summary (profiles/traffic_dominant_kernel.md), when it was measured on this node."""
@@ -76,9 +115,10 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=5)
     ap.add_argument("--cpu-images", type=int, default=-1, help="oracle sample size (-1: ~15 s worth)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the per-layer conv sweep")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch node by node instead of replaying the captured HIP graph")
-    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib"],
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
                          "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -92,6 +132,9 @@ def main():
 
     if args.phase == "calib":
         calibrate(ia, pw)
+        return
+    if args.phase == "sweep":
+        conv_sweep(ia, pw, args.batch, max(args.profile_iters, 10))
         return
     tmp = tempfile.TemporaryDirectory()
     path, flops_img = pw.MODELS[args.model](tmp.name, seed=0, imgsz=args.imgsz)
@@ -172,6 +215,8 @@ def main():
         log(f"  {prof1[i]:8.4f} ms  {inf1[i]['kernel']:12s} {inf1[i]['desc']}")
     m1.close()
 
+    sweep = None if args.no_sweep else conv_sweep(ia, pw, B, max(args.profile_iters, 10))
+
     # ---- CPU baseline: the oracle on a bounded sample of the same workload
     cpu = None
     if not args.no_cpu:
@@ -210,6 +255,7 @@ def main():
         "conv_mfma_frac": round(conv_frac, 4),
         "tflops_effective": round(flops_img * ips / 1e12, 2),
         "roofline": roof,
+        "conv_sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

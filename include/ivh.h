@@ -87,7 +87,8 @@ int ivh_read_tensor_f16(ivh_model * m, const char * name, uint16_t * host, int b
 int ivh_tensor_numel(const ivh_model * m, const char * name, size_t * numel);
 int ivh_last_run_ms(const ivh_model * m, double * ms);
 
-/* profiling: per-node device time (ms, mean over iters), HIP events on the model stream */
+/* profiling: per-node device time (ms): each node run `iters` times back to back between two
+   HIP events on the model stream, mean per run; a full pass afterwards restores all tensors */
 int ivh_node_count(ivh_model * m, int * n);
 int ivh_profile_nodes(ivh_model * m, int batch, int iters, double * ms, int cap);
 /* node i: op, kernel family and shape text; algorithmic FLOPs and fp16 bytes per image */

@@ -235,7 +235,7 @@ int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel,
       dst[n - 1] = 0;
     };
     cp(op, op_len, s.op);
-    cp(kernel, kernel_len, s.kernel);
+    cp(kernel, kernel_len, M(m).nodeKernel(i));
     cp(desc, desc_len, s.desc);
     if (flops) *flops = s.flops;
     if (bytes) *bytes = s.bytes;

@@ -71,6 +71,8 @@ class Model {
   std::vector<double> profileNodes(int batch, int iters);
   int nodeCount() const { return (int)nodes_.size(); }
   const NodeStat & nodeStat(int i) const { return stats_.at(i); }
+  // kernel family node i launches at the largest batch (conv_halo / conv_igemm / conv_stem ...)
+  std::string nodeKernel(int i);
   size_t arenaBytes(int batch) const { return (size_t)arena_elems1_ * batch * 2; }
   size_t weightBytes() const { return weight_bytes_; }
 

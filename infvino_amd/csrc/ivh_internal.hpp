@@ -49,9 +49,11 @@ struct ConvParams {
   float * ws = nullptr;
   // stem MFMA path: w holds fp16 [ceil(Cout/16)*16][32] (k = ci*9 + ky*3 + kx, zero padded)
   int stem_mfma = 0;
-  // 3x3 stride-1 halo kernel: 16 -> 8x16 output tiles, 8 -> 16x8 tiles, 0 -> im2col kernel;
-  // w is then packed [co][32-channel chunk][tap][32]
+  // 3x3 stride-1 pad-1 LDS-patch kernel (conv_halo.hip): halo = tile config + 1 (0: not
+  // used), th x tw = output tile of the tall batch image; w is then packed
+  // [co][chunk][tap][ck] with ck = halo_ck(Cin) and halo_taps(ck) taps per chunk
   int halo = 0;
+  int th = 0, tw = 0;
 };
 
 // Generic small-op descriptor (elementwise / pooling / data movement).

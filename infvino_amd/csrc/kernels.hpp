@@ -12,7 +12,16 @@ constexpr int kIgemmBK = 32;               // K tile (packed weight rows are a m
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
 void launch_conv_igemm(const ConvParams & p, hipStream_t s);
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
-int halo_tw(int Ho, int Wo);                    // 16: 8x16 tiles, 8: 16x8 tiles
+
+// conv_halo.hip: 3x3 stride-1 pad-1 convs with an LDS input patch
+int halo_ck(int cin);       // input-channel chunk of the weight packing (16 / 32 / 64)
+int halo_taps(int ck);      // taps per chunk in the packing (9, or 10 with a zero tap)
+// tile config (cfg) and output tile th x tw for a layer at a batch size; false: not eligible
+bool halo_plan(int cin, int cout, int H, int W, int batch, int * cfg, int * th, int * tw);
+long halo_grid_x(const ConvParams & p);
+int halo_bn(int cfg);
+int halo_pmax(int cfg);
+void launch_conv_halo(const ConvParams & p, hipStream_t s);
 
 // kernels_misc.hip
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout
