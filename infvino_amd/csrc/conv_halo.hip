@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
 #pragma unroll
     for (int i = 0; i < P_IT; ++i) {
       const int e = tid + i * 256;
-      if (i + 1 < P_IT || e < PP * CQ) {
+      if (e < PP * CQ) {
         h8 v = rp[i];
         if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
         *reinterpret_cast<h8 *>(Ps + (e / CQ) * CKP + q8) = v;
@@ -241,40 +241,61 @@ constexpr HaloCfgDesc kHaloCfg[8] = {
 };
 }  // namespace
 
-int halo_ck(int cin) { return cin <= 16 ? 16 : (cin <= 32 ? 32 : 64); }
+// Chunk per config (measured on MI355X): the BM 128 x BN 128 config runs 64-channel steps
+// (two work-groups per CU fit either way); every other config uses 32-channel chunks, which
+// keep the BM 256 configs at two work-groups per CU.
+int halo_cfg_ck(int cfg, int cin) { return cin <= 16 ? 16 : (cin <= 32 || cfg != 7 ? 32 : 64); }
 int halo_taps(int ck) { return ck == 16 ? 10 : 9; }
 
+// Best tile of one config for a layer: fewest pixel slots plus patch fill; false if none.
+static bool halo_tile(int cfg, int cout, int H, int W, int batch, long * wgs, int * th, int * tw)
+{
+  const HaloCfgDesc & d = kHaloCfg[cfg];
+  const long Htot = (long)batch * (H + 1) - 1;
+  double best = 1e30;
+  for (int w = 1; w <= W && w <= d.bm; ++w) {
+    int h = d.bm / w;
+    h = (int)std::min<long>(h, Htot);
+    h = std::min(h, d.pmax / (w + 2) - 2);
+    if (h < 1) continue;
+    const long ty = (Htot + h - 1) / h, tx = (W + w - 1) / w;
+    const int hh = (int)((Htot + ty - 1) / ty), ww = (int)((W + tx - 1) / tx);  // balanced
+    const double cost = (double)(ty * tx) * (d.bm + 0.3 * (hh + 2) * (ww + 2));
+    if (cost < best) {
+      best = cost;
+      *th = hh;
+      *tw = ww;
+      *wgs = ty * tx * ((cout + d.bn - 1) / d.bn);
+    }
+  }
+  return best < 1e30;
+}
+
+// Config choice (from MI355X measurements of the conv sweep shapes at batch 64): wide
+// layers take BM 256 pixel tiles when that grid still gives 1.5 work-groups per CU, else
+// BM 128; Cout <= 64 takes BM 128 (BN 64); Cout <= 32 takes BM 256.  Small grids fall back
+// to the other BM.
 bool halo_plan(int cin, int cout, int H, int W, int batch, int * cfg, int * th, int * tw)
 {
   (void)cin;
   // tall-image rows and widths stay below 2^22 (the kernel's float-reciprocal divisions)
   if (H < 2 || W < 2 || (long)batch * (H + 1) >= (1L << 22) || W >= (1 << 22)) return false;
   const int bnc = cout <= 16 ? 0 : (cout <= 32 ? 1 : (cout <= 64 ? 2 : 3));
-  const long Htot = (long)batch * (H + 1) - 1;
-  double best = 1e30;
-  int bc = -1, bh = 0, bw = 0;
-  for (int big = 0; big < 2; ++big) {
-    const int ci = big ? bnc : 4 + bnc;
-    const HaloCfgDesc & d = kHaloCfg[ci];
-    for (int w = 1; w <= W && w <= d.bm; ++w) {
-      int h = d.bm / w;
-      h = (int)std::min<long>(h, Htot);
-      h = std::min(h, d.pmax / (w + 2) - 2);
-      if (h < 1) continue;
-      const long ty = (Htot + h - 1) / h, tx = (W + w - 1) / w;
-      const int hh = (int)((Htot + ty - 1) / ty), ww = (int)((W + tx - 1) / tx);  // balanced
-      const long tiles = ty * tx;
-      const long wgs = tiles * ((cout + d.bn - 1) / d.bn);
-      // cost: MFMA slots + patch fill, and a penalty when the grid cannot fill 256 CUs
-      double cost = (double)tiles * (d.bm + 0.3 * (hh + 2) * (ww + 2));
-      if (wgs < 256) cost *= 256.0 / (double)wgs;
-      if (cost < best) { best = cost; bc = ci; bh = hh; bw = ww; }
-    }
-  }
-  if (bc < 0) return false;
-  *cfg = bc;
-  *th = bh;
-  *tw = bw;
+  const int big = bnc, small = 4 + bnc;
+  long wb = 0, ws = 0;
+  int hb = 0, hs = 0, tb = 0, ts = 0;
+  const bool okb = halo_tile(big, cout, H, W, batch, &wb, &hb, &tb);
+  const bool oks = halo_tile(small, cout, H, W, batch, &ws, &hs, &ts);
+  int c;
+  if (bnc == 3) c = (okb && wb >= 384) ? big : small;
+  else if (bnc == 2) c = small;
+  else c = (okb && wb >= 256) ? big : small;
+  if (c == big && !okb) c = small;
+  if (c == small && !oks) c = big;
+  if ((c == big && !okb) || (c == small && !oks)) return false;
+  *cfg = c;
+  *th = c == big ? hb : hs;
+  *tw = c == big ? tb : ts;
   return true;
 }
 
@@ -292,7 +313,7 @@ static void launch_hc(const ConvParams & p, hipStream_t s)
 {
   using T = TileShape<MB, WGM, WGN, TM, TN>;
   dim3 grid((unsigned)halo_grid_x(p), (unsigned)((p.Cout + T::BN - 1) / T::BN), 1);
-  const int ck = halo_ck(p.Cin);
+  const int ck = p.ck;
   if (ck == 16) hipLaunchKernelGGL((conv3x3s1_kernel<MB, WGM, WGN, TM, TN, 16, PMAX>), grid, dim3(256), 0, s, p);
   else if (ck == 32) hipLaunchKernelGGL((conv3x3s1_kernel<MB, WGM, WGN, TM, TN, 32, PMAX>), grid, dim3(256), 0, s, p);
   else hipLaunchKernelGGL((conv3x3s1_kernel<MB, WGM, WGN, TM, TN, 64, PMAX>), grid, dim3(256), 0, s, p);

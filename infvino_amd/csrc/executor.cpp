@@ -746,17 +746,21 @@ void Model::uploadWeights()
       const int S = is3 ? n.i("stride", 1) : n.i("S", 1);
       const int pad = is3 ? n.i("pad", 1) : n.i("P", 1);
       if (K == 3 && S == 1 && pad == 1 && x_nhwc && !(flags_ & IVH_FLAG_NO_HALO)) {
-        const int ck = halo_ck(cin_g), taps = halo_taps(ck);
-        const int nch = (cin_g + ck - 1) / ck;
-        const int kh = nch * taps * ck;
-        std::vector<uint16_t> Q((size_t)rows * kh, 0);
-        for (int co = 0; co < Cout; ++co)
-          for (int ci = 0; ci < cin_g; ++ci)
-            for (int t = 0; t < 9; ++t)
-              Q[(size_t)co * kh + ((ci / ck) * taps + t) * ck + (ci % ck)] = W[((size_t)co * cin_g + ci) * 9 + t];
-        pk.w_halo = upload(Q.data(), Q.size() * 2);
-        pk.kpad_halo = kh;
-        pk.halo = 1;
+        // every chunk size some tile config may use for this Cin
+        for (int cfg : {0, 7}) {
+          const int ck = halo_cfg_ck(cfg, cin_g), taps = halo_taps(ck), ci = ck == 16 ? 0 : (ck == 32 ? 1 : 2);
+          if (pk.w_halo[ci]) continue;
+          const int nch = (cin_g + ck - 1) / ck;
+          const int kh = nch * taps * ck;
+          std::vector<uint16_t> Q((size_t)rows * kh, 0);
+          for (int co = 0; co < Cout; ++co)
+            for (int c = 0; c < cin_g; ++c)
+              for (int t = 0; t < 9; ++t)
+                Q[(size_t)co * kh + ((c / ck) * taps + t) * ck + (c % ck)] = W[((size_t)co * cin_g + c) * 9 + t];
+          pk.w_halo[ci] = upload(Q.data(), Q.size() * 2);
+          pk.kpad_halo[ci] = kh;
+        }
+        pk.halo = true;
       }
     } else if (kind == 1 && G == 1 && cin_g <= 3 && K == 3 && Cout <= 32) {
       // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened
@@ -903,13 +907,16 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
         q.tw = tw;
         const long wgs = halo_grid_x(q) * ((p.Cout + halo_bn(hc) - 1) / halo_bn(hc));
         if (wgs >= 160 || p.ksplit == 1) {
+          const int ck = halo_cfg_ck(hc, p.Cin), ci = ck == 16 ? 0 : (ck == 32 ? 1 : 2);
+          if (!pk.w_halo[ci]) fail("halo packing missing for chunk size " + std::to_string(ck));
           p.halo = hc + 1;
           p.th = th;
           p.tw = tw;
+          p.ck = ck;
           p.ksplit = 1;
           p.ws = nullptr;
-          p.w = static_cast<const __half *>(pk.w_halo);
-          p.kpad = pk.kpad_halo;
+          p.w = static_cast<const __half *>(pk.w_halo[ci]);
+          p.kpad = pk.kpad_halo[ci];
         }
       }
       if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) ||
@@ -1223,7 +1230,8 @@ void Model::validate(const Launch & l) const
       const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
       if (p.halo) {
-        const int cfg = p.halo - 1, ck = halo_ck(p.Cin);
+        const int cfg = p.halo - 1, ck = p.ck;
+        if (cfg < 0 || cfg > 7 || ck != halo_cfg_ck(cfg, p.Cin)) throw std::runtime_error("halo chunk size");
         if (p.K != 3 || p.S != 1 || p.P != 1 || p.ksplit != 1 || cfg < 0 || cfg > 7 || p.th < 1 || p.tw < 1 ||
             p.Ho != p.H || p.Wo != p.W || (p.th + 2) * (p.tw + 2) > halo_pmax(cfg) ||
             p.th * p.tw > (cfg < 4 ? 256 : 128) || (p.Cout + halo_bn(cfg) - 1) / halo_bn(cfg) * halo_bn(cfg) > rows)

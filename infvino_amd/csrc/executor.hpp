@@ -124,9 +124,11 @@ class Model {
     int kind = 0;
     int kpad = 0, cin8 = 0;
     bool stem = false;  // direct conv with Cin <= 3, 3x3: fp16 MFMA stem packing
-    void * w_halo = nullptr;  // 3x3 s1: [co][chunk][tap][32] packing for the halo kernel
-    int kpad_halo = 0;
-    int halo = 0;             // tile choice (16 / 8), 0 = not eligible
+    // 3x3 s1 pad 1: [co][chunk][tap][ck] packings for the LDS-patch kernel, by chunk size
+    // ck = 16 / 32 / 64 (index 0 / 1 / 2); null where not packed
+    void * w_halo[3] = {nullptr, nullptr, nullptr};
+    int kpad_halo[3] = {0, 0, 0};
+    bool halo = false;
   };
   std::vector<Packed> packed_;              // per node
   float * ws_ = nullptr;                    // split-K partials

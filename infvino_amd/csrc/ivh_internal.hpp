@@ -51,9 +51,10 @@ struct ConvParams {
   int stem_mfma = 0;
   // 3x3 stride-1 pad-1 LDS-patch kernel (conv_halo.hip): halo = tile config + 1 (0: not
   // used), th x tw = output tile of the tall batch image; w is then packed
-  // [co][chunk][tap][ck] with ck = halo_ck(Cin) and halo_taps(ck) taps per chunk
+  // [co][chunk][tap][ck] with ck = halo_cfg_ck(cfg, Cin) and halo_taps(ck) taps per chunk
   int halo = 0;
   int th = 0, tw = 0;
+  int ck = 0;  // input-channel chunk of the halo weight packing (16 / 32 / 64)
 };
 
 // Generic small-op descriptor (elementwise / pooling / data movement).

@@ -14,8 +14,8 @@ void launch_conv_igemm(const ConvParams & p, hipStream_t s);
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
 
 // conv_halo.hip: 3x3 stride-1 pad-1 convs with an LDS input patch
-int halo_ck(int cin);       // input-channel chunk of the weight packing (16 / 32 / 64)
-int halo_taps(int ck);      // taps per chunk in the packing (9, or 10 with a zero tap)
+int halo_cfg_ck(int cfg, int cin);  // input-channel chunk a tile config uses (16 / 32 / 64)
+int halo_taps(int ck);               // taps per chunk in the packing (9, or 10 with a zero tap)
 // tile config (cfg) and output tile th x tw for a layer at a batch size; false: not eligible
 bool halo_plan(int cin, int cout, int H, int W, int batch, int * cfg, int * th, int * tw);
 long halo_grid_x(const ConvParams & p);
