@@ -763,11 +763,19 @@ void Model::uploadWeights()
         pk.halo = true;
       }
     } else if (kind == 1 && G == 1 && cin_g <= 3 && K == 3 && Cout <= 32) {
-      // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened
+      // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened;
+      // for Cout <= 16 followed by the row-tiled kernel's [16][64] with k = tap*4 + ci
       const int rows = (Cout + 15) / 16 * 16;
-      std::vector<uint16_t> P((size_t)rows * 32, 0);
+      std::vector<uint16_t> P((size_t)rows * 32 + 16 * 64, 0);
       for (int co = 0; co < Cout; ++co)
         for (int k = 0; k < cin_g * 9; ++k) P[(size_t)co * 32 + k] = W[(size_t)co * cin_g * 9 + k];
+      if (Cout <= 16) {
+        for (int co = 0; co < Cout; ++co)
+          for (int ci = 0; ci < cin_g; ++ci)
+            for (int t = 0; t < 9; ++t)
+              P[(size_t)rows * 32 + co * 64 + t * 4 + ci] = W[((size_t)co * cin_g + ci) * 9 + t];
+        pk.stem_w2 = rows * 32;
+      }
       pk.w = upload(P.data(), P.size() * 2);
       pk.stem = true;
     } else if (kind == 1) {
@@ -926,6 +934,7 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     } else if (pk.kind == 1) {
       L.kind = Launch::kDirect;
       p.stem_mfma = pk.stem ? 1 : 0;
+      if (pk.stem && pk.stem_w2 > 0) p.w2 = static_cast<const __half *>(pk.w) + pk.stem_w2;
     } else {
       L.kind = Launch::kDw;
     }
@@ -1250,6 +1259,11 @@ void Model::validate(const Launch & l) const
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
       check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");
       if (p.Cin * 9 > 32 || p.Cout > 32) throw std::runtime_error("stem geometry");
+      if (stem_rows_supported(p)) {
+        check(p.w2, 0, 16 * 64 - 1, 2, "stem rows w");
+        // each staged row reads W pixels of every channel plane; outputs cover Ho x Wo x Cout
+        check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem rows x");
+      }
     } else if (l.kind == Launch::kDirect) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "direct x");
       check(p.w, 0, (long)p.Cin * p.K * p.K * (p.Cout / p.G) + 16 - 1, 4, "direct w");

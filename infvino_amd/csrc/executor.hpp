@@ -124,6 +124,7 @@ class Model {
     int kind = 0;
     int kpad = 0, cin8 = 0;
     bool stem = false;  // direct conv with Cin <= 3, 3x3: fp16 MFMA stem packing
+    long stem_w2 = 0;   // element offset of the row-tiled stem packing in w (0: none)
     // 3x3 s1 pad 1: [co][chunk][tap][ck] packings for the LDS-patch kernel, by chunk size
     // ck = 16 / 32 / 64 (index 0 / 1 / 2); null where not packed
     void * w_halo[3] = {nullptr, nullptr, nullptr};

@@ -47,8 +47,10 @@ struct ConvParams {
   // second kernel reduces them in fixed order and applies the epilogue
   int ksplit = 1;
   float * ws = nullptr;
-  // stem MFMA path: w holds fp16 [ceil(Cout/16)*16][32] (k = ci*9 + ky*3 + kx, zero padded)
+  // stem MFMA path: w holds fp16 [ceil(Cout/16)*16][32] (k = ci*9 + ky*3 + kx, zero padded);
+  // w2 (Cout <= 16) the row-tiled kernel's fp16 [16][64] (k = tap*4 + ci, zero padded)
   int stem_mfma = 0;
+  const __half * w2 = nullptr;
   // 3x3 stride-1 pad-1 LDS-patch kernel (conv_halo.hip): halo = tile config + 1 (0: not
   // used), th x tw = output tile of the tall batch image; w is then packed
   // [co][chunk][tap][ck] with ck = halo_cfg_ck(cfg, Cin) and halo_taps(ck) taps per chunk

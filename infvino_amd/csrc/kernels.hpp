@@ -27,6 +27,7 @@ void launch_conv_halo(const ConvParams & p, hipStream_t s);
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout
 void launch_dwconv(const ConvParams & p, hipStream_t s);        // depthwise, any layout
 bool dwconv_vectorizable(const ConvParams & p);
+bool stem_rows_supported(const ConvParams & p);  // the row-tiled stem kernel applies
 
 enum SmallOp : int {
   kEwSame = 0,     // y = op(a, b), same geometry; b.img == 0 && b.cs == 0 -> scalar

@@ -2,26 +2,12 @@
 // depthwise conv, the small ops of kernels/ops.cl, and the boundary conversions.
 // None of these use MFMA; they are written for coalesced HBM access with batch B as an
 // outer grid axis.  Element addressing goes through ivh::View (NCHW or NHWC, strided).
-#include "ivh_internal.hpp"
+#include "conv_common.hpp"
 #include "kernels.hpp"
 
 #include <initializer_list>
 
 namespace ivh {
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ float actf(float v, int act)
-{
-  switch (act) {
-  case kActSiLU: return v / (1.0f + __expf(-v));
-  case kActReLU: return fmaxf(v, 0.0f);
-  case kActHSwish: return v * fminf(fmaxf(v + 3.0f, 0.0f), 6.0f) / 6.0f;
-  case kActHSigmoid: return fminf(fmaxf(v + 3.0f, 0.0f), 6.0f) / 6.0f;
-  case kActSigmoid: return 1.0f / (1.0f + __expf(-v));
-  default: return v;
-  }
-}
 
 __device__ __forceinline__ long vidx(const View & v, int b, int c, long p)
 {
@@ -82,7 +68,7 @@ __global__ void __launch_bounds__(256) conv_direct_kernel(const ConvParams p)
   for (int j = 0; j < COB; ++j) {
     const int co = g * cout_g + col + j;
     float v = acc[j] + ((p.bias && col + j < cout_g) ? p.bias[co] : 0.0f);
-    v = actf(v, p.act);
+    v = act_f(v, p.act);
     if (p.r.ptr && col + j < cout_g) v += vld(p.r, b, co, hw);
     out[j] = v;
   }
@@ -163,7 +149,7 @@ __global__ void __launch_bounds__(256) conv_stem_mfma_kernel(const ConvParams p)
       for (int v = 0; v < 4; ++v) {
         const int co = co0 + v;
         float x = acc[v] + (co < p.Cout && p.bias ? p.bias[co] : 0.0f);
-        x = actf(x, p.act);
+        x = act_f(x, p.act);
         if (p.r.ptr && co < p.Cout) x += vld(p.r, b, co, pix);
         o[v] = x;
       }
@@ -181,6 +167,135 @@ __global__ void __launch_bounds__(256) conv_stem_mfma_kernel(const ConvParams p)
   }
 }
 
+// Row-tiled stem for the common case (kernels/conv_cin3.cl:67-118 semantics): 3x3 stride 2
+// pad 1, Cin <= 3, Cout <= 16, planar NCHW input, channels-last output, no residual.  A
+// work-group owns TR output rows of one image.  It stages the 2*TR+1 input rows it needs in
+// LDS as [row][col][4] (channels interleaved, 4th slot zero; two zero columns on each side
+// for the padding), loading each channel plane with 16-byte coalesced loads.  Each wave then
+// takes 16-pixel blocks: K = 9 taps x 4 channel slots (36, two 16x16x32 MFMAs: taps 0-7 and
+// tap 8), B fragments are two 8-byte LDS reads per lane, weights ([16][64], k = tap*4 + ci)
+// stay in registers, and the D layout gives each lane 4 consecutive channels of one pixel,
+// so a block is 16 pixels x 32 bytes written contiguously.
+template <int TR, int UIT, int ACT>
+__global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
+{
+  extern __shared__ __attribute__((aligned(16))) _Float16 srow[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.y, oy0 = blockIdx.x * TR;
+  const int W = p.W, LW = W + 4;               // LDS row: 2 pad columns each side
+  const int G = W >> 3;                        // 8-pixel column groups per input row
+  const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img;
+  // zero the pad columns of every staged row
+  for (int e = tid; e < (2 * TR + 1) * 4; e += 256) {
+    const int lr = e >> 2, c = e & 3;
+    const int col = c < 2 ? c : W + c;
+    *reinterpret_cast<h4s *>(srow + ((long)lr * LW + col) * 4) = h4s{};
+  }
+  // every load of this thread is issued before the first LDS store (UIT units of three
+  // 16-byte channel loads; the host keeps (2*TR+1)*W/8 <= 256*UIT)
+  h8s c[UIT][3];
+  int dsto[UIT];
+#pragma unroll
+  for (int i = 0; i < UIT; ++i) {
+    const int u = tid + 256 * i;
+    const int lr = u / G, g = u - lr * G;
+    const int iy = 2 * oy0 - 1 + lr;
+    dsto[i] = u < (2 * TR + 1) * G ? (lr * LW + 8 * g + 2) * 4 : -1;
+    const bool ok = dsto[i] >= 0 && iy >= 0 && iy < p.H;
+#pragma unroll
+    for (int ci = 0; ci < 3; ++ci)
+      c[i][ci] = (ok && ci < p.Cin) ? *reinterpret_cast<const h8s *>(xb + (long)ci * p.x.cs + (long)iy * W + 8 * g) : h8s{};
+  }
+#pragma unroll
+  for (int i = 0; i < UIT; ++i) {
+    if (dsto[i] < 0) continue;
+    _Float16 * dst = srow + dsto[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h8s v;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        v[4 * h + 0] = c[i][0][2 * j + h];
+        v[4 * h + 1] = c[i][1][2 * j + h];
+        v[4 * h + 2] = c[i][2][2 * j + h];
+        v[4 * h + 3] = (_Float16)0.0f;
+      }
+      *reinterpret_cast<h8s *>(dst + 8 * j) = v;
+    }
+  }
+  __syncthreads();
+
+  const int co = lane & 15, q = lane >> 4;
+  const _Float16 * W4 = reinterpret_cast<const _Float16 *>(p.w2);
+  const h8s a1 = *reinterpret_cast<const h8s *>(W4 + co * 64 + 8 * q);
+  const h8s a2 = *reinterpret_cast<const h8s *>(W4 + co * 64 + 32 + 8 * q);
+  float bias[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) bias[v] = (p.bias && 4 * q + v < p.Cout) ? p.bias[4 * q + v] : 0.0f;
+  const int CB = (p.Wo + 15) >> 4;
+  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img;
+  auto tap_ld = [&](int r, int ox, int t) {
+    const int ky = t / 3, kx = t - 3 * ky;
+    return *reinterpret_cast<const h4s *>(srow + ((long)(2 * r + ky) * LW + 2 * ox + kx + 1) * 4);
+  };
+  // four blocks per pass: all LDS fragment reads first, then the MFMAs and the stores
+  const int nblk = TR * CB;
+  for (int base = wave; base < nblk; base += 16) {
+    h8s b1[4], b2[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int blk = base + 4 * k < nblk ? base + 4 * k : base;
+      const int r = blk / CB, cb = blk - r * CB;
+      const int ox = cb * 16 + (lane & 15);
+      const int oxc = ox < p.Wo ? ox : p.Wo - 1;
+      const h4s t0 = tap_ld(r, oxc, 2 * q), t1 = tap_ld(r, oxc, 2 * q + 1);
+      const h4s t8 = q == 0 ? tap_ld(r, oxc, 8) : h4s{};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b1[k][e] = t0[e];
+        b1[k][4 + e] = t1[e];
+        b2[k][e] = t8[e];
+        b2[k][4 + e] = (_Float16)0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int blk = base + 4 * k;
+      f4s acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1[k], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b2[k], acc, 0, 0, 0);
+      if (blk >= nblk) continue;
+      const int r = blk / CB, cb = blk - r * CB;
+      const int ox = cb * 16 + (lane & 15), oy = oy0 + r;
+      if (oy >= p.Ho || ox >= p.Wo) continue;
+      _Float16 * yp = yb + ((long)oy * p.Wo + ox) * p.y.cs + 4 * q;
+      if (4 * q + 4 <= p.Cout) {
+        h4s hv;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) hv[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
+        *reinterpret_cast<h4s *>(yp) = hv;
+      } else {
+        for (int v = 0; v < 4 && 4 * q + v < p.Cout; ++v) yp[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
+      }
+    }
+  }
+}
+
+constexpr int kStemTR = 4, kStemUIT = 4;
+
+// LDS bytes of the row-tiled stem for an input width
+static long stem_rows_lds(int W) { return (long)(2 * kStemTR + 1) * (W + 4) * 8; }
+
+bool stem_rows_supported(const ConvParams & p)
+{
+  auto al = [](const void * ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0; };
+  return p.stem_mfma && p.w2 && p.K == 3 && p.S == 2 && p.P == 1 && p.G == 1 && p.Cin >= 1 && p.Cin <= 3 &&
+         p.Cout <= 16 && !p.r.ptr && p.x.layout == kNCHW && p.y.layout == kNHWC && (p.W % 8) == 0 &&
+         (p.x.cs % 8) == 0 && (p.x.img % 8) == 0 && al(p.x.ptr, 16) && (p.y.cs % 4) == 0 && (p.y.img % 4) == 0 &&
+         al(p.y.ptr, 8) && p.Ho == (p.H - 1) / 2 + 1 && p.Wo == (p.W - 1) / 2 + 1 && stem_rows_lds(p.W) <= 65536 &&
+         (2 * kStemTR + 1) * (p.W / 8) <= 256 * kStemUIT;
+}
+
 bool stem_supported(const ConvParams & p)
 {
   return p.K == 3 && p.G == 1 && p.Cin >= 1 && p.Cin <= 3 && p.Cout <= 32 && p.stem_mfma;
@@ -188,6 +303,19 @@ bool stem_supported(const ConvParams & p)
 
 void launch_conv_direct(const ConvParams & p, hipStream_t s)
 {
+  if (stem_rows_supported(p)) {
+    const dim3 grid((unsigned)((p.Ho + kStemTR - 1) / kStemTR), (unsigned)p.batch);
+    const size_t lds = (size_t)stem_rows_lds(p.W);
+    switch (p.act) {
+    case kActSiLU: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActSiLU>), grid, dim3(256), lds, s, p); break;
+    case kActReLU: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActReLU>), grid, dim3(256), lds, s, p); break;
+    case kActHSwish: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActHSwish>), grid, dim3(256), lds, s, p); break;
+    case kActHSigmoid: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActHSigmoid>), grid, dim3(256), lds, s, p); break;
+    case kActSigmoid: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActSigmoid>), grid, dim3(256), lds, s, p); break;
+    default: hipLaunchKernelGGL((conv_stem_rows_kernel<kStemTR, kStemUIT, kActNone>), grid, dim3(256), lds, s, p); break;
+    }
+    return;
+  }
   if (stem_supported(p)) {
     const dim3 grid(nblk((long)p.Ho * p.Wo, 256), (unsigned)p.batch);
     const bool nchw = p.x.layout == kNCHW;
@@ -260,7 +388,7 @@ __global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float v = acc[e] + (p.bias ? p.bias[c + e] : 0.0f);
-    v = actf(v, p.act);
+    v = act_f(v, p.act);
     if (p.r.ptr) v += vld(p.r, b, c + e, hw);
     out[e] = (_Float16)v;
   }
@@ -288,7 +416,7 @@ __global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p)
       acc += vld(p.x, b, c, (long)iy * p.W + ix) * W[(ky * p.K + kx) * p.Cin + c];
     }
   }
-  float v = actf(acc + (p.bias ? p.bias[c] : 0.0f), p.act);
+  float v = act_f(acc + (p.bias ? p.bias[c] : 0.0f), p.act);
   if (p.r.ptr) v += vld(p.r, b, c, hw);
   vst(p.y, b, c, hw, v);
 }
@@ -357,7 +485,7 @@ __global__ void ew_unary_kernel(const SmallParams q)  // ew_unary (ops.cl:50-63)
   if (i >= n) return;
   int c; long p;
   cp_of(q, i, c, p);
-  vst(q.y, b, c, p, actf(vld(q.a, b, c, p), q.op));
+  vst(q.y, b, c, p, act_f(vld(q.a, b, c, p), q.op));
 }
 
 __global__ void copy_kernel(const SmallParams q)  // copy_c / concat part / layout change
@@ -594,7 +722,7 @@ __global__ void __launch_bounds__(256) ew_vec8_kernel(const SmallParams q, int m
   } else if (mode == 2) {
     const h8 x = ld8(q.a.ptr, pa);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = (_Float16)actf((float)x[e], q.op);
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)act_f((float)x[e], q.op);
   } else {
     const _Float16 * ap = reinterpret_cast<const _Float16 *>(q.a.ptr);
     const _Float16 * bp = reinterpret_cast<const _Float16 *>(q.b.ptr);
