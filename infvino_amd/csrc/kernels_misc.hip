@@ -167,6 +167,60 @@ __global__ void __launch_bounds__(256) conv_stem_mfma_kernel(const ConvParams p)
   }
 }
 
+// 1x1 conv with few output channels on planar (NCHW) input and output -- the DFL
+// projection of the pose head (16 bins -> 1), conv_general.cl:7-48 semantics: one lane =
+// 8 consecutive pixels x all Cout (<= 8), 16-byte loads per input channel, fp32 weights
+// [Cin][Cout] read uniformly, fp32 accumulation.
+template <int COUT>
+__global__ void __launch_bounds__(256) conv1x1_nchw8_kernel(const ConvParams p)
+{
+  const int HW = p.H * p.W, P8 = HW >> 3;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (t >= P8) return;
+  const int p0 = t * 8;
+  const float * W = reinterpret_cast<const float *>(p.w);
+  float acc[COUT][8];
+#pragma unroll
+  for (int c = 0; c < COUT; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[c][e] = 0.0f;
+  const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img + p0;
+  for (int ci = 0; ci < p.Cin; ++ci) {
+    const h8 xv = *reinterpret_cast<const h8 *>(xb + (long)ci * p.x.cs);
+#pragma unroll
+    for (int c = 0; c < COUT; ++c) {
+      const float w = c < p.Cout ? W[ci * p.Cout + c] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[c][e] += w * (float)xv[e];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < COUT; ++c) {
+    if (c >= p.Cout) break;
+    const float bv = p.bias ? p.bias[c] : 0.0f;
+    h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (_Float16)act_f(acc[c][e] + bv, p.act);
+    if (p.r.ptr) {
+      const h8 rv = *reinterpret_cast<const h8 *>(reinterpret_cast<const _Float16 *>(p.r.ptr) + (long)b * p.r.img +
+                                                  (long)c * p.r.cs + p0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] + (float)rv[e]);
+    }
+    *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + (long)c * p.y.cs + p0) = v;
+  }
+}
+
+bool conv1x1_nchw8_ok(const ConvParams & p)
+{
+  auto a8 = [](const View & v) {
+    return v.layout == kNCHW && ((v.cs | v.img | (long)(reinterpret_cast<uintptr_t>(v.ptr) >> 1)) & 7) == 0;
+  };
+  return p.K == 1 && p.S == 1 && p.P == 0 && p.G == 1 && p.Cout <= 8 && p.H == p.Ho && p.W == p.Wo &&
+         ((long)p.H * p.W) % 8 == 0 && a8(p.x) && a8(p.y) && (!p.r.ptr || a8(p.r));
+}
+
 // Row-tiled stem for the common case (kernels/conv_cin3.cl:67-118 semantics): 3x3 stride 2
 // pad 1, Cin <= 3, Cout <= 16, planar NCHW input, channels-last output, no residual.  A
 // work-group owns TR output rows of one image.  It stages the 2*TR+1 input rows it needs in
@@ -326,6 +380,13 @@ void launch_conv_direct(const ConvParams & p, hipStream_t s)
       if (nchw) hipLaunchKernelGGL((conv_stem_mfma_kernel<2, true>), grid, dim3(256), 0, s, p);
       else hipLaunchKernelGGL((conv_stem_mfma_kernel<2, false>), grid, dim3(256), 0, s, p);
     }
+    return;
+  }
+  if (conv1x1_nchw8_ok(p)) {
+    const dim3 grid(nblk((long)p.H * p.W / 8, 256), (unsigned)p.batch);
+    if (p.Cout <= 1) hipLaunchKernelGGL(conv1x1_nchw8_kernel<1>, grid, dim3(256), 0, s, p);
+    else if (p.Cout <= 4) hipLaunchKernelGGL(conv1x1_nchw8_kernel<4>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(conv1x1_nchw8_kernel<8>, grid, dim3(256), 0, s, p);
     return;
   }
   const int cout_g = p.Cout / p.G;
@@ -797,21 +858,20 @@ __global__ void __launch_bounds__(256) rows_vec8_kernel(const SmallParams q, int
   const int b = blockIdx.y;
   if (t >= rows * L8) return;
   const int r = t / L8, j = (t - r * L8) * 8;
-  int src, dst;
+  long src, dst;
   if (kind == 0) {        // y row r = (o, l) <- x row o*axdim + start + l
     const int o = r / q.i4, l = r - o * q.i4;
-    dst = r;
-    src = o * q.i1 + q.i3 + l;
-  } else if (kind == 1) { // x row r = (o, ax) -> y row o*tot + off + ax
-    const int o = r / q.i1, ax = r - o * q.i1;
-    src = r;
-    dst = o * q.i3 + q.i4 + ax;
+    dst = (long)r * L;
+    src = (long)(o * q.i1 + q.i3 + l) * L;
+  } else if (kind == 1) { // x block o (axis x inner, L elements) -> y at (o*tot + off)*inner
+    src = (long)r * L;
+    dst = ((long)r * q.i3 + q.i4) * q.i2;
   } else {                // y row r = (d2, d1) <- x row d1*D2 + d2
     const int d2 = r / q.i0, d1 = r - d2 * q.i0;
-    dst = r;
-    src = d1 * q.i1 + d2;
+    dst = (long)r * L;
+    src = (long)(d1 * q.i1 + d2) * L;
   }
-  st8(q.y.ptr, (long)b * q.y.img + (long)dst * L + j, ld8(q.a.ptr, (long)b * q.a.img + (long)src * L + j));
+  st8(q.y.ptr, (long)b * q.y.img + dst + j, ld8(q.a.ptr, (long)b * q.a.img + src + j));
 }
 
 // ew_binary_bcast with 8 consecutive outputs per lane (output innermost extent % 8 == 0).
@@ -862,6 +922,48 @@ __global__ void __launch_bounds__(256) softmax_reg_kernel(const SmallParams q)
 #pragma unroll
   for (int a = 0; a < 32; ++a)
     if (a < q.i1) y[(long)a * q.i2] = (_Float16)(v[a] * inv);
+}
+
+// softmax over a short strided axis with 8 consecutive inner positions per lane (inner % 8
+// == 0): 16-byte loads and stores; the axis values stay in registers as fp16 and exp is
+// recomputed for the output (the same fp32 arithmetic as softmax_reg_kernel).
+template <int AMAX>
+__global__ void __launch_bounds__(256) softmax_vec8_kernel(const SmallParams q)
+{
+  const int I8 = q.i2 >> 3;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= q.i0 * I8) return;
+  const int o = i / I8, r = (i - o * I8) * 8;
+  const long base = (long)b * q.a.img + (long)o * q.i1 * q.i2 + r;
+  const long ybase = (long)b * q.y.img + (long)o * q.i1 * q.i2 + r;
+  h8 xv[AMAX];
+  float m[8], sum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) { m[e] = -3.4e38f; sum[e] = 0.0f; }
+#pragma unroll
+  for (int a = 0; a < AMAX; ++a)
+    if (a < q.i1) {
+      xv[a] = ld8(q.a.ptr, base + (long)a * q.i2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], (float)xv[a][e]);
+    }
+#pragma unroll
+  for (int a = 0; a < AMAX; ++a)
+    if (a < q.i1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum[e] += __expf((float)xv[a][e] - m[e]);
+    }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sum[e] = 1.0f / sum[e];
+#pragma unroll
+  for (int a = 0; a < AMAX; ++a)
+    if (a < q.i1) {
+      h8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (_Float16)(__expf((float)xv[a][e] - m[e]) * sum[e]);
+      st8(q.y.ptr, ybase + (long)a * q.i2, v);
+    }
 }
 
 // softmax over the contiguous last axis (inner == 1): one wave per row, shuffle reductions.
@@ -933,10 +1035,12 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
   case kSliceAxis:
   case kConcatOuter:
   case kPermute: {
-    const int L = q.i2;
+    // concat: one row per outer index, axis x inner contiguous elements on both sides
+    const int L = kind == kConcatOuter ? q.i1 * q.i2 : q.i2;
     if (L % 8 || !al8(q.a) || !al8(q.y)) return false;
+    if (kind == kConcatOuter && (((long)q.i3 * q.i2) % 8 || ((long)q.i4 * q.i2) % 8)) return false;
     if (kind == kPermute && q.op != 0) return false;
-    const int rows = kind == kSliceAxis ? q.i0 * q.i4 : (kind == kConcatOuter ? q.i0 * q.i1 : q.i0 * q.i1);
+    const int rows = kind == kSliceAxis ? q.i0 * q.i4 : (kind == kConcatOuter ? q.i0 : q.i0 * q.i1);
     const int k = kind == kSliceAxis ? 0 : (kind == kConcatOuter ? 1 : 2);
     hipLaunchKernelGGL(rows_vec8_kernel, dim3(nblk((long)rows * (L / 8), 256), B), blk, 0, s, q, k, L, rows);
     return true;
@@ -946,6 +1050,12 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
     hipLaunchKernelGGL(ew_bcast8_kernel, dim3(nblk(q.n / 8, 256), B), blk, 0, s, q);
     return true;
   case kSoftmax:
+    if (q.i2 % 8 == 0 && q.i1 <= 32 && al8(q.a) && al8(q.y)) {
+      const unsigned g = nblk((long)q.i0 * (q.i2 / 8), 256);
+      if (q.i1 <= 16) hipLaunchKernelGGL(softmax_vec8_kernel<16>, dim3(g, B), blk, 0, s, q);
+      else hipLaunchKernelGGL(softmax_vec8_kernel<32>, dim3(g, B), blk, 0, s, q);
+      return true;
+    }
     if (q.i2 > 1 && q.i1 <= 32) {
       hipLaunchKernelGGL(softmax_reg_kernel, dim3(nblk((long)q.i0 * q.i2, 256), B), blk, 0, s, q);
       return true;
