@@ -321,6 +321,11 @@ static void launch_hc(const ConvParams & p, hipStream_t s)
 
 void launch_conv_halo(const ConvParams & p, hipStream_t s)
 {
+  const int bc = conv_batch_chunk(p);
+  if (bc < p.batch) {
+    for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_halo(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
+    return;
+  }
   switch (p.halo - 1) {
   case 0: launch_hc<16, 4, 1, 4, 1, 360>(p, s); break;
   case 1: launch_hc<32, 4, 1, 2, 1, 360>(p, s); break;

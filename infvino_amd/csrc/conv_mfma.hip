@@ -14,8 +14,8 @@
 //   one 16-byte load of a channels-last pixel.
 // Work-group: 4 waves (256 lanes), tile BM = 128 pixels x BN channels, each wave TM x TN
 // 32x32 MFMA blocks.  Linear pixel tiles over all images; the im2col tile is gathered from
-// global memory (any K, stride, pad; every input pixel is re-read per tap from L2), BK = 32
-// double buffered through LDS.  The 3x3 stride-1 convs with a well-filled grid use the
+// global memory (any K, stride, pad; every input pixel is re-read per tap from L2), K steps
+// of 32 or 64 double buffered through LDS.  The 3x3 stride-1 convs with a well-filled grid use the
 // LDS-patch kernel of conv_halo.hip instead.  With split-K the fp32 partials go to a
 // workspace and splitk_reduce_kernel finishes.
 #include "conv_common.hpp"
@@ -23,49 +23,29 @@
 
 namespace ivh {
 
-typedef Mf<32>::acc_t f16v;
-
-template <int WGM, int WGN, int TM, int TN>
-struct Tile {
-  static constexpr int BM = WGM * TM * 32;
-  static constexpr int BN = WGN * TN * 32;
-  static constexpr int BK = 32;
-  static constexpr int LDK = BK + 8;  // padded LDS row: 16-byte reads conflict free
-  static constexpr int KCH = BK / 8;
-  static constexpr int OUT = TileShape<32, WGM, WGN, TM, TN>::EPI;
-};
-
-// MFMA block product over one 16-deep K slice: A (weights) rows from wrow (row stride
-// `wstride` halves per output channel), B (pixels) at per-tile LDS offsets boff[tm].
-template <int TM, int TN>
-__device__ __forceinline__ void mfma_step(f16v (&acc)[TN][TM], const _Float16 * wrow, const _Float16 * prow,
-                                          const int (&boff)[TM], int wstride)
-{
-  h8 fa[TN], fb[TM];
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) fa[tn] = *reinterpret_cast<const h8 *>(wrow + tn * 32 * wstride);
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) fb[tm] = *reinterpret_cast<const h8 *>(prow + boff[tm]);
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-      acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tn], fb[tm], acc[tn][tm], 0, 0, 0);
-}
-
 // ------------------------------------------------------------ im2col kernel
-template <int WGM, int WGN, int TM, int TN>
+// Tile: BM = WGM*TM*32 output pixels (linear over all images) x BN = WGN*TN*32 channels,
+// K steps of BK (32 or 64, chosen with the packing).  A (pixel) loads: a thread owns fixed
+// tile rows and one 8-channel piece of every K step; the tap / channel of its piece moves
+// incrementally, out-of-image taps and K padding load from past the buffer's range (zeros),
+// and the ragged channels of a last piece (Cin % 8) are zeroed when written to LDS.  B
+// (weight) loads are buffer loads at a loop-invariant offset plus the step's scalar offset.
+// Both are prefetched one step ahead in registers and double buffered in LDS.
+template <int WGM, int WGN, int TM, int TN, int BK>
 __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 {
-  using T = Tile<WGM, WGN, TM, TN>;
-  constexpr int BM = T::BM, BN = T::BN, BK = T::BK, LDK = T::LDK, KCH = T::KCH;
-  constexpr int A_IT = BM * KCH / 256, B_IT = (BN * KCH + 255) / 256;
-  constexpr int STAGE = 2 * (BM + BN) * LDK;
-  static_assert(WGM * WGN == 4, "four waves per work-group");
-  static_assert((BM * KCH) % 256 == 0 && (256 % KCH) == 0, "tile/thread mismatch");
-  __shared__ __attribute__((aligned(16))) _Float16 lds[STAGE > T::OUT ? STAGE : T::OUT];
-  _Float16 * As = lds;                 // [2][BM][LDK]
-  _Float16 * Bs = lds + 2 * BM * LDK;  // [2][BN][LDK]
+  using F = Mf<32>;
+  using T = TileShape<32, WGM, WGN, TM, TN>;
+  typedef F::acc_t acc_t;
+  constexpr int BM = T::BM, BN = T::BN;
+  constexpr int LDK = BK + 8;                 // padded LDS row: 16-byte reads conflict free
+  constexpr int KC = BK / 8;                  // 16-byte pieces per row and step
+  constexpr int RPI = 256 / KC;               // rows covered by one pass of the 256 threads
+  constexpr int A_IT = BM / RPI, B_IT = (BN + RPI - 1) / RPI;
+  constexpr int STAGE = BM * LDK + BN * LDK;
+  constexpr int L_ALL = 2 * STAGE > T::EPI ? 2 * STAGE : T::EPI;
+  static_assert(BM % RPI == 0, "tile rows");
+  __shared__ __attribute__((aligned(16))) _Float16 lds[L_ALL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
@@ -73,32 +53,46 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   const long M = (long)p.batch * HWo;
   const long m0 = (long)blockIdx.x * BM;
   const int n0 = blockIdx.y * BN;
+  const int kc = tid % KC, r0 = tid / KC;
 
-  // A (im2col) load slots: thread owns rows tid/KCH + i*(256/KCH), chunk kc
-  const int kc = tid % KCH;
-  const _Float16 * arow[A_IT];
-  int aiy[A_IT], aix[A_IT];
+  const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
+
+  // A rows of this thread: image base offset and the input corner of the output pixel
+  int abase[A_IT], aiy[A_IT], aix[A_IT];
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
-    const long pm = m0 + tid / KCH + i * (256 / KCH);
+    const long pm = m0 + r0 + i * RPI;
     if (pm < M) {
       const int b = (int)(pm / HWo), hw = (int)(pm - (long)b * HWo);
       const int oy = hw / p.Wo, ox = hw - oy * p.Wo;
-      arow[i] = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img;
+      abase[i] = b * (int)p.x.img;
       aiy[i] = oy * p.S - p.P;
       aix[i] = ox * p.S - p.P;
     } else {
-      arow[i] = nullptr;
-      aiy[i] = -100000;
-      aix[i] = -100000;
+      abase[i] = 0;
+      aiy[i] = -0x4000000;  // never inside the image
+      aix[i] = 0;
     }
   }
-  // K range of this work-group (split-K: blockIdx.z-th slice of the K tiles)
+  unsigned bsrc[B_IT];
+#pragma unroll
+  for (int i = 0; i < B_IT; ++i) {
+    const int r = r0 + i * RPI < BN ? r0 + i * RPI : 0;
+    bsrc[i] = (unsigned)((r * p.kpad + kc * 8) * 2);
+  }
+
+  // K range of this work-group (split-K: blockIdx.z-th slice of the K steps)
   const int nk_all = p.kpad / BK;
   const int per = (nk_all + p.ksplit - 1) / p.ksplit;
   const int kt0 = blockIdx.z * per;
   const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
+  const int nk = kt1 > kt0 ? kt1 - kt0 : 0;
   const int taps = p.K * p.K;
+  // position (tap, ky, kx, ci) of this thread's piece in the current load step
   int ci = kt0 * BK + kc * 8, tap = 0, ky = 0, kx = 0;
   auto norm_k = [&]() {
     while (ci >= p.cin8) {
@@ -108,73 +102,77 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
     }
   };
   norm_k();
-  const _Float16 * wbase = reinterpret_cast<const _Float16 *>(p.w);
   const bool ragged = (p.Cin & 7) != 0;
 
   h8 ra[A_IT], rb[B_IT];
-  auto load_tile = [&](int kt) {
+  int aci = 0;  // channel of the loaded A piece (for the ragged mask at store time)
+  auto load = [&](int kt) {
+    aci = ci;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
-      h8 v = {};
-      if (tap < taps) {
-        const int iy = aiy[i] + ky, ix = aix[i] + kx;
-        if ((unsigned)iy < (unsigned)p.H && (unsigned)ix < (unsigned)p.W) {
-          v = *reinterpret_cast<const h8 *>(arow[i] + ((long)iy * p.W + ix) * p.x.cs + ci);
-          if (ragged) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (ci + e >= p.Cin) v[e] = (_Float16)0.0f;
-          }
-        }
-      }
-      ra[i] = v;
+      const int iy = aiy[i] + ky, ix = aix[i] + kx;
+      const bool ok = tap < taps && (unsigned)iy < (unsigned)p.H && (unsigned)ix < (unsigned)p.W;
+      const unsigned off = ok ? (unsigned)((abase[i] + (iy * p.W + ix) * p.x.cs + ci) * 2) : kBufOOB;
+      ra[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
 #pragma unroll
-    for (int i = 0; i < B_IT; ++i) {
-      const int r = tid / KCH + i * (256 / KCH);
-      if (r < BN) rb[i] = *reinterpret_cast<const h8 *>(wbase + (long)(n0 + r) * p.kpad + kt * BK + kc * 8);
-    }
+    for (int i = 0; i < B_IT; ++i)
+      rb[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
     ci += BK;
     norm_k();
   };
-  auto store_tile = [&](int buf) {
+  auto store = [&](_Float16 * st) {
+    u16x8 keep;
 #pragma unroll
-    for (int i = 0; i < A_IT; ++i)
-      *reinterpret_cast<h8 *>(As + (buf * BM + tid / KCH + i * (256 / KCH)) * LDK + kc * 8) = ra[i];
+    for (int e = 0; e < 8; ++e) keep[e] = aci + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
 #pragma unroll
-    for (int i = 0; i < B_IT; ++i) {
-      const int r = tid / KCH + i * (256 / KCH);
-      if (r < BN) *reinterpret_cast<h8 *>(Bs + (buf * BN + r) * LDK + kc * 8) = rb[i];
+    for (int i = 0; i < A_IT; ++i) {
+      h8 v = ra[i];
+      if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
+      *reinterpret_cast<h8 *>(st + (r0 + i * RPI) * LDK + kc * 8) = v;
     }
+#pragma unroll
+    for (int i = 0; i < B_IT; ++i)
+      if (r0 + i * RPI < BN) *reinterpret_cast<h8 *>(st + (BM + r0 + i * RPI) * LDK + kc * 8) = rb[i];
   };
 
-  f16v acc[TN][TM];
+  acc_t acc[TN][TM];
 #pragma unroll
   for (int a = 0; a < TN; ++a)
 #pragma unroll
     for (int b = 0; b < TM; ++b)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+      for (int v = 0; v < F::NV; ++v) acc[a][b][v] = 0.0f;
 
-  int boff[TM];
+  const int brow = (wm * TM * 32 + (lane & 31)) * LDK + F::kq(lane);
+  const int arow = (BM + wn * TN * 32 + (lane & 31)) * LDK + F::kq(lane);
+  auto step = [&](int s, const _Float16 * cur, _Float16 * nxt) {
+    if (s + 1 < nk) load(kt0 + s + 1);
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) boff[tm] = (wm * TM * 32 + tm * 32 + (lane & 31)) * LDK + (lane >> 5) * 8;
-
-  const int nk = kt1 - kt0;
+    for (int j = 0; j < BK / 16; ++j) {
+      h8 fa[TN], fb[TM];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) fa[tn] = *reinterpret_cast<const h8 *>(cur + arow + tn * 32 * LDK + j * 16);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) fb[tm] = *reinterpret_cast<const h8 *>(cur + brow + tm * 32 * LDK + j * 16);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = F::mma(fa[tn], fb[tm], acc[tn][tm]);
+    }
+    if (s + 1 < nk) store(nxt);
+    __syncthreads();
+  };
+  _Float16 * const S0 = lds;
+  _Float16 * const S1 = lds + STAGE;
   if (nk > 0) {
-    load_tile(kt0);
-    store_tile(0);
+    load(kt0);
+    store(S0);
   }
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_tile(kt0 + kt + 1);
-    const _Float16 * wrow = Bs + (cur * BN + wn * TN * 32 + (lane & 31)) * LDK + (lane >> 5) * 8;
-    const _Float16 * prow = As + cur * BM * LDK;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) mfma_step<TM, TN>(acc, wrow + kk * 16, prow + kk * 16, boff, LDK);
-    if (kt + 1 < nk) store_tile(cur ^ 1);
-    __syncthreads();
+  for (int s = 0; s < nk; s += 2) {
+    step(s, S0, S1);
+    if (s + 1 < nk) step(s + 1, S1, S0);
   }
 
   tile_epilogue<32, WGM, WGN, TM, TN>(acc, p, lds, n0, [&](int pl, int & b, int & hw) {
@@ -215,18 +213,44 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const ConvParams p, 
 // Tile table: a small CDNA4 choice per op (BN from Cout; BM = 128 pixels).
 int igemm_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
 
-template <int WGM, int WGN, int TM, int TN>
+template <int WGM, int WGN, int TM, int TN, int BK>
 static void launch_t(const ConvParams & p, hipStream_t s)
 {
-  using T = Tile<WGM, WGN, TM, TN>;
+  using T = TileShape<32, WGM, WGN, TM, TN>;
   const long M = (long)p.batch * p.Ho * p.Wo;
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
-  hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const long n = M * p.Cout;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
                        (int)grid.y * T::BN);
   }
+}
+
+template <int BK>
+static void launch_bk(const ConvParams & p, hipStream_t s)
+{
+  switch (igemm_bn(p.Cout)) {
+  case 32: launch_t<4, 1, 1, 1, BK>(p, s); break;
+  case 64: launch_t<2, 2, 2, 1, BK>(p, s); break;
+  default: launch_t<2, 2, 2, 2, BK>(p, s); break;
+  }
+}
+
+// K step of a layer (measured on MI355X): 64 for wide layers with a long K, where the MFMA
+// work per barrier matters; 32 otherwise, where the smaller LDS stages keep more
+// work-groups resident for the memory-bound layers.  The packed K is a multiple of it.
+int igemm_bk(int cout, int kk)
+{
+  if (cout <= 64 || kk < 512) return 32;
+  const int k64 = (kk + 63) / 64 * 64;
+  return (k64 - kk) * 8 <= kk ? 64 : 32;
+}
+
+int igemm_kpad(int cout, int kk)
+{
+  const int bk = igemm_bk(cout, kk);
+  return (kk + bk - 1) / bk * bk;
 }
 
 // Split-K factor: convs whose output tiles cannot fill the chip (batch 1, 20x20 / 40x40
@@ -243,17 +267,37 @@ int igemm_ksplit(long M, int cout, int kpad)
   return s < 2 ? 1 : s;
 }
 
+// Batch chunk that keeps a conv's input view below 2^31 bytes (the kernels' buffer ranges
+// and 32-bit element offsets); every image of a chunk is independent of the others.
+int conv_batch_chunk(const ConvParams & p)
+{
+  const long per = std::max<long>(p.x.img * 2, 1);
+  return (int)std::max<long>(1, std::min<long>(p.batch, ((1L << 31) - 1) / per - 1));
+}
+
+ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb)
+{
+  ConvParams q = p;
+  q.batch = nb;
+  q.x.ptr += (long)b0 * p.x.img;
+  q.y.ptr += (long)b0 * p.y.img;
+  if (q.r.ptr) q.r.ptr += (long)b0 * p.r.img;
+  return q;
+}
+
 void launch_conv_igemm(const ConvParams & p, hipStream_t s)
 {
+  const int bc = conv_batch_chunk(p);
+  if (bc < p.batch) {
+    for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_igemm(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
+    return;
+  }
   if (p.halo) {
     launch_conv_halo(p, s);
     return;
   }
-  switch (igemm_bn(p.Cout)) {
-  case 32: launch_t<4, 1, 1, 1>(p, s); break;
-  case 64: launch_t<2, 2, 2, 1>(p, s); break;
-  default: launch_t<2, 2, 2, 2>(p, s); break;
-  }
+  if (p.bk == 64) launch_bk<64>(p, s);
+  else launch_bk<32>(p, s);
 }
 
 }  // namespace ivh

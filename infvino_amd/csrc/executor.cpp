@@ -731,7 +731,7 @@ void Model::uploadWeights()
     pk.kind = kind;
     if (kind == 0) {
       const int cin8 = (int)round_up(cin_g, 8);
-      const int kpad = (int)round_up((long)K * K * cin8, kIgemmBK);
+      const int kpad = igemm_kpad(Cout, K * K * cin8);
       const int rows = (int)round_up(Cout, kIgemmRowPad);
       std::vector<uint16_t> P((size_t)rows * kpad, 0);
       for (int co = 0; co < Cout; ++co)
@@ -902,13 +902,14 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
       L.kind = Launch::kIgemm;
       p.cin8 = pk.cin8;
       p.kpad = pk.kpad;
+      p.bk = igemm_bk(p.Cout, p.K * p.K * p.cin8);
       if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
         p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
         if (p.ksplit > 1) p.ws = ws_;
       }
       // LDS-patch kernel when its grid fills the chip; otherwise im2col (+ split-K)
       int hc, th, tw;
-      if (pk.halo && p.K == 3 && p.S == 1 && p.P == 1 && (long)batch * p.x.img * 2 < (1L << 31) &&
+      if (pk.halo && p.K == 3 && p.S == 1 && p.P == 1 &&
           halo_plan(p.Cin, p.Cout, p.H, p.W, batch, &hc, &th, &tw)) {
         ConvParams q = p;
         q.th = th;
@@ -1246,7 +1247,6 @@ void Model::validate(const Launch & l) const
             p.th * p.tw > (cfg < 4 ? 256 : 128) || (p.Cout + halo_bn(cfg) - 1) / halo_bn(cfg) * halo_bn(cfg) > rows)
           throw std::runtime_error("halo geometry");
         if (p.kpad != (p.Cin + ck - 1) / ck * halo_taps(ck) * ck) throw std::runtime_error("halo weight packing");
-        if ((long)p.batch * p.x.img * 2 >= (1L << 31)) throw std::runtime_error("halo input view exceeds 2^31 bytes");
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("halo geometry too large");
       }
       if (p.ksplit > 1) {
@@ -1254,7 +1254,8 @@ void Model::validate(const Launch & l) const
         if ((size_t)p.ksplit * rows * M > ws_floats_) throw std::runtime_error("split-K workspace too small");
         check(p.ws, 0, (long)p.ksplit * rows * M - 1, 4, "igemm split-K workspace");
       }
-      if (p.kpad % kIgemmBK) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (p.kpad % kIgemmBK || (!p.halo && (p.bk != 32 && p.bk != 64))) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (!p.halo && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
     } else if (l.kind == Launch::kDirect && p.stem_mfma) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
       check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");

@@ -43,6 +43,7 @@ struct ConvParams {
   int act = 0;
   int cin8 = 0;   // input channels rounded up to 8 (im2col K chunking)
   int kpad = 0;   // packed K per output channel, multiple of the K tile
+  int bk = 32;    // implicit-GEMM K step (32 / 64); kpad is a multiple of it
   // split-K (implicit GEMM): ksplit > 1 writes fp32 partials [ksplit][Npad][M] to ws and a
   // second kernel reduces them in fixed order and applies the epilogue
   int ksplit = 1;

@@ -8,9 +8,13 @@ namespace ivh {
 
 // conv_mfma.hip
 int igemm_bn(int cout);                    // N tile of the implicit GEMM for a Cout
-constexpr int kIgemmBK = 32;               // K tile (packed weight rows are a multiple)
+int igemm_bk(int cout, int kk);            // K step of a layer with K*K*cin8 = kk (32 / 64)
+int igemm_kpad(int cout, int kk);          // packed K: kk rounded up to that step
+constexpr int kIgemmBK = 32;               // packed K is always a multiple of this
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
 void launch_conv_igemm(const ConvParams & p, hipStream_t s);
+int conv_batch_chunk(const ConvParams & p);                      // images per launch (< 2^31 B input)
+ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb);  // images [b0, b0 + nb)
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
 
 // conv_halo.hip: 3x3 stride-1 pad-1 convs with an LDS input patch
