@@ -125,3 +125,74 @@ def test_cpp_backend_dropin(tmp_path):
     xf = ((i * np.uint64(2654435761)) % np.uint64(1000)).astype(np.float32) / np.float32(1000.0)
     ref = O.h2f(O.run_plan(p, O.f2h_trunc(xf), 2)[0].ravel())
     assert _model_ok(O.f2h(got), O.f2h(ref), "C++ HipBackend mbv3 b2")
+
+
+# ----------------------------------------------------------------- decode + NMS parity
+# Decoded detections after the reference's PoseDecoder + NMS (restated in oracle/decode.py),
+# HIP raw heads vs oracle raw heads, conf 0.25 / IoU 0.7.  Random-init heads put many
+# anchors near a decision: an anchor whose fate differs between the two is accepted only
+# when a near-tie explains it -- its score within EPS_S of conf, an overlap with a kept box
+# within EPS_I of the IoU threshold, or an overlapping kept box with a score within EPS_S --
+# or when it overlaps such an anchor (the flip then cascades).  Matched detections must
+# agree to BOX_TOL / KPT_TOL pixels (network input coordinates).
+EPS_S, EPS_I, BOX_TOL, KPT_TOL = 2e-3, 2e-2, 2.0, 2.0
+
+
+def _explained(dh, do, conf, thr):
+    from oracle import decode as D
+    A = {d.anchor: d for d in dh}
+    B = {d.anchor: d for d in do}
+    unmatched = {a: (A.get(a) or B.get(a)) for a in set(A) ^ set(B)}
+    kept = list(A.values()) + list(B.values())
+    kbox = np.array([d.box for d in kept], np.float32).reshape(-1, 4)
+    ksc = np.array([d.score for d in kept], np.float32)
+    seeds = set()
+    for a, d in unmatched.items():
+        if abs(d.score - conf) <= EPS_S:
+            seeds.add(a)
+            continue
+        io = D.iou_one_to_many(d.box, kbox)
+        other = np.array([k.anchor != a for k in kept])
+        if np.any(other & (np.abs(io - thr) <= EPS_I)) or np.any(other & (io > thr - EPS_I) & (np.abs(ksc - d.score) <= EPS_S)):
+            seeds.add(a)
+    done = set(seeds)
+    changed = True
+    while changed:
+        changed = False
+        for a, d in unmatched.items():
+            if a in done:
+                continue
+            if any(D.iou(d.box, unmatched[b].box) > thr - EPS_I for b in done):
+                done.add(a)
+                changed = True
+    return len(A.keys() & B.keys()), unmatched, done
+
+
+@pytest.mark.parametrize("name,imgsz,batch", [("yolov8n-pose", 640, 2), ("yolo11n-pose", 640, 1)])
+def test_pose_decode_parity(tmp_path, name, imgsz, batch):
+    from oracle import decode as D
+    path, _ = pw.MODELS[name](str(tmp_path), seed=0, imgsz=imgsz)
+    p = O.Plan.load(path)
+    x = _inputs(p, batch, 3)
+    m = ia.PlanModel(path, 0, batch)
+    m.setInput(x, batch)
+    m.run(batch)
+    got = m.readOutputF32(0, batch).reshape(batch, 56, -1)
+    m.close()
+    ref = O.h2f(O.run_plan(p, x, batch)[0]).reshape(batch, 56, -1)
+    conf, thr = 0.25, 0.7
+    # the reference's max_det (ModelInfo.hpp:34) and the whole kept set
+    for b, max_det in [(b, md) for b in range(batch) for md in (300, 10 ** 6)]:
+        dh = D.pose_decode(got[b], conf=conf, iou_thr=thr, max_det=max_det)
+        do = D.pose_decode(ref[b], conf=conf, iou_thr=thr, max_det=max_det)
+        nmatch, unmatched, explained = _explained(dh, do, conf, thr)
+        A = {d.anchor: d for d in dh}
+        B = {d.anchor: d for d in do}
+        box_err = max([np.max(np.abs(np.subtract(A[a].box, B[a].box))) for a in A.keys() & B.keys()] or [0.0])
+        kpt_err = max([np.max(np.abs(A[a].keypoints - B[a].keypoints)) for a in A.keys() & B.keys()] or [0.0])
+        print(f"{name} image {b} max_det {max_det}: hip {len(dh)} oracle {len(do)} matched {nmatch} unmatched {len(unmatched)} "
+              f"explained {len(explained)} box_err {box_err:.3f}px kpt_err {kpt_err:.3f}px")
+        assert len(do) > 0
+        assert set(unmatched) == explained, f"unexplained: {sorted(set(unmatched) - explained)[:10]}"
+        assert nmatch >= 0.9 * max(len(dh), len(do))
+        assert box_err <= BOX_TOL and kpt_err <= KPT_TOL
