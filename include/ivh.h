@@ -96,6 +96,60 @@ int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel,
                   char * desc, size_t desc_len, double * flops, double * bytes);
 int ivh_memory_info(const ivh_model * m, int batch, size_t * arena_bytes, size_t * weight_bytes);
 
+/* ---------------------------------------------------------------- single-op entry points
+ * One operation on caller-owned device buffers (hipMalloc'd; `stream` is a hipStream_t, NULL
+ * for the null stream), for op-level checks and benchmarks: the reference drives its kernels
+ * one at a time from scripts/kernel_check.py:34-137 and tools/infvino_numtest.cpp:88-100
+ * through PlanModel's per-op dispatch (src/PlanModel.cpp:3418-3990, small ops 2681-3088).
+ * Every tensor holds `batch` images back to back (image stride = its per-image element
+ * count, channels-last tensors: H*W*round8(C)); fp16 storage, fp32 accumulation.  The calls
+ * enqueue and return; a bad argument is reported before anything is enqueued.
+ */
+typedef struct ivh_conv_desc {
+  int cin, cout, h, w;      /* input / output channels, input height and width */
+  int k, stride, pad, groups;
+  int act;                  /* 0 none, 1 SiLU, 2 ReLU, 3 HardSwish, 4 HardSigmoid, 5 Sigmoid */
+  int has_bias;             /* 1: the packing holds a bias */
+  int channels_last;        /* 1: x, res and y are NHWC, pixel stride round8(C); 0: NCHW */
+} ivh_conv_desc;
+
+/* output height and width of d */
+int ivh_conv_out_dims(const ivh_conv_desc * d, int * ho, int * wo);
+/* bytes of d's packed operands (the device buffer ivh_pack_conv_weights fills) */
+int ivh_conv_packed_bytes(const ivh_conv_desc * d, size_t * bytes);
+/* packs plan-order fp16 weights w[cout][cin/groups][k][k] and fp16 bias[cout] (host memory;
+   bias NULL when !has_bias) into packed_dev (replaces the reference's per-kernel weight
+   repacks, src/PlanModel.cpp:232-334); synchronous */
+int ivh_pack_conv_weights(const ivh_conv_desc * d, const uint16_t * w_host, const uint16_t * bias_host,
+                          void * packed_dev);
+/* y = act(conv(x, w) + b) (+ res; res may be NULL): conv1x1 -> gemm_f16 (kernels/gemm.cl:183-669),
+   conv3x3 -> conv3x3_ov / _blk / _cin3 / _f16, grouped and depthwise -> conv_general
+   (src/PlanModel.cpp:3447-3933) */
+int ivh_conv2d_f16(const ivh_conv_desc * d, const void * x, const void * packed, const void * res, void * y,
+                   int batch, void * stream);
+/* the same for a depthwise conv only (groups == cin == cout, k 3 or 5): depthwise_f16 /
+   depthwise_blk (kernels/conv_general.cl:85-187, depthwise_blk.cl:118-228) */
+int ivh_dwconv_f16(const ivh_conv_desc * d, const void * x, const void * packed, const void * res, void * y,
+                   int batch, void * stream);
+/* FC: y[b][o] = act(sum_i W[o][i] x[b][i] + bias[o]), x [batch][n_in], y [batch][n_out]; packed
+   with the desc {cin n_in, cout n_out, h 1, w 1, k 1, stride 1, pad 0, groups 1, act, has_bias,
+   channels_last 0}: conv1x1_gemv_f16 (kernels/conv1x1.cl:157-198) */
+int ivh_gemv_f16(const ivh_conv_desc * d, const void * x, const void * packed, void * y, int batch, void * stream);
+/* elementwise over n elements per image (ew_binary / ew_unary, kernels/ops.cl:10-63): with b,
+   y = a op b (op 0 add, 1 sub, 2 mul, 3 div; b_scalar: b is one element shared by all);
+   with b == NULL, y = act_op(a) (op: the activation codes of ivh_conv_desc.act) */
+int ivh_eltwise_f16(int op, const void * a, const void * b, int b_scalar, void * y, size_t n, int batch,
+                    void * stream);
+/* NCHW [batch][c][h][w]: kind 0 maxpool (k, s, p; taps outside the image ignored, ops.cl:148-166),
+   kind 1 nearest upsample by s (k, p unused; ops.cl:168-179) */
+int ivh_pool_f16(int kind, const void * x, void * y, int c, int h, int w, int k, int s, int p, int batch,
+                 void * stream);
+/* softmax over the middle axis of [outer][axis][inner] (ops.cl:181-197) */
+int ivh_softmax_f16(const void * x, void * y, int outer, int axis, int inner, int batch, void * stream);
+/* y[i] = a[i] . b[i]: a [bb][m][k], b [bb][k][n], y [bb][m][n] per image (ops.cl:276-294) */
+int ivh_bmm_f16(const void * a, const void * b, void * y, int bb, int m, int k, int n, int batch,
+                void * stream);
+
 #ifdef __cplusplus
 }
 #endif

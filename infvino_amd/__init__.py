@@ -35,6 +35,14 @@ IVH_FLAG_NO_HALO = 0x100
 # every symbol include/ivh.h declares, with (restype, argtypes)
 _vp, _i, _u32, _sz, _d = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_double
 _ip, _szp, _dp, _i64p = C.POINTER(C.c_int), C.POINTER(C.c_size_t), C.POINTER(C.c_double), C.POINTER(C.c_int64)
+class ConvDesc(C.Structure):
+    """ivh_conv_desc (include/ivh.h)."""
+    _fields_ = [(n, C.c_int) for n in ("cin", "cout", "h", "w", "k", "stride", "pad", "groups", "act",
+                                       "has_bias", "channels_last")]
+
+
+_cdp = C.POINTER(ConvDesc)
+
 SIGNATURES = {
     "ivh_last_error": (C.c_char_p, []),
     "ivh_version": (_i, [_ip, _ip]),
@@ -61,6 +69,17 @@ SIGNATURES = {
     "ivh_profile_nodes": (_i, [_vp, _i, _i, _dp, _i]),
     "ivh_node_info": (_i, [_vp, _i, C.c_char_p, _sz, C.c_char_p, _sz, C.c_char_p, _sz, _dp, _dp]),
     "ivh_memory_info": (_i, [_vp, _i, _szp, _szp]),
+    # single-op entry points (device pointers as integers, stream None = null stream)
+    "ivh_conv_out_dims": (_i, [_cdp, _ip, _ip]),
+    "ivh_conv_packed_bytes": (_i, [_cdp, _szp]),
+    "ivh_pack_conv_weights": (_i, [_cdp, _vp, _vp, _vp]),
+    "ivh_conv2d_f16": (_i, [_cdp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "ivh_dwconv_f16": (_i, [_cdp, _vp, _vp, _vp, _vp, _i, _vp]),
+    "ivh_gemv_f16": (_i, [_cdp, _vp, _vp, _vp, _i, _vp]),
+    "ivh_eltwise_f16": (_i, [_i, _vp, _vp, _i, _vp, _sz, _i, _vp]),
+    "ivh_pool_f16": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "ivh_softmax_f16": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
+    "ivh_bmm_f16": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
 }
 
 _lib = None

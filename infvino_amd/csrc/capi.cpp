@@ -3,13 +3,17 @@
 // std::runtime_error message (src/ClBackend.cpp:16-18,36-39; src/PlanModel.cpp:437,498,536-539).
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstring>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "../../include/ivh.h"
+#include "conv_pack.hpp"
 #include "executor.hpp"
+#include "kernels.hpp"
 
 struct ivh_model {
   ivh::Model * m = nullptr;
@@ -53,6 +57,90 @@ void dims_out(const std::vector<int64_t> & d, int64_t * dims, int * rank)
     for (size_t i = 0; i < d.size(); ++i) dims[i] = d[i];
   }
   *rank = (int)d.size();
+}
+// ---- single-op helpers
+ivh::ConvSpec conv_spec(const ivh_conv_desc * d, bool gemv)
+{
+  if (!d) throw std::invalid_argument("null conv descriptor");
+  if (d->cin < 1 || d->cout < 1 || d->h < 1 || d->w < 1 || d->k < 1 || d->stride < 1 || d->pad < 0 ||
+      d->groups < 1 || d->cin % d->groups || d->cout % d->groups || d->act < 0 || d->act > 5)
+    throw std::invalid_argument("conv descriptor: bad geometry");
+  ivh::ConvSpec s;
+  s.Cin = d->cin; s.Cout = d->cout; s.H = d->h; s.W = d->w;
+  s.K = d->k; s.S = d->stride; s.P = d->pad; s.G = d->groups;
+  s.act = d->act;
+  s.has_bias = d->has_bias != 0;
+  s.x_nhwc = d->channels_last != 0;
+  s.x_vec1 = gemv && d->cin % 8 == 0;
+  if (s.Ho() < 1 || s.Wo() < 1) throw std::invalid_argument("conv descriptor: empty output");
+  return s;
+}
+
+ivh::View tensor_view(const void * ptr, int C, int H, int W, bool nhwc)
+{
+  ivh::View v;
+  v.ptr = static_cast<__half *>(const_cast<void *>(ptr));
+  v.layout = nhwc ? ivh::kNHWC : ivh::kNCHW;
+  const int cs8 = (C + 7) / 8 * 8;
+  v.cs = nhwc ? cs8 : H * W;
+  v.img = nhwc ? (long)H * W * cs8 : (long)C * H * W;
+  return v;
+}
+
+void check_launch(const char * what)
+{
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) throw std::runtime_error(std::string("HIP error in ") + what + ": " + hipGetErrorString(e));
+}
+
+void check_batch(int batch)
+{
+  if (batch < 1 || batch > 65535) throw std::invalid_argument("batch must be in [1, 65535]");
+}
+
+void run_conv(const ivh_conv_desc * d, bool gemv, bool dw_only, const void * x, const void * packed, const void * res,
+              void * y, int batch, void * stream)
+{
+  const ivh::ConvSpec s = conv_spec(d, gemv);
+  const ivh::ConvPacking pk = ivh::conv_packing(s);
+  if (dw_only && pk.family != ivh::kFamDw) throw std::invalid_argument("not a depthwise conv (groups == cin == cout, k 3/5)");
+  if (gemv && (s.H != 1 || s.W != 1 || s.K != 1 || s.G != 1 || s.P != 0)) throw std::invalid_argument("gemv descriptor");
+  check_batch(batch);
+  if (!x || !packed || !y) throw std::invalid_argument("null operand");
+  ivh::ConvParams p;
+  p.batch = batch;
+  p.Cin = s.Cin; p.H = s.H; p.W = s.W;
+  p.Cout = s.Cout; p.Ho = s.Ho(); p.Wo = s.Wo();
+  p.K = s.K; p.S = s.S; p.P = s.P; p.G = s.G;
+  p.act = s.act;
+  p.x = tensor_view(x, s.Cin, s.H, s.W, s.x_nhwc);
+  p.y = tensor_view(y, s.Cout, p.Ho, p.Wo, s.x_nhwc);
+  if (res) p.r = tensor_view(res, s.Cout, p.Ho, p.Wo, s.x_nhwc);
+  if (gemv) {  // [batch][n] rows: one pixel per image, presented channels-last
+    for (ivh::View * v : {&p.x, &p.y, &p.r}) {
+      if (!v->ptr) continue;
+      const int C = v == &p.x ? s.Cin : s.Cout;
+      v->layout = ivh::kNHWC;
+      v->cs = (C + 7) / 8 * 8;
+      v->img = C;
+    }
+  }
+  const int k = ivh::conv_resolve(s, pk, packed, batch, nullptr, p);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (k == ivh::kLaunchIgemm) ivh::launch_conv_igemm(p, st);
+  else if (k == ivh::kLaunchDirect) ivh::launch_conv_direct(p, st);
+  else ivh::launch_dwconv(p, st);
+  check_launch("conv");
+}
+
+ivh::View flat_view(const void * ptr, long n)
+{
+  ivh::View v;
+  v.ptr = static_cast<__half *>(const_cast<void *>(ptr));
+  v.layout = ivh::kNCHW;
+  v.cs = (int)n;
+  v.img = n;
+  return v;
 }
 }  // namespace
 
@@ -246,6 +334,150 @@ int ivh_memory_info(const ivh_model * m, int batch, size_t * arena_bytes, size_t
   return guard([&] {
     if (arena_bytes) *arena_bytes = M(m).arenaBytes(batch);
     if (weight_bytes) *weight_bytes = M(m).weightBytes();
+  });
+}
+
+int ivh_conv_out_dims(const ivh_conv_desc * d, int * ho, int * wo)
+{
+  return guard([&] {
+    const ivh::ConvSpec s = conv_spec(d, false);
+    if (ho) *ho = s.Ho();
+    if (wo) *wo = s.Wo();
+  });
+}
+
+int ivh_conv_packed_bytes(const ivh_conv_desc * d, size_t * bytes)
+{
+  return guard([&] {
+    if (!bytes) throw std::invalid_argument("null bytes");
+    *bytes = ivh::conv_packing(conv_spec(d, d && d->h == 1 && d->w == 1 && d->k == 1)).bytes;
+  });
+}
+
+int ivh_pack_conv_weights(const ivh_conv_desc * d, const uint16_t * w_host, const uint16_t * bias_host,
+                          void * packed_dev)
+{
+  return guard([&] {
+    const ivh::ConvSpec s = conv_spec(d, d && d->h == 1 && d->w == 1 && d->k == 1);
+    if (!w_host || !packed_dev) throw std::invalid_argument("null operand");
+    if (s.has_bias && !bias_host) throw std::invalid_argument("has_bias set but bias is null");
+    const ivh::ConvPacking pk = ivh::conv_packing(s);
+    std::vector<uint8_t> blob;
+    ivh::conv_pack(s, pk, w_host, s.has_bias ? bias_host : nullptr, blob);
+    const hipError_t e = hipMemcpy(packed_dev, blob.data(), blob.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(e));
+  });
+}
+
+int ivh_conv2d_f16(const ivh_conv_desc * d, const void * x, const void * packed, const void * res, void * y,
+                   int batch, void * stream)
+{
+  return guard([&] { run_conv(d, false, false, x, packed, res, y, batch, stream); });
+}
+
+int ivh_dwconv_f16(const ivh_conv_desc * d, const void * x, const void * packed, const void * res, void * y,
+                   int batch, void * stream)
+{
+  return guard([&] { run_conv(d, false, true, x, packed, res, y, batch, stream); });
+}
+
+int ivh_gemv_f16(const ivh_conv_desc * d, const void * x, const void * packed, void * y, int batch, void * stream)
+{
+  return guard([&] { run_conv(d, true, false, x, packed, nullptr, y, batch, stream); });
+}
+
+int ivh_eltwise_f16(int op, const void * a, const void * b, int b_scalar, void * y, size_t n, int batch,
+                    void * stream)
+{
+  return guard([&] {
+    check_batch(batch);
+    if (!a || !y) throw std::invalid_argument("null operand");
+    if (n < 1 || n > (size_t)INT32_MAX) throw std::invalid_argument("element count out of range");
+    if (b ? (op < 0 || op > 3) : (op < 0 || op > 5)) throw std::invalid_argument("bad eltwise op");
+    ivh::SmallParams q;
+    q.batch = batch;
+    q.C = 1; q.H = 1; q.W = (int)n;
+    q.n = (long)n;
+    q.op = op;
+    q.a = flat_view(a, (long)n);
+    q.y = flat_view(y, (long)n);
+    int kind = ivh::kEwUnary;
+    if (b) {
+      q.b = flat_view(b, (long)n);
+      if (b_scalar) { q.b.img = 0; q.b.cs = 0; }
+      kind = ivh::kEwSame;
+    }
+    ivh::launch_small(kind, q, static_cast<hipStream_t>(stream));
+    check_launch("eltwise");
+  });
+}
+
+int ivh_pool_f16(int kind, const void * x, void * y, int c, int h, int w, int k, int s, int p, int batch,
+                 void * stream)
+{
+  return guard([&] {
+    check_batch(batch);
+    if (!x || !y) throw std::invalid_argument("null operand");
+    if (c < 1 || h < 1 || w < 1 || s < 1 || (kind != 0 && kind != 1)) throw std::invalid_argument("bad pool geometry");
+    ivh::SmallParams q;
+    q.batch = batch;
+    q.C = c; q.H = h; q.W = w;
+    if (kind == 0) {
+      if (k < 1 || p < 0 || p >= k) throw std::invalid_argument("bad maxpool window");
+      q.K = k; q.S = s; q.P = p;
+      q.Ho = (h + 2 * p - k) / s + 1;
+      q.Wo = (w + 2 * p - k) / s + 1;
+      if (q.Ho < 1 || q.Wo < 1) throw std::invalid_argument("empty maxpool output");
+    } else {
+      q.i0 = s;
+      q.Ho = h * s;
+      q.Wo = w * s;
+    }
+    q.a = tensor_view(x, c, h, w, false);
+    q.y = tensor_view(y, c, q.Ho, q.Wo, false);
+    ivh::launch_small(kind == 0 ? ivh::kMaxPool : ivh::kResizeNN, q, static_cast<hipStream_t>(stream));
+    check_launch("pool");
+  });
+}
+
+int ivh_softmax_f16(const void * x, void * y, int outer, int axis, int inner, int batch, void * stream)
+{
+  return guard([&] {
+    check_batch(batch);
+    if (!x || !y) throw std::invalid_argument("null operand");
+    if (outer < 1 || axis < 1 || inner < 1 || (long)outer * axis * inner > INT32_MAX)
+      throw std::invalid_argument("bad softmax geometry");
+    ivh::SmallParams q;
+    q.batch = batch;
+    q.i0 = outer; q.i1 = axis; q.i2 = inner;
+    const long n = (long)outer * axis * inner;
+    q.C = 1; q.H = 1; q.W = (int)n;
+    q.n = n;
+    q.a = flat_view(x, n);
+    q.y = flat_view(y, n);
+    ivh::launch_small(ivh::kSoftmax, q, static_cast<hipStream_t>(stream));
+    check_launch("softmax");
+  });
+}
+
+int ivh_bmm_f16(const void * a, const void * b, void * y, int bb, int m, int k, int n, int batch, void * stream)
+{
+  return guard([&] {
+    check_batch(batch);
+    if (!a || !b || !y) throw std::invalid_argument("null operand");
+    if (bb < 1 || m < 1 || k < 1 || n < 1 || (long)bb * m * n > INT32_MAX || (long)bb * m * k > INT32_MAX ||
+        (long)bb * k * n > INT32_MAX)
+      throw std::invalid_argument("bad bmm geometry");
+    ivh::SmallParams q;
+    q.batch = batch;
+    q.i0 = bb; q.i1 = m; q.i2 = k; q.i3 = n;
+    q.a = flat_view(a, (long)bb * m * k);
+    q.b = flat_view(b, (long)bb * k * n);
+    q.y = flat_view(y, (long)bb * m * n);
+    q.C = 1; q.H = 1; q.W = bb * m * n;
+    q.n = (long)bb * m * n;
+    ivh::launch_small(ivh::kBmm, q, static_cast<hipStream_t>(stream));
+    check_launch("bmm");
   });
 }
 

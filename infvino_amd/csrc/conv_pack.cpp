@@ -1,0 +1,206 @@
+// Convolution operands: family choice, packing and launch resolution (see conv_pack.hpp).
+// Packings restate the reference's weight layouts for this backend's kernels:
+//   implicit GEMM  fp16 [round_up(Cout,128)][kpad], k = (ky*K + kx)*cin8 + ci
+//   LDS patch      fp16 [round_up(Cout,128)][chunk][tap][ck] (3x3 stride 1 pad 1)
+//   stem           fp16 [ceil(Cout/16)*16][32], k = ci*9 + tap; and [16][64], k = tap*4 + ci
+//   direct         fp32 [G][Cin/G][K][K][Cout/G]
+//   depthwise      fp32 [K][K][C]
+// (the reference packs per kernel too: PlanModel.cpp:232-334).
+#include "conv_pack.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/ivh.h"
+#include "kernels.hpp"
+
+namespace ivh {
+
+namespace {
+
+long rup(long v, long m) { return (v + m - 1) / m * m; }
+
+float h2f_bits(uint16_t h)
+{
+  const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  uint32_t u;
+  if (e == 0) {
+    if (m == 0) u = s;
+    else {  // subnormal
+      int ee = -1;
+      uint32_t mm = m;
+      do { ++ee; mm <<= 1; } while (!(mm & 0x400));
+      u = s | ((uint32_t)(127 - 15 - ee) << 23) | ((mm & 0x3ff) << 13);
+    }
+  } else if (e == 31) u = s | 0x7f800000u | (m << 13);
+  else u = s | ((e + 112) << 23) | (m << 13);
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+int halo_index(int ck) { return ck == 16 ? 0 : (ck == 32 ? 1 : 2); }
+
+}  // namespace
+
+ConvPacking conv_packing(const ConvSpec & s)
+{
+  if (s.Cin < 1 || s.Cout < 1 || s.G < 1 || s.Cin % s.G || s.Cout % s.G || s.K < 1 || s.S < 1 || s.P < 0)
+    throw std::runtime_error("conv geometry");
+  ConvPacking pk;
+  const int cin_g = s.Cin / s.G;
+  const bool dw = s.G > 1 && s.G == s.Cin && s.Cout == s.Cin && (s.K == 3 || s.K == 5);
+  if (dw) pk.family = kFamDw;
+  else if (s.G == 1 && (s.x_nhwc || s.x_vec1)) pk.family = kFamIgemm;
+  else pk.family = kFamDirect;
+  if (s.flags & IVH_FLAG_DIRECT_ONLY) pk.family = dw ? kFamDw : kFamDirect;
+
+  size_t off = 0;
+  auto seg = [&](size_t bytes) {
+    const size_t o = off;
+    off = rup((long)(off + bytes), 256);
+    return o;
+  };
+  if (s.has_bias) pk.bias = seg((size_t)(rup(s.Cout, kIgemmRowPad) + 16) * 4);
+  if (pk.family == kFamIgemm) {
+    const int rows = (int)rup(s.Cout, kIgemmRowPad);
+    pk.cin8 = (int)rup(cin_g, 8);
+    pk.kpad = igemm_kpad(s.Cout, s.K * s.K * pk.cin8);
+    pk.w = seg((size_t)rows * pk.kpad * 2);
+    if (s.K == 3 && s.S == 1 && s.P == 1 && s.x_nhwc && !(s.flags & IVH_FLAG_NO_HALO)) {
+      for (int cfg : {0, 7}) {  // every chunk size some tile config may use for this Cin
+        const int ck = halo_cfg_ck(cfg, cin_g), hi = halo_index(ck);
+        if (pk.halo[hi] != kNoSeg) continue;
+        pk.kpad_halo[hi] = (cin_g + ck - 1) / ck * halo_taps(ck) * ck;
+        pk.halo[hi] = seg((size_t)rows * pk.kpad_halo[hi] * 2);
+      }
+    }
+  } else if (pk.family == kFamDirect && s.G == 1 && cin_g <= 3 && s.K == 3 && s.Cout <= 32) {
+    const int rows = (s.Cout + 15) / 16 * 16;
+    pk.stem = true;
+    pk.w = seg(((size_t)rows * 32 + 16 * 64) * 2);
+    if (s.Cout <= 16) pk.stem_w2 = pk.w + (size_t)rows * 32 * 2;
+  } else if (pk.family == kFamDirect) {
+    pk.w = seg(((size_t)s.G * cin_g * s.K * s.K * (s.Cout / s.G) + 32) * 4);
+  } else {
+    pk.w = seg(((size_t)s.K * s.K * s.Cout + 8) * 4);
+  }
+  pk.bytes = off;
+  return pk;
+}
+
+void conv_pack(const ConvSpec & s, const ConvPacking & pk, const uint16_t * W, const uint16_t * B,
+               std::vector<uint8_t> & blob)
+{
+  blob.assign(pk.bytes, 0);
+  const int Cout = s.Cout, K = s.K, G = s.G, cin_g = s.Cin / s.G;
+  auto at = [&](int co, int ci, int t) { return W[((size_t)co * cin_g + ci) * K * K + t]; };
+  if (pk.bias != kNoSeg) {
+    float * bf = reinterpret_cast<float *>(blob.data() + pk.bias);
+    for (int c = 0; c < Cout; ++c) bf[c] = B ? h2f_bits(B[c]) : 0.0f;
+  }
+  if (pk.family == kFamIgemm) {
+    uint16_t * P = reinterpret_cast<uint16_t *>(blob.data() + pk.w);
+    for (int co = 0; co < Cout; ++co)
+      for (int ci = 0; ci < cin_g; ++ci)
+        for (int t = 0; t < K * K; ++t) P[(size_t)co * pk.kpad + t * pk.cin8 + ci] = at(co, ci, t);
+    for (int hi = 0; hi < 3; ++hi) {
+      if (pk.halo[hi] == kNoSeg) continue;
+      const int ck = hi == 0 ? 16 : (hi == 1 ? 32 : 64), taps = halo_taps(ck), kh = pk.kpad_halo[hi];
+      uint16_t * Q = reinterpret_cast<uint16_t *>(blob.data() + pk.halo[hi]);
+      for (int co = 0; co < Cout; ++co)
+        for (int ci = 0; ci < cin_g; ++ci)
+          for (int t = 0; t < 9; ++t) Q[(size_t)co * kh + ((ci / ck) * taps + t) * ck + (ci % ck)] = at(co, ci, t);
+    }
+  } else if (pk.stem) {
+    uint16_t * P = reinterpret_cast<uint16_t *>(blob.data() + pk.w);
+    for (int co = 0; co < Cout; ++co)
+      for (int k = 0; k < cin_g * 9; ++k) P[(size_t)co * 32 + k] = W[(size_t)co * cin_g * 9 + k];
+    if (pk.stem_w2 != kNoSeg) {
+      uint16_t * P2 = reinterpret_cast<uint16_t *>(blob.data() + pk.stem_w2);
+      for (int co = 0; co < Cout; ++co)
+        for (int ci = 0; ci < cin_g; ++ci)
+          for (int t = 0; t < 9; ++t) P2[co * 64 + t * 4 + ci] = at(co, ci, t);
+    }
+  } else if (pk.family == kFamDirect) {
+    float * P = reinterpret_cast<float *>(blob.data() + pk.w);
+    const int cout_g = Cout / G;
+    for (int co = 0; co < Cout; ++co) {
+      const int g = co / cout_g, cl = co % cout_g;
+      for (int ci = 0; ci < cin_g; ++ci)
+        for (int t = 0; t < K * K; ++t)
+          P[(((size_t)g * cin_g + ci) * K * K + t) * cout_g + cl] = h2f_bits(at(co, ci, t));
+    }
+  } else {
+    float * P = reinterpret_cast<float *>(blob.data() + pk.w);
+    for (int c = 0; c < Cout; ++c)
+      for (int t = 0; t < K * K; ++t) P[(size_t)t * Cout + c] = h2f_bits(W[(size_t)c * K * K + t]);
+  }
+}
+
+int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_blob, int batch, float * ws,
+                 ConvParams & p)
+{
+  const char * base = static_cast<const char *>(dev_blob);
+  p.bias = pk.bias != kNoSeg ? reinterpret_cast<const float *>(base + pk.bias) : nullptr;
+  p.w = reinterpret_cast<const __half *>(base + pk.w);
+  if (pk.family == kFamDw) return kLaunchDw;
+  if (pk.family == kFamDirect) {
+    p.stem_mfma = pk.stem ? 1 : 0;
+    if (pk.stem && pk.stem_w2 != kNoSeg) p.w2 = reinterpret_cast<const __half *>(base + pk.stem_w2);
+    return kLaunchDirect;
+  }
+  p.cin8 = pk.cin8;
+  p.kpad = pk.kpad;
+  p.bk = igemm_bk(p.Cout, p.K * p.K * p.cin8);
+  p.ksplit = 1;
+  p.ws = nullptr;
+  if (ws) {
+    p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
+    if (p.ksplit > 1) p.ws = ws;
+  }
+  // LDS-patch kernel when its grid fills the chip; otherwise im2col (+ split-K)
+  int hc, th, tw;
+  if (p.K == 3 && p.S == 1 && p.P == 1 && halo_plan(p.Cin, p.Cout, p.H, p.W, batch, &hc, &th, &tw)) {
+    const int ck = halo_cfg_ck(hc, p.Cin), hi = halo_index(ck);
+    if (pk.halo[hi] != kNoSeg) {
+      ConvParams q = p;
+      q.th = th;
+      q.tw = tw;
+      const long wgs = halo_grid_x(q) * ((p.Cout + halo_bn(hc) - 1) / halo_bn(hc));
+      if (wgs >= 160 || p.ksplit == 1) {
+        p.halo = hc + 1;
+        p.th = th;
+        p.tw = tw;
+        p.ck = ck;
+        p.ksplit = 1;
+        p.ws = nullptr;
+        p.w = reinterpret_cast<const __half *>(base + pk.halo[hi]);
+        p.kpad = pk.kpad_halo[hi];
+      }
+    }
+  }
+  if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) || (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
+    throw std::runtime_error("implicit-GEMM input view not 16-byte aligned NHWC");
+  if (p.kpad < p.K * p.K * p.cin8 || p.cin8 < p.Cin) throw std::runtime_error("packed weight geometry");
+  (void)s;
+  return kLaunchIgemm;
+}
+
+size_t conv_splitk_floats(const ConvSpec & s, const ConvPacking & pk, int max_batch)
+{
+  if (pk.family != kFamIgemm) return 0;
+  const long hwo = (long)s.Ho() * s.Wo();
+  const int bn = igemm_bn(s.Cout);
+  const long npad = (long)(s.Cout + bn - 1) / bn * bn;
+  size_t need = 0;
+  for (int b = 1; b <= max_batch; ++b) {
+    const int ks = igemm_ksplit((long)b * hwo, s.Cout, pk.kpad);
+    if (ks > 1) need = std::max(need, (size_t)ks * npad * b * hwo);
+  }
+  return need;
+}
+
+}  // namespace ivh

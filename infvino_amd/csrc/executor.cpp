@@ -702,117 +702,51 @@ void Model::uploadWeights()
     const Tensor & wt = *T_[wname];
     if (wt.kind != Tensor::kInit) throw std::runtime_error("conv weight is not an init: " + wname);
     const std::vector<uint16_t> & W = host[wname];
-    const int Cout = (int)wt.dims.at(0);
-    const int K = is1 ? 1 : (is3 ? 3 : n.i("K", 3));
-    const int G = isg ? n.i("G", 1) : 1;
-    const int cin_g = (int)(wt.numel / ((long)Cout * K * K));
-    const std::string bname = n.ins.size() > 2 ? n.ins[2] : "-";
-    Packed pk;
-    if (bname != "-") {
-      const auto & B = host.at(bname);
-      if ((long)B.size() < Cout) throw std::runtime_error("bias too short: " + bname);
-      std::vector<float> bf(round_up(Cout, kIgemmRowPad) + 16, 0.0f);
-      for (int c = 0; c < Cout; ++c) bf[c] = h2f(B[c]);
-      pk.bias = static_cast<float *>(upload(bf.data(), bf.size() * 4));
-    }
-    // kernel family decided here (layouts are known): 0 igemm, 1 direct, 2 depthwise
+    ConvSpec cs;
+    cs.Cout = (int)wt.dims.at(0);
+    cs.K = is1 ? 1 : (is3 ? 3 : n.i("K", 3));
+    cs.G = isg ? n.i("G", 1) : 1;
+    const int cin_g = (int)(wt.numel / ((long)cs.Cout * cs.K * cs.K));
     const Tensor & x = *T_[is1 ? n.ins.at(1) : n.ins.at(0)];
-    const int Cin = is1 ? (int)wt.dims.at(1) : x.C;
-    const bool dw = isg && G == Cin && Cout == Cin && (K == 3 || K == 5);
-    const Root & xr = *roots_[x.root < 0 ? 0 : x.root];
-    const bool x_nhwc = x.kind == Tensor::kAct && xr.layout == kNHWC && (x.coff % 8) == 0;
-    long Nx = is1 ? x.numel / std::max(Cin, 1) : (long)x.H * x.W;
-    const bool x_vec1 = is1 && Nx == 1 && x.kind != Tensor::kInit && (x.eoff % 8) == 0 && xr.layout == kNCHW;
-    int kind;
-    if (dw) kind = 2;
-    else if (G == 1 && (x_nhwc || x_vec1)) kind = 0;
-    else kind = 1;
-    if (flags_ & IVH_FLAG_DIRECT_ONLY) kind = dw ? 2 : 1;
-    pk.kind = kind;
-    if (kind == 0) {
-      const int cin8 = (int)round_up(cin_g, 8);
-      const int kpad = igemm_kpad(Cout, K * K * cin8);
-      const int rows = (int)round_up(Cout, kIgemmRowPad);
-      std::vector<uint16_t> P((size_t)rows * kpad, 0);
-      for (int co = 0; co < Cout; ++co)
-        for (int ci = 0; ci < cin_g; ++ci)
-          for (int ky = 0; ky < K; ++ky)
-            for (int kx = 0; kx < K; ++kx)
-              P[(size_t)co * kpad + (ky * K + kx) * cin8 + ci] = W[(((size_t)co * cin_g + ci) * K + ky) * K + kx];
-      pk.w = upload(P.data(), P.size() * 2);
-      pk.cin8 = cin8;
-      pk.kpad = kpad;
-      // 3x3 stride 1 pad 1: also pack [co][chunk][tap][ck] for the LDS-patch kernel
-      const int S = is3 ? n.i("stride", 1) : n.i("S", 1);
-      const int pad = is3 ? n.i("pad", 1) : n.i("P", 1);
-      if (K == 3 && S == 1 && pad == 1 && x_nhwc && !(flags_ & IVH_FLAG_NO_HALO)) {
-        // every chunk size some tile config may use for this Cin
-        for (int cfg : {0, 7}) {
-          const int ck = halo_cfg_ck(cfg, cin_g), taps = halo_taps(ck), ci = ck == 16 ? 0 : (ck == 32 ? 1 : 2);
-          if (pk.w_halo[ci]) continue;
-          const int nch = (cin_g + ck - 1) / ck;
-          const int kh = nch * taps * ck;
-          std::vector<uint16_t> Q((size_t)rows * kh, 0);
-          for (int co = 0; co < Cout; ++co)
-            for (int c = 0; c < cin_g; ++c)
-              for (int t = 0; t < 9; ++t)
-                Q[(size_t)co * kh + ((c / ck) * taps + t) * ck + (c % ck)] = W[((size_t)co * cin_g + c) * 9 + t];
-          pk.w_halo[ci] = upload(Q.data(), Q.size() * 2);
-          pk.kpad_halo[ci] = kh;
-        }
-        pk.halo = true;
-      }
-    } else if (kind == 1 && G == 1 && cin_g <= 3 && K == 3 && Cout <= 32) {
-      // stem: fp16 [ceil(Cout/16)*16][32], row co = the plan's w[co][ci][ky][kx] flattened;
-      // for Cout <= 16 followed by the row-tiled kernel's [16][64] with k = tap*4 + ci
-      const int rows = (Cout + 15) / 16 * 16;
-      std::vector<uint16_t> P((size_t)rows * 32 + 16 * 64, 0);
-      for (int co = 0; co < Cout; ++co)
-        for (int k = 0; k < cin_g * 9; ++k) P[(size_t)co * 32 + k] = W[(size_t)co * cin_g * 9 + k];
-      if (Cout <= 16) {
-        for (int co = 0; co < Cout; ++co)
-          for (int ci = 0; ci < cin_g; ++ci)
-            for (int t = 0; t < 9; ++t)
-              P[(size_t)rows * 32 + co * 64 + t * 4 + ci] = W[((size_t)co * cin_g + ci) * 9 + t];
-        pk.stem_w2 = rows * 32;
-      }
-      pk.w = upload(P.data(), P.size() * 2);
-      pk.stem = true;
-    } else if (kind == 1) {
-      const int cout_g = Cout / G;
-      std::vector<float> P((size_t)G * cin_g * K * K * cout_g + 32, 0.0f);
-      for (int co = 0; co < Cout; ++co) {
-        const int g = co / cout_g, cl = co % cout_g;
-        for (int ci = 0; ci < cin_g; ++ci)
-          for (int t = 0; t < K * K; ++t)
-            P[(((size_t)g * cin_g + ci) * K * K + t) * cout_g + cl] = h2f(W[((size_t)co * cin_g + ci) * K * K + t]);
-      }
-      pk.w = upload(P.data(), P.size() * 4);
+    cs.Cin = is1 ? (int)wt.dims.at(1) : cin_g * cs.G;
+    if (is1) {
+      const long N = x.numel / std::max(cs.Cin, 1);
+      if (x.dims.size() == 4 && (long)x.H * x.W == N && x.C == cs.Cin) { cs.H = x.H; cs.W = x.W; }
+      else { cs.H = (int)N; cs.W = 1; }
     } else {
-      std::vector<float> P((size_t)K * K * Cout + 8, 0.0f);
-      for (int c = 0; c < Cout; ++c)
-        for (int t = 0; t < K * K; ++t) P[(size_t)t * Cout + c] = h2f(W[(size_t)c * K * K + t]);
-      pk.w = upload(P.data(), P.size() * 4);
+      cs.H = x.H;
+      cs.W = x.W;
+      cs.S = is3 ? n.i("stride", 1) : n.i("S", 1);
+      cs.P = is3 ? n.i("pad", 1) : n.i("P", 1);
     }
+    cs.act = n.i("act");
+    const std::string bname = n.ins.size() > 2 ? n.ins[2] : "-";
+    cs.has_bias = bname != "-";
+    const uint16_t * B = nullptr;
+    if (cs.has_bias) {
+      const auto & Bv = host.at(bname);
+      if ((long)Bv.size() < cs.Cout) throw std::runtime_error("bias too short: " + bname);
+      B = Bv.data();
+    }
+    // kernel family decided here, where layouts are known
+    const Root & xr = *roots_[x.root < 0 ? 0 : x.root];
+    cs.x_nhwc = x.kind == Tensor::kAct && xr.layout == kNHWC && (x.coff % 8) == 0;
+    cs.x_vec1 = is1 && (long)cs.H * cs.W == 1 && x.kind != Tensor::kInit && (x.eoff % 8) == 0 && xr.layout == kNCHW;
+    cs.flags = flags_;
+    Packed pk;
+    pk.spec = cs;
+    pk.pk = conv_packing(cs);
+    std::vector<uint8_t> blob;
+    conv_pack(cs, pk.pk, W.data(), B, blob);
+    pk.dev = upload(blob.data(), blob.size());
     packed_[ni] = pk;
   }
   // split-K workspace: the largest need over every node and every batch size, so launch
   // lists and captured graphs of different batch sizes share one fixed buffer
   size_t need = 0;
-  if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
-    for (size_t ni = 0; ni < nodes_.size(); ++ni) {
-      if (packed_[ni].kind != 0 || !packed_[ni].w) continue;
-      const Tensor & y = *T_[nodes_[ni].outs[0]];
-      const int cout = y.numel > 0 ? (int)T_[nodes_[ni].op == "conv1x1" ? nodes_[ni].ins[0] : nodes_[ni].ins[1]]->dims[0] : 0;
-      const long hwo = cout > 0 ? y.numel / cout : 0;
-      const int bn = igemm_bn(cout);
-      const long npad = (long)(cout + bn - 1) / bn * bn;
-      for (int b = 1; b <= max_batch_; ++b) {
-        const int ks = igemm_ksplit((long)b * hwo, cout, packed_[ni].kpad);
-        if (ks > 1) need = std::max(need, (size_t)ks * npad * b * hwo);
-      }
-    }
-  }
+  if (!(flags_ & IVH_FLAG_NO_SPLITK))
+    for (size_t ni = 0; ni < nodes_.size(); ++ni)
+      if (packed_[ni].dev) need = std::max(need, conv_splitk_floats(packed_[ni].spec, packed_[ni].pk, max_batch_));
   if (need) {
     ws_ = static_cast<float *>(devAlloc(need * 4, false));
     ws_floats_ = need;
@@ -885,8 +819,6 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
     if (yt.numel != (long)p.Cout * p.Ho * p.Wo) fail("output numel mismatch");
     p.act = n.i("act");
-    p.bias = pk.bias;
-    p.w = static_cast<const __half *>(pk.w);
     p.x = view(xt.name, batch);
     p.y = view(yt.name, batch);
     if (has(3)) {
@@ -898,47 +830,16 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     auto pix1 = [](View & v, int C) { v.layout = kNHWC; v.cs = (int)round_up(C, 8); };
     if (p.H * p.W == 1) pix1(p.x, p.Cin);
     if (p.Ho * p.Wo == 1) { pix1(p.y, p.Cout); if (p.r.ptr) pix1(p.r, p.Cout); }
-    if (pk.kind == 0) {
-      L.kind = Launch::kIgemm;
-      p.cin8 = pk.cin8;
-      p.kpad = pk.kpad;
-      p.bk = igemm_bk(p.Cout, p.K * p.K * p.cin8);
-      if (!(flags_ & IVH_FLAG_NO_SPLITK)) {
-        p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
-        if (p.ksplit > 1) p.ws = ws_;
-      }
-      // LDS-patch kernel when its grid fills the chip; otherwise im2col (+ split-K)
-      int hc, th, tw;
-      if (pk.halo && p.K == 3 && p.S == 1 && p.P == 1 &&
-          halo_plan(p.Cin, p.Cout, p.H, p.W, batch, &hc, &th, &tw)) {
-        ConvParams q = p;
-        q.th = th;
-        q.tw = tw;
-        const long wgs = halo_grid_x(q) * ((p.Cout + halo_bn(hc) - 1) / halo_bn(hc));
-        if (wgs >= 160 || p.ksplit == 1) {
-          const int ck = halo_cfg_ck(hc, p.Cin), ci = ck == 16 ? 0 : (ck == 32 ? 1 : 2);
-          if (!pk.w_halo[ci]) fail("halo packing missing for chunk size " + std::to_string(ck));
-          p.halo = hc + 1;
-          p.th = th;
-          p.tw = tw;
-          p.ck = ck;
-          p.ksplit = 1;
-          p.ws = nullptr;
-          p.w = static_cast<const __half *>(pk.w_halo[ci]);
-          p.kpad = pk.kpad_halo[ci];
-        }
-      }
-      if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) ||
-          (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
-        fail("implicit-GEMM input view not 16-byte aligned NHWC");
-      if (p.kpad < p.K * p.K * p.cin8 || p.cin8 < p.Cin) fail("packed weight geometry");
-    } else if (pk.kind == 1) {
-      L.kind = Launch::kDirect;
-      p.stem_mfma = pk.stem ? 1 : 0;
-      if (pk.stem && pk.stem_w2 > 0) p.w2 = static_cast<const __half *>(pk.w) + pk.stem_w2;
-    } else {
-      L.kind = Launch::kDw;
+    if (!pk.dev || pk.spec.Cin != p.Cin || pk.spec.Cout != p.Cout || pk.spec.H != p.H || pk.spec.W != p.W ||
+        pk.spec.K != p.K || pk.spec.G != p.G || pk.spec.Ho() != p.Ho || pk.spec.Wo() != p.Wo)
+      fail("packed conv geometry");
+    int k;
+    try {
+      k = conv_resolve(pk.spec, pk.pk, pk.dev, batch, (flags_ & IVH_FLAG_NO_SPLITK) ? nullptr : ws_, p);
+    } catch (const std::exception & e) {
+      fail(e.what());
     }
+    L.kind = k == kLaunchIgemm ? Launch::kIgemm : (k == kLaunchDirect ? Launch::kDirect : Launch::kDw);
     out.push_back(L);
     return;
   }
@@ -1574,7 +1475,7 @@ void Model::buildStats()
       const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
       const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
       s.flops = 2.0 * wt.numel * (double)y.numel / std::max<int64_t>(wt.dims[0], 1);
-      const int kind = packed_[ni].kind;
+      const int kind = packed_[ni].pk.family;
       s.kernel = kind == 0 ? "conv_igemm" : (kind == 1 ? "conv_direct" : "dwconv");
       std::snprintf(buf, sizeof(buf), "%s %dx%dx%d->%dx%dx%d k%d s%d g%d act%d%s", n.op.c_str(), xt.C, xt.H, xt.W,
                     y.C, y.H, y.W, is1 ? 1 : (n.op == "conv3x3" ? 3 : n.i("K", 3)),

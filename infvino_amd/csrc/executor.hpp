@@ -10,6 +10,7 @@
 #include <string>
 #include <vector>
 
+#include "conv_pack.hpp"
 #include "ivh_internal.hpp"
 
 namespace ivh {
@@ -119,17 +120,9 @@ class Model {
   size_t weight_bytes_ = 0;
   std::map<std::string, void *> init_dev_;  // raw fp16 inits
   struct Packed {
-    void * w = nullptr;
-    float * bias = nullptr;
-    int kind = 0;
-    int kpad = 0, cin8 = 0;
-    bool stem = false;  // direct conv with Cin <= 3, 3x3: fp16 MFMA stem packing
-    long stem_w2 = 0;   // element offset of the row-tiled stem packing in w (0: none)
-    // 3x3 s1 pad 1: [co][chunk][tap][ck] packings for the LDS-patch kernel, by chunk size
-    // ck = 16 / 32 / 64 (index 0 / 1 / 2); null where not packed
-    void * w_halo[3] = {nullptr, nullptr, nullptr};
-    int kpad_halo[3] = {0, 0, 0};
-    bool halo = false;
+    ConvSpec spec;
+    ConvPacking pk;
+    void * dev = nullptr;  // device copy of the packed operand blob
   };
   std::vector<Packed> packed_;              // per node
   float * ws_ = nullptr;                    // split-K partials
