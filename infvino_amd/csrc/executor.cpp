@@ -151,6 +151,7 @@ Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t 
   if (!(flags_ & IVH_FLAG_NO_FUSE)) {
     fuseResidual();
     fuseActivation();
+    fusePermuteMatmul();
   }
   plan();
   if (!dry_) HIPCHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
@@ -333,6 +334,45 @@ void Model::fuseActivation()
     c.outs[0] = u.outs[0];
     producer[u.outs[0]] = pit->second;
     remove[i] = 1;
+  }
+  std::vector<PlanNode> kept;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if (!remove[i]) kept.push_back(std::move(nodes_[i]));
+  nodes_ = std::move(kept);
+}
+
+// permute_0213 swapping the last two dimensions (mode 1) whose only consumer is a bmm operand
+// -> the bmm reads the permute's input as a transposed operand (attr ta / tb), and the
+// permute launches nothing.  The C2PSA attention's q^T and attn^T (YOLO11n) are such pairs.
+void Model::fusePermuteMatmul()
+{
+  if (flags_ & IVH_FLAG_NO_FUSE) return;
+  std::map<std::string, int> producer, uses;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & o : nodes_[i].outs) producer[o] = (int)i;
+  for (const auto & n : nodes_)
+    for (const auto & in : n.ins)
+      if (in != "-") ++uses[in];
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  std::vector<char> remove(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    PlanNode & m = nodes_[i];
+    if (m.op != "bmm" || m.ins.size() < 2) continue;
+    for (int j = 0; j < 2; ++j) {
+      auto pit = producer.find(m.ins[j]);
+      if (pit == producer.end() || remove[pit->second]) continue;
+      const PlanNode & pn = nodes_[pit->second];
+      if (pn.op != "permute_0213" || pn.i("mode") != 1 || uses[m.ins[j]] != 1 || outs.count(m.ins[j])) continue;
+      const Tensor & src = *T_[pn.ins.at(0)];
+      const Tensor & dst = *T_[m.ins[j]];
+      // [.., D2, I] -> [.., I, D2]: the source's last two dims are the operand's, swapped
+      if (src.dims.size() < 2 || dst.dims.size() != src.dims.size() || src.numel != dst.numel ||
+          src.dims.back() != dst.dims[dst.dims.size() - 2] || dst.dims.back() != src.dims[src.dims.size() - 2])
+        continue;
+      m.ins[j] = pn.ins[0];
+      m.attr[j == 0 ? "ta" : "tb"] = "1";
+      remove[pit->second] = 1;
+    }
   }
   std::vector<PlanNode> kept;
   for (size_t i = 0; i < nodes_.size(); ++i)
@@ -1073,11 +1113,16 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     const auto & ad = at.dims;
     const auto & bd = bt.dims;
     if (ad.size() < 2 || bd.size() < 2) fail("matmul rank");
-    const int M = (int)ad[ad.size() - 2], K = (int)ad.back(), Nn = (int)bd.back();
+    // operands folded from a last-two-dims permute are stored transposed (fusePermuteMatmul)
+    const bool ta = n.i("ta") == 1, tb = n.i("tb") == 1;
+    const int M = (int)(ta ? ad.back() : ad[ad.size() - 2]), K = (int)(ta ? ad[ad.size() - 2] : ad.back());
+    const int Nn = (int)(tb ? bd[bd.size() - 2] : bd.back()), Kb = (int)(tb ? bd.back() : bd[bd.size() - 2]);
+    if (Kb != K) fail("matmul inner dimensions differ");
     const long BB = at.numel / ((long)M * K);
-    if ((long)K * Nn * BB != bt.numel && !((long)K * Nn == bt.numel && BB == 1)) fail("matmul operand shapes");
+    if ((long)K * Nn * BB != bt.numel) fail("matmul operand shapes");
     if (BB * M * Nn != yt.numel) fail("matmul output numel");
     q.i0 = (int)BB; q.i1 = M; q.i2 = K; q.i3 = Nn;
+    q.op = (ta ? 1 : 0) | (tb ? 2 : 0);
     if (q.a.layout != kNCHW || q.b.layout != kNCHW || q.y.layout != kNCHW) fail("matmul needs NCHW");
     L.small = kBmm;
     out.push_back(L);
@@ -1232,6 +1277,7 @@ void Model::validate(const Launch & l) const
     flat(q.y, q.C, "gap y");
     break;
   case kBmm:
+    if ((long)q.batch * q.i0 > 65535) throw std::runtime_error("bmm batch x heads exceeds the grid");
     flat(q.a, (long)q.i0 * q.i1 * q.i2, "bmm a");
     flat(q.b, (long)q.i0 * q.i2 * q.i3, "bmm b");
     flat(q.y, (long)q.i0 * q.i1 * q.i3, "bmm y");

@@ -83,6 +83,7 @@ class Model {
   void parse(const std::string & path);
   void fuseResidual();
   void fuseActivation();
+  void fusePermuteMatmul();
   void plan();
   int chanBroadcast(const PlanNode & n) const;
   void assignViews();

@@ -46,10 +46,12 @@ enum SmallOp : int {
   kSoftmax,        // NCHW flat: i0 outer, i1 axdim, i2 inner
   kPermute,        // NCHW flat: i0 D1, i1 D2, i2 I, op = mode
   kGap,            // a view [C,H,W] -> y flat [C]
-  kBmm,            // NCHW flat: i0 BB, i1 M, i2 K, i3 N  (a: [BB][M][K], b: [BB][K][N])
+  kBmm,            // NCHW flat: i0 BB, i1 M, i2 K, i3 N  (a: [BB][M][K], b: [BB][K][N]);
+                   // op bit 0: a stored [BB][K][M], bit 1: b stored [BB][N][K]
   kBiasAdd,        // NCHW flat: i0 HW
 };
 void launch_small(int kind, const SmallParams & p, hipStream_t s);
+void launch_bmm_mfma(const SmallParams & q, hipStream_t s);  // bmm_mfma.hip
 
 // boundary conversions (include/infvino/Half.hpp semantics for the truncating one)
 void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t s);

@@ -717,21 +717,6 @@ __global__ void __launch_bounds__(256) gap_kernel(const SmallParams q)
 }
 
 // bmm (ops.cl:276-294): fp32 accumulation, one lane per output.
-__global__ void bmm_kernel(const SmallParams q)
-{
-  const long total = (long)q.i0 * q.i1 * q.i3;
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const int b = blockIdx.y;
-  if (i >= total) return;
-  const long n = i % q.i3, t = i / q.i3;
-  const long m = t % q.i1, bb = t / q.i1;
-  const _Float16 * A = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img + (bb * q.i1 + m) * q.i2;
-  const _Float16 * B = reinterpret_cast<const _Float16 *>(q.b.ptr) + (long)b * q.b.img + bb * q.i2 * q.i3 + n;
-  float acc = 0.0f;
-  for (int k = 0; k < q.i2; ++k) acc += (float)A[k] * (float)B[(long)k * q.i3];
-  reinterpret_cast<_Float16 *>(q.y.ptr)[(long)b * q.y.img + i] = (_Float16)acc;
-}
-
 __global__ void bias_add_kernel(const SmallParams q)  // ops.cl:268-274
 {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1100,9 +1085,7 @@ void launch_small(int kind, const SmallParams & q, hipStream_t s)
     hipLaunchKernelGGL(permute_kernel, dim3(nblk((long)q.i0 * q.i1 * q.i2, 256), B), blk, 0, s, q);
     break;
   case kGap: hipLaunchKernelGGL(gap_kernel, dim3((unsigned)((q.C + 3) / 4), B), blk, 0, s, q); break;
-  case kBmm:
-    hipLaunchKernelGGL(bmm_kernel, dim3(nblk((long)q.i0 * q.i1 * q.i3, 256), B), blk, 0, s, q);
-    break;
+  case kBmm: launch_bmm_mfma(q, s); break;
   case kBiasAdd: hipLaunchKernelGGL(bias_add_kernel, dim3(nblk(q.n, 256), B), blk, 0, s, q); break;
   default: break;
   }
