@@ -11,6 +11,8 @@ table goes to stderr.
   conv_mfma_frac all conv FLOPs of a step / conv device time / dense fp16 MFMA peak
   conv_sweep     the conv operator sweep (stem, strided / stride-1 3x3, depthwise) at the
                  same batch: per layer time, TFLOP/s, GB/s and fraction of its binding roof
+  other_models   MobileNetV3-small 224 (batch 1 / 32 / 256) and YOLO11n-pose 640 (batch 1 /
+                 64): images/s of graph replays and batch-1 latency
   cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
                  workload on this host's cores -- a reported baseline, not a target
 """
@@ -87,6 +89,45 @@ def conv_sweep(ia, pw, batch, iters):
     return rows
 
 
+def model_lines(ia, pw, specs, steps, warmup):
+    """The other model configurations: images/s of graph replays at each batch (inputs
+    resident in HBM) and the synchronous batch-1 latency."""
+    out = {}
+    for name, imgsz, batches in specs:
+        tmp = tempfile.TemporaryDirectory()
+        path, flops = pw.MODELS[name](tmp.name, seed=0, imgsz=imgsz)
+        row = {"imgsz": imgsz, "gflop_per_image": round(flops / 1e9, 3)}
+        bmax = max(batches)
+        x = np.random.default_rng(0).random(3 * imgsz * imgsz * bmax, dtype=np.float32).astype(np.float16)
+        m = ia.PlanModel(path, 0, bmax, ia.IVH_FLAG_ASYNC)
+        m.setInput(x.view(np.uint16), bmax)
+        for b in batches:
+            for _ in range(warmup):
+                m.run(b)
+            m.sync()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m.run(b)
+            m.sync()
+            row[f"images_per_s_b{b}"] = round(b * steps / (time.perf_counter() - t0), 1)
+        m.close()
+        m1 = ia.PlanModel(path, 0, 1, 0)
+        m1.setInput(x.view(np.uint16)[:3 * imgsz * imgsz], 1)
+        for _ in range(warmup):
+            m1.run(1)
+        lat = []
+        for _ in range(steps):
+            t = time.perf_counter()
+            m1.run(1)
+            lat.append(time.perf_counter() - t)
+        m1.close()
+        row["latency_b1_ms"] = round(float(np.mean(lat)) * 1e3, 4)
+        out[name] = row
+        log(f"[models] {name}@{imgsz}: " + ", ".join(f"{k}={v}" for k, v in row.items()))
+        tmp.cleanup()
+    return out
+
+
 def measured_traffic(node_desc, batch):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
     summary (profiles/traffic_dominant_kernel.md), when it was measured on this node."""
@@ -116,6 +157,7 @@ def main():
     ap.add_argument("--cpu-images", type=int, default=-1, help="oracle sample size (-1: ~15 s worth)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-layer conv sweep")
+    ap.add_argument("--no-models", action="store_true", help="skip the MobileNetV3 / YOLO11n lines")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch node by node instead of replaying the captured HIP graph")
     ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep"],
@@ -216,6 +258,8 @@ def main():
     m1.close()
 
     sweep = None if args.no_sweep else conv_sweep(ia, pw, B, max(args.profile_iters, 10))
+    others = None if args.no_models else model_lines(
+        ia, pw, [("mobilenetv3-small", 224, (1, 32, 256)), ("yolo11n-pose", 640, (1, 64))], 20, 5)
 
     # ---- CPU baseline: the oracle on a bounded sample of the same workload
     cpu = None
@@ -256,6 +300,7 @@ def main():
         "tflops_effective": round(flops_img * ips / 1e12, 2),
         "roofline": roof,
         "conv_sweep": sweep,
+        "other_models": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
