@@ -52,6 +52,31 @@ def calibrate(ia, pw):
     log("[bench] calibration pass: 5 x (128 MiB read + 128 MiB write)")
 
 
+def sweep_plan(pw, d, name):
+    """Plan of one conv sweep layer in the layout it has inside a model: the stem reads the
+    NCHW graph input, every other conv sits between two ReLUs (channels-last tensors)."""
+    _, cin, cout, H, W, k, s, g, act = next(c for c in pw.CONV_SWEEP if c[0] == name)
+    pb = pw.PlanBuilder(d, seed=0)
+    x = pb.input("x", [1, cin, H, W])
+    if not name.startswith("stem"):
+        x = pb.unary(x, pw.UN_RELU)
+    y = pb.unary(pb.conv(x, cout, k, s, groups=g, act=act), pw.UN_RELU)
+    pb.output(y)
+    return pb.write()
+
+
+def layer_runs(ia, pw, name, batch, iters):
+    """One sweep layer's plan, `iters` eager passes (for counter collection on that conv)."""
+    with tempfile.TemporaryDirectory() as d:
+        m = ia.PlanModel(sweep_plan(pw, d, name), 0, batch, ia.IVH_FLAG_NO_GRAPH)
+        x0 = np.random.default_rng(0).random(m.inputNumel() * batch, dtype=np.float32)
+        m.setInput(x0.astype(np.float16).view(np.uint16), batch)
+        for _ in range(iters):
+            m.run(batch)
+        m.close()
+    log(f"[bench] layer {name} batch {batch}: {iters} passes")
+
+
 def conv_sweep(ia, pw, batch, iters):
     """The conv operator sweep (stem, strided and stride-1 3x3, depthwise) at `batch`, each
     conv measured in the layout it has inside a model: the stem reads the NCHW graph input,
@@ -63,13 +88,7 @@ def conv_sweep(ia, pw, batch, iters):
     rows = []
     for name, cin, cout, H, W, k, s, g, act in pw.CONV_SWEEP:
         with tempfile.TemporaryDirectory() as d:
-            pb = pw.PlanBuilder(d, seed=0)
-            x = pb.input("x", [1, cin, H, W])
-            if not name.startswith("stem"):
-                x = pb.unary(x, pw.UN_RELU)
-            y = pb.unary(pb.conv(x, cout, k, s, groups=g, act=act), pw.UN_RELU)
-            pb.output(y)
-            m = ia.PlanModel(pb.write(), 0, batch, ia.IVH_FLAG_NO_GRAPH)
+            m = ia.PlanModel(sweep_plan(pw, d, name), 0, batch, ia.IVH_FLAG_NO_GRAPH)
             x0 = np.random.default_rng(0).random(m.inputNumel() * batch, dtype=np.float32)
             m.setInput(x0.astype(np.float16).view(np.uint16), batch)
             m.run(batch)
@@ -160,9 +179,11 @@ def main():
     ap.add_argument("--no-models", action="store_true", help="skip the MobileNetV3 / YOLO11n lines")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch node by node instead of replaying the captured HIP graph")
-    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep"],
+    ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer for --phase layer")
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
-                         "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE")
+                         "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE; "
+                         "sweep: the conv sweep only; layer: --steps passes of one sweep layer (--layer)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -177,6 +198,9 @@ def main():
         return
     if args.phase == "sweep":
         conv_sweep(ia, pw, args.batch, max(args.profile_iters, 10))
+        return
+    if args.phase == "layer":
+        layer_runs(ia, pw, args.layer, args.batch, args.steps)
         return
     tmp = tempfile.TemporaryDirectory()
     path, flops_img = pw.MODELS[args.model](tmp.name, seed=0, imgsz=args.imgsz)

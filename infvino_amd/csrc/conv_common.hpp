@@ -27,6 +27,18 @@ __device__ __forceinline__ int idiv_small(int n, int d, float inv)
   return q;
 }
 
+// Work-group w of a launch is dispatched to XCD w % 8, and each XCD has its own L2.  This
+// maps the hardware order to a tile order in which every XCD owns one contiguous range of
+// tiles (a bijection on [0, n)), so neighbouring tiles -- which share input rows -- run on
+// the same XCD and hit its L2 instead of HBM.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_tile(int w, int n)
+{
+  const int per = n / kXcds, rem = n - per * kXcds;
+  const int x = w % kXcds, i = w / kXcds;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
 // Activation codes and formulas of the reference epilogues (kernels/gemm.cl:137-154,
 // conv_ov.cl:121-131, conv_general.cl:71-83), evaluated in fp32.
 __device__ __forceinline__ float act_f(float v, int act)
@@ -139,10 +151,10 @@ __device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM]
 // the reference order act(acc + b) + r (gemm.cl:644-650, conv_ov.cl:285-288).  The tile is
 // staged in LDS and written with 16-byte stores (NHWC along channels, NCHW along pixels).
 // pix(pl, b, hw): tile pixel slot pl -> image b, output pixel hw; false when outside.
-// With p.ksplit > 1 the fp32 partials go to the workspace [z][co][pixel] instead.
+// With p.ksplit > 1 the fp32 partials go to the workspace [kz][co][pixel] instead.
 template <int MB, int WGM, int WGN, int TM, int TN, class PixFn>
 __device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][TM], const ConvParams & p,
-                                              _Float16 * lds, int n0, PixFn pix)
+                                              _Float16 * lds, int n0, int kz, PixFn pix)
 {
   using F = Mf<MB>;
   using T = TileShape<MB, WGM, WGN, TM, TN>;
@@ -154,7 +166,7 @@ __device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][
 
   if (p.ksplit > 1) {
     const int Npad = gridDim.y * BN;
-    float * wsz = p.ws + (long)blockIdx.z * Npad * M;
+    float * wsz = p.ws + (long)kz * Npad * M;
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
 #pragma unroll

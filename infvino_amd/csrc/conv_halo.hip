@@ -57,9 +57,12 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
   const int Hs = p.H + 1;                                  // rows per image incl. separator
   const int Htot = p.batch * Hs - 1;                       // tall-image rows
   const int tiles_x = (p.Wo + TW - 1) / TW;
-  const int tyi = blockIdx.x / tiles_x, txi = blockIdx.x - tyi * tiles_x;
+  // XCD-aware order over (spatial tile, channel tile), spatial tiles fastest
+  const int lin = xcd_tile(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+  const int bx = lin % gridDim.x, by = lin / gridDim.x;
+  const int tyi = bx / tiles_x, txi = bx - tyi * tiles_x;
   const int oy0 = tyi * TH, ox0 = txi * TW;
-  const int n0 = blockIdx.y * BN;
+  const int n0 = by * BN;
   const int nchunks = (p.Cin + CK - 1) / CK;
   const int nsteps = nchunks * SPC;
   const float inv_pw = __builtin_amdgcn_rcpf((float)PW), inv_tw = __builtin_amdgcn_rcpf((float)TW);
@@ -215,7 +218,7 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
     if (s + 1 < nsteps) step(s + 1, W1, W0);
   }
 
-  tile_epilogue<MB, WGM, WGN, TM, TN>(acc, p, lds, n0, [&](int pl, int & b, int & hw) {
+  tile_epilogue<MB, WGM, WGN, TM, TN>(acc, p, lds, n0, 0, [&](int pl, int & b, int & hw) {
     if (pl >= TH * TW) return false;
     const int ty = idiv_small(pl, TW, inv_tw), tx = pl - ty * TW;
     const int gy = oy0 + ty, ox = ox0 + tx;

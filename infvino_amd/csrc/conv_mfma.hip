@@ -51,8 +51,12 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   const int wm = wave % WGM, wn = wave / WGM;
   const int HWo = p.Ho * p.Wo;
   const long M = (long)p.batch * HWo;
-  const long m0 = (long)blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
+  // XCD-aware order over (pixel tile, channel tile, K slice), pixel tiles fastest
+  const int lin = xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                           gridDim.x * gridDim.y * gridDim.z);
+  const int bx = lin % gridDim.x, by = (lin / gridDim.x) % gridDim.y, bz = lin / (gridDim.x * gridDim.y);
+  const long m0 = (long)bx * BM;
+  const int n0 = by * BN;
   const int kc = tid % KC, r0 = tid / KC;
 
   const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
@@ -88,7 +92,7 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   // K range of this work-group (split-K: blockIdx.z-th slice of the K steps)
   const int nk_all = p.kpad / BK;
   const int per = (nk_all + p.ksplit - 1) / p.ksplit;
-  const int kt0 = blockIdx.z * per;
+  const int kt0 = bz * per;
   const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
   const int nk = kt1 > kt0 ? kt1 - kt0 : 0;
   const int taps = p.K * p.K;
@@ -175,7 +179,7 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
     if (s + 1 < nk) step(s + 1, S1, S0);
   }
 
-  tile_epilogue<32, WGM, WGN, TM, TN>(acc, p, lds, n0, [&](int pl, int & b, int & hw) {
+  tile_epilogue<32, WGM, WGN, TM, TN>(acc, p, lds, n0, bz, [&](int pl, int & b, int & hw) {
     const long pm = m0 + pl;
     if (pm >= M) return false;
     b = (int)(pm / HWo);

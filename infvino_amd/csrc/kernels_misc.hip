@@ -235,7 +235,9 @@ __global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
 {
   extern __shared__ __attribute__((aligned(16))) _Float16 srow[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.y, oy0 = blockIdx.x * TR;
+  // XCD-aware order over (row tile, image): consecutive row tiles share an input row
+  const int lin = xcd_tile(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+  const int b = lin / gridDim.x, oy0 = (lin % gridDim.x) * TR;
   const int W = p.W, LW = W + 4;               // LDS row: 2 pad columns each side
   const int G = W >> 3;                        // 8-pixel column groups per input row
   const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img;
