@@ -27,6 +27,12 @@ __device__ __forceinline__ int idiv_small(int n, int d, float inv)
   return q;
 }
 
+// n / d with f = fastdiv_make(d): see FastDiv.
+__device__ __forceinline__ unsigned fastdiv(unsigned n, FastDiv f)
+{
+  return (unsigned)(((unsigned long long)__umulhi(n, f.m) + n) >> f.l);
+}
+
 // Work-group w of a launch is dispatched to XCD w % 8, and each XCD has its own L2.  This
 // maps the hardware order to a tile order in which every XCD owns one contiguous range of
 // tiles (a bijection on [0, n)), so neighbouring tiles -- which share input rows -- run on
@@ -120,11 +126,17 @@ __device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM]
   const int wm = wave % WGM, wn = wave / WGM;
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
+    // bias: runs of 4 rows are 4 consecutive channels, one 16-byte load each (the MFMA
+    // families' bias is zero padded to a multiple of 128 channels)
     float bv[F::NV];
 #pragma unroll
-    for (int v = 0; v < F::NV; ++v) {
-      const int co = n0 + wn * TN * MB + tn * MB + F::row(lane, v);
-      bv[v] = (p.bias && co < p.Cout) ? p.bias[co] : 0.0f;
+    for (int v4 = 0; v4 < F::NV; v4 += 4) {
+      float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + n0 + wn * TN * MB + tn * MB + F::row(lane, v4));
+      bv[v4] = b4.x;
+      bv[v4 + 1] = b4.y;
+      bv[v4 + 2] = b4.z;
+      bv[v4 + 3] = b4.w;
     }
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {

@@ -30,8 +30,9 @@ namespace ivh {
 // incrementally, out-of-image taps and K padding load from past the buffer's range (zeros),
 // and the ragged channels of a last piece (Cin % 8) are zeroed when written to LDS.  B
 // (weight) loads are buffer loads at a loop-invariant offset plus the step's scalar offset.
-// Both are prefetched one step ahead in registers and double buffered in LDS.
-template <int WGM, int WGN, int TM, int TN, int BK>
+// Both are prefetched one step ahead in registers and double buffered in LDS.  RAG: Cin is
+// not a multiple of 8 (the compile-time switch keeps the masking out of the common case).
+template <int WGM, int WGN, int TM, int TN, int BK, bool RAG>
 __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 {
   using F = Mf<32>;
@@ -50,12 +51,12 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
   const int HWo = p.Ho * p.Wo;
-  const long M = (long)p.batch * HWo;
+  const unsigned M = (unsigned)p.batch * HWo;  // below 2^31 (the launcher's batch chunks)
   // XCD-aware order over (pixel tile, channel tile, K slice), pixel tiles fastest
   const int lin = xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
                            gridDim.x * gridDim.y * gridDim.z);
   const int bx = lin % gridDim.x, by = (lin / gridDim.x) % gridDim.y, bz = lin / (gridDim.x * gridDim.y);
-  const long m0 = (long)bx * BM;
+  const unsigned m0 = (unsigned)bx * BM;
   const int n0 = by * BN;
   const int kc = tid % KC, r0 = tid / KC;
 
@@ -69,10 +70,10 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   int abase[A_IT], aiy[A_IT], aix[A_IT];
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
-    const long pm = m0 + r0 + i * RPI;
+    const unsigned pm = m0 + r0 + i * RPI;
     if (pm < M) {
-      const int b = (int)(pm / HWo), hw = (int)(pm - (long)b * HWo);
-      const int oy = hw / p.Wo, ox = hw - oy * p.Wo;
+      const int b = (int)fastdiv(pm, p.dv_hwo), hw = (int)pm - b * HWo;
+      const int oy = (int)fastdiv((unsigned)hw, p.dv_wo), ox = hw - oy * p.Wo;
       abase[i] = b * (int)p.x.img;
       aiy[i] = oy * p.S - p.P;
       aix[i] = ox * p.S - p.P;
@@ -96,22 +97,27 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   const int kt1 = kt0 + per < nk_all ? kt0 + per : nk_all;
   const int nk = kt1 > kt0 ? kt1 - kt0 : 0;
   const int taps = p.K * p.K;
-  // position (tap, ky, kx, ci) of this thread's piece in the current load step
-  int ci = kt0 * BK + kc * 8, tap = 0, ky = 0, kx = 0;
-  auto norm_k = [&]() {
-    while (ci >= p.cin8) {
+  // position (tap, ci) of this thread's piece in the current load step; a step advances it
+  // by dq taps and dr channels.  ky = tap / K as (tap * kmul) >> 16, exact for tap < 2^16 / K
+  // (the launcher keeps K * K + 16 below that).
+  const int dq = BK / p.cin8, dr = BK - dq * p.cin8;
+  const unsigned kmul = (65536u + p.K - 1) / p.K;
+  int tap = (kt0 * BK + kc * 8) / p.cin8;
+  int ci = kt0 * BK + kc * 8 - tap * p.cin8;
+  auto advance = [&]() {
+    ci += dr;
+    tap += dq;
+    if (ci >= p.cin8) {
       ci -= p.cin8;
       ++tap;
-      if (++kx == p.K) { kx = 0; ++ky; }
     }
   };
-  norm_k();
-  const bool ragged = (p.Cin & 7) != 0;
 
   h8 ra[A_IT], rb[B_IT];
   int aci = 0;  // channel of the loaded A piece (for the ragged mask at store time)
   auto load = [&](int kt) {
     aci = ci;
+    const int ky = (int)(((unsigned)tap * kmul) >> 16), kx = tap - ky * p.K;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int iy = aiy[i] + ky, ix = aix[i] + kx;
@@ -122,17 +128,18 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 #pragma unroll
     for (int i = 0; i < B_IT; ++i)
       rb[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
-    ci += BK;
-    norm_k();
+    advance();
   };
   auto store = [&](_Float16 * st) {
     u16x8 keep;
+    if (RAG) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) keep[e] = aci + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+      for (int e = 0; e < 8; ++e) keep[e] = aci + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+    }
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       h8 v = ra[i];
-      if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
+      if (RAG) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
       *reinterpret_cast<h8 *>(st + (r0 + i * RPI) * LDK + kc * 8) = v;
     }
 #pragma unroll
@@ -180,10 +187,10 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
   }
 
   tile_epilogue<32, WGM, WGN, TM, TN>(acc, p, lds, n0, bz, [&](int pl, int & b, int & hw) {
-    const long pm = m0 + pl;
+    const unsigned pm = m0 + pl;
     if (pm >= M) return false;
-    b = (int)(pm / HWo);
-    hw = (int)(pm - (long)b * HWo);
+    b = (int)fastdiv(pm, p.dv_hwo);
+    hw = (int)pm - b * HWo;
     return true;
   });
 }
@@ -222,8 +229,13 @@ static void launch_t(const ConvParams & p, hipStream_t s)
 {
   using T = TileShape<32, WGM, WGN, TM, TN>;
   const long M = (long)p.batch * p.Ho * p.Wo;
+  if (M >= (1L << 31) || p.K * p.K + 16 >= 65536 / p.K) throw std::runtime_error("implicit-GEMM conv geometry");
+  ConvParams q = p;
+  q.dv_hwo = fastdiv_make((unsigned)(p.Ho * p.Wo));
+  q.dv_wo = fastdiv_make((unsigned)p.Wo);
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
-  hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK>), grid, dim3(256), 0, s, p);
+  if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, true>), grid, dim3(256), 0, s, q);
+  else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, false>), grid, dim3(256), 0, s, q);
   if (p.ksplit > 1) {
     const long n = M * p.Cout;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,

@@ -32,9 +32,27 @@ struct View {
 };
 
 // One convolution launch.  Output pixels of all images form the GEMM M axis.
+// Division of unsigned 32-bit n by a run-time invariant d >= 1 through a multiply-high
+// (Granlund & Montgomery, "Division by invariant integers using multiplication", 1994,
+// round-up variant): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> l for every n < 2^32 (the sum taken in 64 bits).
+struct FastDiv {
+  unsigned m = 1;
+  int l = 0;
+};
+inline FastDiv fastdiv_make(unsigned d)
+{
+  FastDiv f;
+  while ((1ull << f.l) < d) ++f.l;
+  f.m = (unsigned)(((1ull << 32) * ((1ull << f.l) - d)) / d + 1);
+  return f;
+}
+
 struct ConvParams {
   View x, y, r;              // input, output, residual (r.ptr == nullptr: none)
   const __half * w = nullptr;  // packed weights (layout depends on the kernel family)
+  // fp32 bias; for the MFMA families it holds round_up(Cout, 128) entries, zero past Cout,
+  // which the epilogues read in 16-byte pieces without a bound check
   const float * bias = nullptr;
   int batch = 1;
   int Cin = 0, H = 0, W = 0;
@@ -58,6 +76,8 @@ struct ConvParams {
   int halo = 0;
   int th = 0, tw = 0;
   int ck = 0;  // input-channel chunk of the halo weight packing (16 / 32 / 64)
+  // divisions by Ho * Wo and by Wo (set by the implicit-GEMM launcher)
+  FastDiv dv_hwo, dv_wo;
 };
 
 // Generic small-op descriptor (elementwise / pooling / data movement).
