@@ -30,9 +30,11 @@ namespace ivh {
 // incrementally, out-of-image taps and K padding load from past the buffer's range (zeros),
 // and the ragged channels of a last piece (Cin % 8) are zeroed when written to LDS.  B
 // (weight) loads are buffer loads at a loop-invariant offset plus the step's scalar offset.
-// Both are prefetched one step ahead in registers and double buffered in LDS.  RAG: Cin is
-// not a multiple of 8 (the compile-time switch keeps the masking out of the common case).
-template <int WGM, int WGN, int TM, int TN, int BK, bool RAG>
+// Both are double buffered in LDS and prefetched PF steps ahead through a ring of PF
+// register stages, so a work-group with a short K loop has its whole K range in flight at
+// once instead of waiting one memory latency per step.  RAG: Cin is not a multiple of 8
+// (the compile-time switch keeps the masking out of the common case).
+template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG>
 __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 {
   using F = Mf<32>;
@@ -113,38 +115,39 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
     }
   };
 
-  h8 ra[A_IT], rb[B_IT];
-  int aci = 0;  // channel of the loaded A piece (for the ragged mask at store time)
-  auto load = [&](int kt) {
-    aci = ci;
+  // register ring: stage d holds the pieces of step d (mod PF) between load and LDS store
+  h8 ra[PF][A_IT], rb[PF][B_IT];
+  int aci[PF];  // channel of the loaded A piece (for the ragged mask at store time)
+  auto load = [&](int kt, int d) {
+    aci[d] = ci;
     const int ky = (int)(((unsigned)tap * kmul) >> 16), kx = tap - ky * p.K;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int iy = aiy[i] + ky, ix = aix[i] + kx;
       const bool ok = tap < taps && (unsigned)iy < (unsigned)p.H && (unsigned)ix < (unsigned)p.W;
       const unsigned off = ok ? (unsigned)((abase[i] + (iy * p.W + ix) * p.x.cs + ci) * 2) : kBufOOB;
-      ra[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+      ra[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i)
-      rb[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
+      rb[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
     advance();
   };
-  auto store = [&](_Float16 * st) {
+  auto store = [&](_Float16 * st, int d) {
     u16x8 keep;
     if (RAG) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) keep[e] = aci + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+      for (int e = 0; e < 8; ++e) keep[e] = aci[d] + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
     }
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
-      h8 v = ra[i];
+      h8 v = ra[d][i];
       if (RAG) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
       *reinterpret_cast<h8 *>(st + (r0 + i * RPI) * LDK + kc * 8) = v;
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i)
-      if (r0 + i * RPI < BN) *reinterpret_cast<h8 *>(st + (BM + r0 + i * RPI) * LDK + kc * 8) = rb[i];
+      if (r0 + i * RPI < BN) *reinterpret_cast<h8 *>(st + (BM + r0 + i * RPI) * LDK + kc * 8) = rb[d][i];
   };
 
   acc_t acc[TN][TM];
@@ -157,8 +160,11 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 
   const int brow = (wm * TM * 32 + (lane & 31)) * LDK + F::kq(lane);
   const int arow = (BM + wn * TN * 32 + (lane & 31)) * LDK + F::kq(lane);
-  auto step = [&](int s, const _Float16 * cur, _Float16 * nxt) {
-    if (s + 1 < nk) load(kt0 + s + 1);
+  // step s (register stage d = s mod PF): step s + PF's loads go into stage d, whose
+  // pieces reached LDS at the end of step s - 1; the MFMAs read LDS buffer s & 1; step
+  // s + 1's pieces then go to the other buffer.
+  auto step = [&](int s, int d, const _Float16 * cur, _Float16 * nxt) {
+    if (s + PF < nk) load(kt0 + s + PF, d);
 #pragma unroll
     for (int j = 0; j < BK / 16; ++j) {
       h8 fa[TN], fb[TM];
@@ -171,19 +177,22 @@ __global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = F::mma(fa[tn], fb[tm], acc[tn][tm]);
     }
-    if (s + 1 < nk) store(nxt);
+    if (s + 1 < nk) store(nxt, (d + 1) % PF);
     __syncthreads();
   };
   _Float16 * const S0 = lds;
   _Float16 * const S1 = lds + STAGE;
-  if (nk > 0) {
-    load(kt0);
-    store(S0);
-  }
+#pragma unroll
+  for (int d = 0; d < PF; ++d)
+    if (d < nk) load(kt0 + d, d);
+  if (nk > 0) store(S0, 0);
   __syncthreads();
-  for (int s = 0; s < nk; s += 2) {
-    step(s, S0, S1);
-    if (s + 1 < nk) step(s + 1, S1, S0);
+  // unrolled so that both the register stage and the LDS buffer of a step are static
+  constexpr int U = PF % 2 == 0 ? PF : 2 * PF;
+  for (int s = 0; s < nk; s += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (s + u < nk) step(s + u, u % PF, (u & 1) ? S1 : S0, (u & 1) ? S0 : S1);
   }
 
   tile_epilogue<32, WGM, WGN, TM, TN>(acc, p, lds, n0, bz, [&](int pl, int & b, int & hw) {
@@ -224,7 +233,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const ConvParams p, 
 // Tile table: a small CDNA4 choice per op (BN from Cout; BM = 128 pixels).
 int igemm_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
 
-template <int WGM, int WGN, int TM, int TN, int BK>
+template <int WGM, int WGN, int TM, int TN, int BK, int PF>
 static void launch_t(const ConvParams & p, hipStream_t s)
 {
   using T = TileShape<32, WGM, WGN, TM, TN>;
@@ -234,8 +243,8 @@ static void launch_t(const ConvParams & p, hipStream_t s)
   q.dv_hwo = fastdiv_make((unsigned)(p.Ho * p.Wo));
   q.dv_wo = fastdiv_make((unsigned)p.Wo);
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
-  if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, true>), grid, dim3(256), 0, s, q);
-  else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, false>), grid, dim3(256), 0, s, q);
+  if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, true>), grid, dim3(256), 0, s, q);
+  else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false>), grid, dim3(256), 0, s, q);
   if (p.ksplit > 1) {
     const long n = M * p.Cout;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
@@ -243,13 +252,16 @@ static void launch_t(const ConvParams & p, hipStream_t s)
   }
 }
 
+// Register prefetch depth (K steps in flight) per tile width (measured on MI355X over
+// depths 1..6: deeper rings cost occupancy on the wide tiles and gain little elsewhere).
+constexpr int PF32 = 2, PF64 = 2, PF128 = 2;
 template <int BK>
 static void launch_bk(const ConvParams & p, hipStream_t s)
 {
   switch (igemm_bn(p.Cout)) {
-  case 32: launch_t<4, 1, 1, 1, BK>(p, s); break;
-  case 64: launch_t<2, 2, 2, 1, BK>(p, s); break;
-  default: launch_t<2, 2, 2, 2, BK>(p, s); break;
+  case 32: launch_t<4, 1, 1, 1, BK, PF32>(p, s); break;
+  case 64: launch_t<2, 2, 2, 1, BK, PF64>(p, s); break;
+  default: launch_t<2, 2, 2, 2, BK, PF128>(p, s); break;
   }
 }
 
