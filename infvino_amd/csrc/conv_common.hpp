@@ -113,11 +113,31 @@ struct TileShape {
   static constexpr int EPI = (BM * (BN + 8) > BN * (BM + 8)) ? BM * (BN + 8) : BN * (BM + 8);
 };
 
+// Bias of a lane's accumulator rows: runs of 4 rows are 4 consecutive channels, one 16-byte
+// load each (the MFMA families' bias is zero padded to a multiple of 128 channels).
+template <int MB, int WGM, int WGN, int TM, int TN>
+__device__ __forceinline__ void load_bias(const ConvParams & p, int n0, float (&bv)[TN][Mf<MB>::NV])
+{
+  using F = Mf<MB>;
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) / WGM;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int v4 = 0; v4 < F::NV; v4 += 4) {
+      float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + n0 + wn * TN * MB + tn * MB + F::row(lane, v4));
+      bv[tn][v4] = b4.x;
+      bv[tn][v4 + 1] = b4.y;
+      bv[tn][v4 + 2] = b4.z;
+      bv[tn][v4 + 3] = b4.w;
+    }
+}
+
 // Epilogue phase 1: bias + activation (compile-time code) in fp32, one rounding to fp16,
 // tile into LDS as [pixel][channel] (NHWC output) or [channel][pixel] (NCHW output).
 template <int ACT, int MB, int WGM, int WGN, int TM, int TN>
-__device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM], const ConvParams & p,
-                                           _Float16 * lds, int n0, bool nhwc)
+__device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM], const float (&bv)[TN][Mf<MB>::NV],
+                                           _Float16 * lds, bool nhwc)
 {
   using F = Mf<MB>;
   using T = TileShape<MB, WGM, WGN, TM, TN>;
@@ -126,18 +146,6 @@ __device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM]
   const int wm = wave % WGM, wn = wave / WGM;
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
-    // bias: runs of 4 rows are 4 consecutive channels, one 16-byte load each (the MFMA
-    // families' bias is zero padded to a multiple of 128 channels)
-    float bv[F::NV];
-#pragma unroll
-    for (int v4 = 0; v4 < F::NV; v4 += 4) {
-      float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + n0 + wn * TN * MB + tn * MB + F::row(lane, v4));
-      bv[v4] = b4.x;
-      bv[v4 + 1] = b4.y;
-      bv[v4 + 2] = b4.z;
-      bv[v4 + 3] = b4.w;
-    }
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
       const int pl = wm * TM * MB + tm * MB + F::col(lane);
@@ -147,7 +155,7 @@ __device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM]
         const int cl = wn * TN * MB + tn * MB + F::row(lane, v4);
         h4 hv;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) hv[k] = (_Float16)act_fast<ACT>(acc[tn][tm][v4 + k] + bv[v4 + k]);
+        for (int k = 0; k < 4; ++k) hv[k] = (_Float16)act_fast<ACT>(acc[tn][tm][v4 + k] + bv[tn][v4 + k]);
         if (nhwc) {
           *reinterpret_cast<h4 *>(lds + pl * (BN + 8) + cl) = hv;
         } else {
@@ -164,9 +172,12 @@ __device__ __forceinline__ void stage_tile(typename Mf<MB>::acc_t (&acc)[TN][TM]
 // staged in LDS and written with 16-byte stores (NHWC along channels, NCHW along pixels).
 // pix(pl, b, hw): tile pixel slot pl -> image b, output pixel hw; false when outside.
 // With p.ksplit > 1 the fp32 partials go to the workspace [kz][co][pixel] instead.
+// tile_epilogue_bv takes the bias values already loaded (load_bias), for kernels whose
+// loads of the next tile are in flight during the epilogue.
 template <int MB, int WGM, int WGN, int TM, int TN, class PixFn>
-__device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][TM], const ConvParams & p,
-                                              _Float16 * lds, int n0, int kz, PixFn pix)
+__device__ __forceinline__ void tile_epilogue_bv(typename Mf<MB>::acc_t (&acc)[TN][TM],
+                                                 const float (&bv)[TN][Mf<MB>::NV], const ConvParams & p,
+                                                 _Float16 * lds, int n0, int kz, PixFn pix)
 {
   using F = Mf<MB>;
   using T = TileShape<MB, WGM, WGN, TM, TN>;
@@ -197,12 +208,12 @@ __device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][
 
   const bool nhwc = p.y.layout == kNHWC;
   switch (p.act) {
-  case kActSiLU: stage_tile<kActSiLU, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
-  case kActReLU: stage_tile<kActReLU, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
-  case kActHSwish: stage_tile<kActHSwish, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
-  case kActHSigmoid: stage_tile<kActHSigmoid, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
-  case kActSigmoid: stage_tile<kActSigmoid, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
-  default: stage_tile<kActNone, MB, WGM, WGN, TM, TN>(acc, p, lds, n0, nhwc); break;
+  case kActSiLU: stage_tile<kActSiLU, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
+  case kActReLU: stage_tile<kActReLU, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
+  case kActHSwish: stage_tile<kActHSwish, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
+  case kActHSigmoid: stage_tile<kActHSigmoid, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
+  case kActSigmoid: stage_tile<kActSigmoid, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
+  default: stage_tile<kActNone, MB, WGM, WGN, TM, TN>(acc, bv, lds, nhwc); break;
   }
   __syncthreads();
 
@@ -270,6 +281,16 @@ __device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][
       }
     }
   }
+}
+
+// Fused epilogue with the bias loaded here (the common case).
+template <int MB, int WGM, int WGN, int TM, int TN, class PixFn>
+__device__ __forceinline__ void tile_epilogue(typename Mf<MB>::acc_t (&acc)[TN][TM], const ConvParams & p,
+                                              _Float16 * lds, int n0, int kz, PixFn pix)
+{
+  float bv[TN][Mf<MB>::NV];
+  load_bias<MB, WGM, WGN, TM, TN>(p, n0, bv);
+  tile_epilogue_bv<MB, WGM, WGN, TM, TN>(acc, bv, p, lds, n0, kz, pix);
 }
 
 }  // namespace ivh

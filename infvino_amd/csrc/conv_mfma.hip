@@ -324,6 +324,10 @@ void launch_conv_igemm(const ConvParams & p, hipStream_t s)
     launch_conv_halo(p, s);
     return;
   }
+  if (p.s2) {
+    launch_conv_s2(p, s);
+    return;
+  }
   if (p.bk == 64) launch_bk<64>(p, s);
   else launch_bk<32>(p, s);
 }

@@ -182,6 +182,21 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
       }
     }
   }
+  // small-channel stride-2 convs: the LDS-patch kernel of conv_s2.hip on the same packing
+  int sc;
+  if (!p.halo && p.K == 3 && p.S == 2 && p.P == 1 && s2_plan(p.Cin, p.Cout, p.Ho, p.Wo, &sc, &th, &tw) &&
+      s2_cfg_ck(sc) == pk.cin8) {
+    ConvParams q = p;
+    q.th = th;
+    q.tw = tw;
+    if (s2_grid(q) >= 160 || p.ksplit == 1) {
+      p.s2 = sc + 1;
+      p.th = th;
+      p.tw = tw;
+      p.ksplit = 1;
+      p.ws = nullptr;
+    }
+  }
   if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) || (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
     throw std::runtime_error("implicit-GEMM input view not 16-byte aligned NHWC");
   if (p.kpad < p.K * p.K * p.cin8 || p.cin8 < p.Cin) throw std::runtime_error("packed weight geometry");

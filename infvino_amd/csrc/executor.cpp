@@ -1179,7 +1179,8 @@ void Model::validate(const Launch & l) const
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
     check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout, HWo), 2, "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
-    if (p.bias) check(p.bias, 0, p.Cout - 1, 4, "conv bias");
+    // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
+    if (p.bias) check(p.bias, 0, (l.kind == Launch::kIgemm ? (p.Cout + 127) / 128 * 128 : p.Cout) - 1, 4, "conv bias");
     if (l.kind == Launch::kIgemm) {
       if (p.x.layout != kNHWC) throw std::runtime_error("igemm needs channels-last input");
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
@@ -1194,6 +1195,14 @@ void Model::validate(const Launch & l) const
           throw std::runtime_error("halo geometry");
         if (p.kpad != (p.Cin + ck - 1) / ck * halo_taps(ck) * ck) throw std::runtime_error("halo weight packing");
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("halo geometry too large");
+      }
+      if (p.s2) {
+        const int cfg = p.s2 - 1;
+        if (cfg < 0 || cfg > 1 || p.halo || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
+            p.cin8 != s2_cfg_ck(cfg) || p.Cout > s2_cfg_bn(cfg) || p.th < 1 || p.tw < 1 ||
+            p.th * p.tw > s2_cfg_bm(cfg) || s2_patch(p.th, p.tw) > s2_cfg_pmax(cfg) ||
+            p.Ho != (p.H - 1) / 2 + 1 || p.Wo != (p.W - 1) / 2 + 1 || p.kpad < 9 * p.cin8)
+          throw std::runtime_error("stride-2 patch geometry");
       }
       if (p.ksplit > 1) {
         const long M = (long)p.batch * HWo;
@@ -1490,7 +1499,8 @@ std::string Model::nodeKernel(int i)
   if (node_launch_begin_.at(i) == node_launch_end_.at(i)) return "(view)";
   const Launch & l = L[node_launch_begin_[i]];
   switch (l.kind) {
-  case Launch::kIgemm: return l.cp.halo ? "conv_halo" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm");
+  case Launch::kIgemm:
+    return l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   default: return s.kernel;

@@ -76,6 +76,9 @@ struct ConvParams {
   int halo = 0;
   int th = 0, tw = 0;
   int ck = 0;  // input-channel chunk of the halo weight packing (16 / 32 / 64)
+  // 3x3 stride-2 small-channel kernel (conv_s2.hip): config + 1 (0: not used); th x tw is
+  // then the output tile of one image and w the implicit-GEMM packing
+  int s2 = 0;
   // divisions by Ho * Wo and by Wo (set by the implicit-GEMM launcher)
   FastDiv dv_hwo, dv_wo;
 };

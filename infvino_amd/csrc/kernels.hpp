@@ -27,6 +27,16 @@ int halo_bn(int cfg);
 int halo_pmax(int cfg);
 void launch_conv_halo(const ConvParams & p, hipStream_t s);
 
+// conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
+bool s2_plan(int cin, int cout, int Ho, int Wo, int * cfg, int * th, int * tw);
+int s2_patch(int th, int tw);  // patch pixels of a th x tw output tile
+int s2_cfg_bm(int cfg);
+int s2_cfg_bn(int cfg);
+int s2_cfg_ck(int cfg);
+int s2_cfg_pmax(int cfg);
+long s2_grid(const ConvParams & p);
+void launch_conv_s2(const ConvParams & p, hipStream_t s);
+
 // kernels_misc.hip
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout
 void launch_dwconv(const ConvParams & p, hipStream_t s);        // depthwise, any layout

@@ -56,6 +56,7 @@ CONVS = [
     (24, 40, 17, 19, 3, 1, 1, 1, ops.ACT_HSWISH, 1, True),     # 3x3 s1 LDS patch, ragged, residual
     (21, 32, 15, 15, 3, 2, 1, 1, ops.ACT_SILU, 1, False),      # 3x3 s2 im2col, Cin % 8 != 0
     (8, 20, 9, 11, 5, 1, 2, 1, ops.ACT_SIGMOID, 1, True),      # 5x5, 8 channels a piece, residual
+    (13, 48, 17, 14, 3, 2, 1, 1, ops.ACT_SILU, 1, True),       # 3x3 s2 LDS patch, pad channels, residual
     (128, 256, 10, 10, 3, 1, 1, 1, ops.ACT_RELU, 1, False),    # wide, K step 64
     (3, 16, 64, 64, 3, 2, 1, 1, ops.ACT_SILU, 0, False),       # stem, planar in and out
     (16, 1, 4, 64, 1, 1, 0, 1, ops.ACT_NONE, 0, False),        # planar 1x1, one output channel

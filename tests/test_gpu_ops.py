@@ -31,6 +31,19 @@ def _run(path, batch, seed=0, lo=0.0, hi=1.0, flags=0):
     return p, x, got
 
 
+def _kernels(path, batch, flags=0):
+    """Kernel labels the planner picks for each node at `batch` (host-only dry run)."""
+    m = ia.PlanModel(path, 0, batch, flags | ia.IVH_FLAG_DRY_RUN)
+    m.run(batch)
+    labels = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    m.close()
+    return labels
+
+
+def _conv_kernel(path, batch, flags=0):
+    return next(k for k in _kernels(path, batch, flags) if k.startswith(("conv", "dwconv")))
+
+
 def _check_f32(path, batch, seed=0, ref_mode=True, **kw):
     p, x, got = _run(path, batch, seed, **kw)
     ref = O.run_plan(p, x, batch)
@@ -54,10 +67,27 @@ def test_conv1x1_config(tmp_path):
         _check_f32(path, b)
 
 
+SWEEP_KERNEL = {"stem": ("conv_stem",), "dw": ("dwconv",),
+                "conv3x3s2": ("conv_igemm", "conv_igemm_sk", "conv_s2"),
+                "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo")}
+
+
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
 def test_conv_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act)
+    """The conv sweep layers as they run inside a model: every conv but the stem reads an
+    internal (channels-last) tensor."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act,
+                             pre_relu=not name.startswith("stem"))
+    assert _conv_kernel(path, 2) in next(v for k, v in SWEEP_KERNEL.items() if name.startswith(k))
     _check_f32(path, 2, ref_mode=(H * W * cin <= 160 * 160 * 32))
+
+
+@pytest.mark.parametrize("cin,cout,hw,k,s,g", [(16, 32, 40, 3, 2, 1), (64, 64, 20, 3, 1, 1), (32, 64, 12, 3, 1, 4)])
+def test_conv_direct_nchw(tmp_path, cin, cout, hw, k, s, g):
+    """A conv reading the NCHW graph input (and grouped convs) runs the direct kernel."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, groups=g, act=pw.ACT_SILU)
+    assert _conv_kernel(path, 2) == "conv_direct"
+    _check_f32(path, 2)
 
 
 @pytest.mark.parametrize("cin,cout,hw,k,s,act", [
@@ -73,34 +103,56 @@ def test_conv_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     (2, 16, 9, 3, 1, 1),       # stem MFMA path, Cin = 2
 ])
 def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act)
+    """Shape classes of the MFMA families (internal channels-last input) and of the stem
+    (the graph input)."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act, pre_relu=cin > 3)
+    kern = _conv_kernel(path, 3)
+    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo")
     _check_f32(path, 3, lo=-1.0)
 
 
-@pytest.mark.parametrize("cin,cout,H,W,batch", [
-    (64, 64, 80, 80, 2),       # the YOLOv8 80x80 bottleneck shape
-    (48, 40, 33, 35, 2),       # ragged 8x16 tiles on both axes
-    (24, 16, 40, 24, 3),       # Cin < 32: one zero-filled chunk
-    (51, 51, 48, 48, 1),       # Cin not a multiple of 8 (pose keypoint branch)
-    (96, 136, 24, 40, 2),      # Cout > 128: two N tiles, 16x8 tiles
+@pytest.mark.parametrize("cin,cout,H,W,batch,s", [
+    (64, 64, 80, 80, 2, 1),    # the YOLOv8 80x80 bottleneck shape
+    (48, 40, 33, 35, 2, 1),    # ragged 8x16 tiles on both axes
+    (24, 16, 40, 24, 3, 1),    # Cin < 32: one zero-filled chunk
+    (51, 51, 48, 48, 1, 1),    # Cin not a multiple of 8 (pose keypoint branch)
+    (96, 136, 24, 40, 2, 1),   # Cout > 128: two N tiles, 16x8 tiles
 ])
-def test_halo_conv3x3(tmp_path, cin, cout, H, W, batch):
-    """3x3 stride-1 convs through the LDS halo kernel vs the oracle and vs the im2col path."""
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=pw.ACT_SILU)
+def test_halo_conv3x3(tmp_path, cin, cout, H, W, batch, s):
+    """3x3 stride-1 convs through the LDS-patch kernel vs the oracle and vs the im2col path."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=s, act=pw.ACT_SILU, pre_relu=True)
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_SPLITK) == "conv_halo"
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_HALO | ia.IVH_FLAG_NO_SPLITK) == "conv_igemm"
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_SPLITK)
     _, _, im2col = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_HALO | ia.IVH_FLAG_NO_SPLITK)
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(im2col[0]))
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch", [
+    (16, 32, 64, 64, 3),       # the YOLO 16->32 downsample shape class: 128-pixel tiles
+    (16, 64, 40, 40, 2),       # 16 in, 64 out: 64-pixel tiles, two channel blocks
+    (12, 40, 33, 35, 2),       # Cin % 16 != 0 (zeroed pad channels), odd H / W: bottom / right pad
+    (9, 24, 9, 70, 3),         # 9 channels (one real channel in the second piece), wide and short
+    (16, 8, 3, 5, 2),          # a 2 x 3 output: one mostly empty tile per image
+])
+def test_conv3x3_s2(tmp_path, cin, cout, H, W, batch):
+    """3x3 stride-2 convs of few channels through the LDS-patch kernel of conv_s2.hip vs the
+    oracle and vs the im2col path."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=2, act=pw.ACT_SILU, pre_relu=True)
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_SPLITK) == "conv_s2"
+    _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_SPLITK)
+
+
 def test_halo_residual_chain(tmp_path):
     """Bottleneck chain (3x3, 3x3 + residual) on 48x48: halo kernel with the fused residual."""
     def build(pb):
-        x = pb.input("x", [1, 32, 48, 48])
+        x = pb.unary(pb.input("x", [1, 32, 48, 48]), pw.UN_RELU)
         t = pb.conv(x, 32, 3)
         t = pb.conv(t, 32, 3)
         return pb.binary(x, t, 0)
     path = _small_plan(tmp_path, build)
+    assert _kernels(path, 2, ia.IVH_FLAG_NO_SPLITK).count("conv_halo") == 2
     _check_f32(path, 2, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
 
 
@@ -113,7 +165,9 @@ def test_halo_residual_chain(tmp_path):
 ])
 def test_split_k(tmp_path, cin, cout, hw, k, s, batch):
     """Small-M / long-K convs take the split-K path (partials + fixed-order reduce)."""
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=pw.ACT_SILU)
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=pw.ACT_SILU, pre_relu=True)
+    assert _conv_kernel(path, batch) == "conv_igemm_sk"
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_SPLITK) != "conv_igemm_sk"
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
     _, _, nosplit = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(nosplit[0]))
