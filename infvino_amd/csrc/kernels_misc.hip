@@ -240,6 +240,7 @@ __global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
   const int b = lin / gridDim.x, oy0 = (lin % gridDim.x) * TR;
   const int W = p.W, LW = W + 4;               // LDS row: 2 pad columns each side
   const int G = W >> 3;                        // 8-pixel column groups per input row
+  const float inv_g = __builtin_amdgcn_rcpf((float)G);
   const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img;
   // zero the pad columns of every staged row
   for (int e = tid; e < (2 * TR + 1) * 4; e += 256) {
@@ -254,7 +255,7 @@ __global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
 #pragma unroll
   for (int i = 0; i < UIT; ++i) {
     const int u = tid + 256 * i;
-    const int lr = u / G, g = u - lr * G;
+    const int lr = idiv_small(u, G, inv_g), g = u - lr * G;
     const int iy = 2 * oy0 - 1 + lr;
     dsto[i] = u < (2 * TR + 1) * G ? (lr * LW + 8 * g + 2) * 4 : -1;
     const bool ok = dsto[i] >= 0 && iy >= 0 && iy < p.H;
@@ -281,6 +282,9 @@ __global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
   }
   __syncthreads();
 
+  // lane: output pixel (lane & 15) of a 16-pixel block, K group q = lane >> 4 (taps 2q and
+  // 2q + 1 of the first MFMA; q == 0 also feeds tap 8 to the second); D gives it channels
+  // 4q .. 4q+3 of its pixel
   const int co = lane & 15, q = lane >> 4;
   const _Float16 * W4 = reinterpret_cast<const _Float16 *>(p.w2);
   const h8s a1 = *reinterpret_cast<const h8s *>(W4 + co * 64 + 8 * q);
@@ -288,56 +292,61 @@ __global__ void __launch_bounds__(256) conv_stem_rows_kernel(const ConvParams p)
   float bias[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) bias[v] = (p.bias && 4 * q + v < p.Cout) ? p.bias[4 * q + v] : 0.0f;
+  // LDS offsets (halves) of the lane's taps relative to its pixel's window corner
+  const int ta = 2 * q, tb = 2 * q + 1;
+  const int off0 = ((ta / 3) * LW + ta % 3) * 4, off1 = ((tb / 3) * LW + tb % 3) * 4;
+  const int off8 = (2 * LW + 2) * 4;
   const int CB = (p.Wo + 15) >> 4;
-  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img;
-  auto tap_ld = [&](int r, int ox, int t) {
-    const int ky = t / 3, kx = t - 3 * ky;
-    return *reinterpret_cast<const h4s *>(srow + ((long)(2 * r + ky) * LW + 2 * ox + kx + 1) * 4);
-  };
-  // four blocks per pass: all LDS fragment reads first, then the MFMAs and the stores
-  const int nblk = TR * CB;
-  for (int base = wave; base < nblk; base += 16) {
-    h8s b1[4], b2[4];
+  const int px = lane & 15;
+  _Float16 * const yb = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + 4 * q;
+  const bool full = 4 * q + 4 <= p.Cout;
+  // blocks (output row r, 16-pixel column block cb); wave w takes cb = w, w + 4, ... four
+  // blocks per pass: all LDS fragment reads first, then the MFMAs and the stores
+  for (int r = 0; r < TR; ++r) {
+    const int oy = oy0 + r;
+    if (oy >= p.Ho) break;
+    const _Float16 * const rbase = srow + (2 * r * LW + 1) * 4;
+    _Float16 * const yrow = yb + (long)oy * p.Wo * p.y.cs;
+    for (int cb0 = wave; cb0 < CB; cb0 += 16) {
+      h8s b1[4], b2[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int blk = base + 4 * k < nblk ? base + 4 * k : base;
-      const int r = blk / CB, cb = blk - r * CB;
-      const int ox = cb * 16 + (lane & 15);
-      const int oxc = ox < p.Wo ? ox : p.Wo - 1;
-      const h4s t0 = tap_ld(r, oxc, 2 * q), t1 = tap_ld(r, oxc, 2 * q + 1);
-      const h4s t8 = q == 0 ? tap_ld(r, oxc, 8) : h4s{};
+      for (int k = 0; k < 4; ++k) {
+        const int cb = cb0 + 4 * k < CB ? cb0 + 4 * k : cb0;
+        const int ox = cb * 16 + px;
+        const _Float16 * src = rbase + 8 * (ox < p.Wo ? ox : p.Wo - 1);
+        const h4s t0 = *reinterpret_cast<const h4s *>(src + off0);
+        const h4s t1 = *reinterpret_cast<const h4s *>(src + off1);
+        const h4s t8 = q == 0 ? *reinterpret_cast<const h4s *>(src + off8) : h4s{};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        b1[k][e] = t0[e];
-        b1[k][4 + e] = t1[e];
-        b2[k][e] = t8[e];
-        b2[k][4 + e] = (_Float16)0.0f;
+        for (int e = 0; e < 4; ++e) {
+          b1[k][e] = t0[e];
+          b1[k][4 + e] = t1[e];
+          b2[k][e] = t8[e];
+          b2[k][4 + e] = (_Float16)0.0f;
+        }
       }
-    }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int blk = base + 4 * k;
-      f4s acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1[k], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b2[k], acc, 0, 0, 0);
-      if (blk >= nblk) continue;
-      const int r = blk / CB, cb = blk - r * CB;
-      const int ox = cb * 16 + (lane & 15), oy = oy0 + r;
-      if (oy >= p.Ho || ox >= p.Wo) continue;
-      _Float16 * yp = yb + ((long)oy * p.Wo + ox) * p.y.cs + 4 * q;
-      if (4 * q + 4 <= p.Cout) {
-        h4s hv;
+      for (int k = 0; k < 4; ++k) {
+        f4s acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1[k], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b2[k], acc, 0, 0, 0);
+        const int ox = (cb0 + 4 * k) * 16 + px;
+        if (cb0 + 4 * k >= CB || ox >= p.Wo) continue;
+        _Float16 * yp = yrow + (long)ox * p.y.cs;
+        if (full) {
+          h4s hv;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) hv[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
-        *reinterpret_cast<h4s *>(yp) = hv;
-      } else {
-        for (int v = 0; v < 4 && 4 * q + v < p.Cout; ++v) yp[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
+          for (int v = 0; v < 4; ++v) hv[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
+          *reinterpret_cast<h4s *>(yp) = hv;
+        } else {
+          for (int v = 0; v < 4 && 4 * q + v < p.Cout; ++v) yp[v] = (_Float16)act_fast<ACT>(acc[v] + bias[v]);
+        }
       }
     }
   }
 }
 
-constexpr int kStemTR = 4, kStemUIT = 4;
+constexpr int kStemTR = 2, kStemUIT = 2;
 
 // LDS bytes of the row-tiled stem for an input width
 static long stem_rows_lds(int W) { return (long)(2 * kStemTR + 1) * (W + 4) * 8; }
@@ -413,49 +422,73 @@ void launch_conv_direct(const ConvParams & p, hipStream_t s)
 // depthwise_blk.cl:118-228): y[c] = act(sum_k x[c]*w[c] + b[c]), K in {3,5}, S in {1,2}.
 // NHWC vector path: one lane = one output pixel x 8 channels, 16-byte loads/stores,
 // fp32 accumulation.  Weights packed fp32 [K][K][C].
-template <int K>
-__global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p)
+template <int K, int S, int PX, int ACT>
+__global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p, FastDiv d_c8, FastDiv d_strip, FastDiv d_ho)
 {
-  const int C8 = p.Cin >> 3;
-  const int HWo = p.Ho * p.Wo;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)p.batch * HWo * C8) return;
-  const int c8 = (int)(idx % C8);
-  const long pix = idx / C8;
-  const int b = (int)(pix / HWo), hw = (int)(pix % HWo);
-  const int oy = hw / p.Wo, ox = hw % p.Wo;
-  const int c = c8 * 8;
+  // lane = (8-channel group, strip of PX output pixels of one row), channel groups fastest so
+  // that neighbouring lanes read and write neighbouring 16-byte pieces
+  constexpr int NX = (PX - 1) * S + K;  // input columns of a strip
+  const int C8 = p.Cin >> 3, nstrip = (p.Wo + PX - 1) / PX;
+  const unsigned idx = blockIdx.x * 256u + threadIdx.x;
+  const unsigned q = fastdiv(idx, d_c8), rowi = fastdiv(q, d_strip), b = fastdiv(rowi, d_ho);
+  if (b >= (unsigned)p.batch) return;
+  const int c8 = (int)(idx - q * C8), strip = (int)(q - rowi * nstrip), oy = (int)(rowi - b * p.Ho);
+  const int c = c8 * 8, ox0 = strip * PX, ix0 = ox0 * S - p.P;
   const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img + c;
   const float * W = reinterpret_cast<const float *>(p.w) + c;
-  float acc[8];
+  float acc[PX][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int j = 0; j < PX; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
 #pragma unroll
   for (int ky = 0; ky < K; ++ky) {
-    const int iy = oy * p.S - p.P + ky;
+    const int iy = oy * S - p.P + ky;
     if ((unsigned)iy >= (unsigned)p.H) continue;
+    const _Float16 * xr = xb + (long)iy * p.W * p.x.cs;
+    h8 xv[NX];
+#pragma unroll
+    for (int t = 0; t < NX; ++t) {
+      const int ix = ix0 + t;
+      xv[t] = (unsigned)ix < (unsigned)p.W ? *reinterpret_cast<const h8 *>(xr + (long)ix * p.x.cs) : h8{};
+    }
 #pragma unroll
     for (int kx = 0; kx < K; ++kx) {
-      const int ix = ox * p.S - p.P + kx;
-      if ((unsigned)ix >= (unsigned)p.W) continue;
-      const h8 xv = *reinterpret_cast<const h8 *>(xb + ((long)iy * p.W + ix) * p.x.cs);
       const float4 w0 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin);
       const float4 w1 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin + 4);
-      acc[0] += (float)xv[0] * w0.x; acc[1] += (float)xv[1] * w0.y;
-      acc[2] += (float)xv[2] * w0.z; acc[3] += (float)xv[3] * w0.w;
-      acc[4] += (float)xv[4] * w1.x; acc[5] += (float)xv[5] * w1.y;
-      acc[6] += (float)xv[6] * w1.z; acc[7] += (float)xv[7] * w1.w;
+#pragma unroll
+      for (int j = 0; j < PX; ++j) {
+        const h8 v = xv[j * S + kx];
+        acc[j][0] += (float)v[0] * w0.x; acc[j][1] += (float)v[1] * w0.y;
+        acc[j][2] += (float)v[2] * w0.z; acc[j][3] += (float)v[3] * w0.w;
+        acc[j][4] += (float)v[4] * w1.x; acc[j][5] += (float)v[5] * w1.y;
+        acc[j][6] += (float)v[6] * w1.z; acc[j][7] += (float)v[7] * w1.w;
+      }
     }
   }
-  h8 out;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float v = acc[e] + (p.bias ? p.bias[c + e] : 0.0f);
-    v = act_f(v, p.act);
-    if (p.r.ptr) v += vld(p.r, b, c + e, hw);
-    out[e] = (_Float16)v;
+  float bv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (p.bias) {
+    const float4 b0 = *reinterpret_cast<const float4 *>(p.bias + c), b1 = *reinterpret_cast<const float4 *>(p.bias + c + 4);
+    bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+    bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
   }
-  *reinterpret_cast<h8 *>(reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + (long)hw * p.y.cs + c) = out;
+  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + c;
+  const _Float16 * rb = p.r.ptr ? reinterpret_cast<const _Float16 *>(p.r.ptr) + (long)b * p.r.img + c : nullptr;
+#pragma unroll
+  for (int j = 0; j < PX; ++j) {
+    const int ox = ox0 + j;
+    if (PX > 1 && ox >= p.Wo) break;
+    const long hw = (long)oy * p.Wo + ox;
+    h8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (_Float16)act_fast<ACT>(acc[j][e] + bv[e]);
+    if (rb) {  // act, one rounding, then the residual (the reference order)
+      const h8 rv = *reinterpret_cast<const h8 *>(rb + hw * p.r.cs);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (_Float16)((float)out[e] + (float)rv[e]);
+    }
+    *reinterpret_cast<h8 *>(yb + hw * p.y.cs) = out;
+  }
 }
 
 // Any-layout depthwise: one lane = one output element.
@@ -489,17 +522,49 @@ bool dwconv_vectorizable(const ConvParams & p)
   auto al = [](const View & v) {
     return v.layout == kNHWC && ((v.cs | (int)v.img | (int)(reinterpret_cast<uintptr_t>(v.ptr) >> 1)) & 7) == 0;
   };
-  return (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) && al(p.x) && al(p.y) &&
-         (!p.r.ptr || p.r.layout == kNHWC);
+  return (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2) && al(p.x) && al(p.y) &&
+         (!p.r.ptr || al(p.r)) && (long)p.batch * p.Ho * p.Wo * (p.Cin / 8) < (1L << 31);
+}
+
+// Output pixels per lane of the channels-last depthwise kernel (a strip of one row;
+// measured on MI355X: one pixel per lane 70 us, four 32 us for 64 channels at 80x80, batch
+// 64 -- neighbouring taps are reused from registers; eight is slower on the 5x5 layers).
+constexpr int kDwPx = 4;
+
+template <int K, int S, int ACT>
+static void launch_dw_t(const ConvParams & p, hipStream_t s)
+{
+  constexpr int PX = kDwPx;
+  const int nstrip = (p.Wo + PX - 1) / PX;
+  const long n = (long)p.batch * p.Ho * nstrip * (p.Cin / 8);
+  hipLaunchKernelGGL((dw_nhwc_kernel<K, S, PX, ACT>), dim3(nblk(n, 256)), dim3(256), 0, s, p,
+                     fastdiv_make((unsigned)(p.Cin / 8)), fastdiv_make((unsigned)nstrip), fastdiv_make((unsigned)p.Ho));
+}
+
+template <int K, int S>
+static void launch_dw_act(const ConvParams & p, hipStream_t s)
+{
+  switch (p.act) {
+  case kActSiLU: launch_dw_t<K, S, kActSiLU>(p, s); break;
+  case kActReLU: launch_dw_t<K, S, kActReLU>(p, s); break;
+  case kActHSwish: launch_dw_t<K, S, kActHSwish>(p, s); break;
+  case kActHSigmoid: launch_dw_t<K, S, kActHSigmoid>(p, s); break;
+  case kActSigmoid: launch_dw_t<K, S, kActSigmoid>(p, s); break;
+  default: launch_dw_t<K, S, kActNone>(p, s); break;
+  }
 }
 
 void launch_dwconv(const ConvParams & p, hipStream_t s)
 {
   const long M = (long)p.batch * p.Ho * p.Wo;
   if (dwconv_vectorizable(p)) {
-    const long n = M * (p.Cin / 8);
-    if (p.K == 3) hipLaunchKernelGGL(dw_nhwc_kernel<3>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(dw_nhwc_kernel<5>, dim3(nblk(n, 256)), dim3(256), 0, s, p);
+    if (p.K == 3) {
+      if (p.S == 1) launch_dw_act<3, 1>(p, s);
+      else launch_dw_act<3, 2>(p, s);
+    } else {
+      if (p.S == 1) launch_dw_act<5, 1>(p, s);
+      else launch_dw_act<5, 2>(p, s);
+    }
   } else {
     hipLaunchKernelGGL(dw_generic_kernel, dim3(nblk(M * p.Cin, 256)), dim3(256), 0, s, p);
   }

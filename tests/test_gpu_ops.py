@@ -174,10 +174,15 @@ def test_split_k(tmp_path, cin, cout, hw, k, s, batch):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("internal", [False, True], ids=["nchw_input", "channels_last"])
 @pytest.mark.parametrize("c,hw,k,s,act", [(16, 112, 3, 2, 3), (96, 14, 5, 1, 3), (72, 28, 5, 2, 3),
-                                          (20, 9, 3, 1, 2), (24, 10, 5, 2, 4)])
-def test_depthwise(tmp_path, c, hw, k, s, act):
-    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=act)
+                                          (20, 9, 3, 1, 2), (24, 10, 5, 2, 4), (64, 23, 3, 1, 1)])
+def test_depthwise(tmp_path, c, hw, k, s, act, internal):
+    """Depthwise convs on the plan's NCHW graph input (one lane per element) and on an
+    internal channels-last tensor (8 channels x a strip of pixels per lane; odd widths leave
+    partial strips)."""
+    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=act, pre_relu=internal)
+    assert _conv_kernel(path, 2) == "dwconv"
     _check_f32(path, 2, lo=-1.0)
 
 
