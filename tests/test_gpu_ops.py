@@ -44,12 +44,22 @@ def _conv_kernel(path, batch, flags=0):
     return next(k for k in _kernels(path, batch, flags) if k.startswith(("conv", "dwconv")))
 
 
+def _diagnose(g, r):
+    """On a mismatch: where and how the result differs (printed with the failure)."""
+    gf, rf = O.h2f(g).ravel(), O.h2f(r).ravel()
+    bad = np.flatnonzero(np.abs(gf - rf) > 1e-2 * (np.abs(rf).max() + 1e-6))
+    print(f"  mismatching elements {bad.size} of {gf.size}; first at {bad[:8].tolist()}")
+    print(f"  got NaN {int(np.isnan(gf).sum())} zeros {int((gf == 0).sum())}; got[:8] {gf[:8]} ref[:8] {rf[:8]}")
+
+
 def _check_f32(path, batch, seed=0, ref_mode=True, **kw):
     p, x, got = _run(path, batch, seed, **kw)
     ref = O.run_plan(p, x, batch)
     for g, r in zip(got, ref):
         mean_rel, max_rel, max_abs, _ = O.rel_errors(O.h2f(g), O.h2f(r.ravel()))
         print(f"{path}: vs f32 oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e} max_abs={max_abs:.2e}")
+        if not (mean_rel < F32_MEAN and max_rel < F32_MAX):
+            _diagnose(g, r)
         assert mean_rel < F32_MEAN and max_rel < F32_MAX
     if ref_mode:
         refr = O.run_plan(p, x, batch, mode=O.REF)
@@ -234,6 +244,8 @@ def test_small_ops(tmp_path, name):
     else:
         mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(g), O.h2f(ref))
         print(f"{name}: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+        if not (mean_rel < F32_MEAN and max_rel < F32_MAX):
+            _diagnose(g, ref)
         assert mean_rel < F32_MEAN and max_rel < F32_MAX
 
 
