@@ -65,10 +65,10 @@ def sweep_plan(pw, d, name):
     return pb.write()
 
 
-def layer_runs(ia, pw, name, batch, iters):
+def layer_runs(ia, pw, name, batch, iters, flags=0):
     """One sweep layer's plan, `iters` eager passes (for counter collection on that conv)."""
     with tempfile.TemporaryDirectory() as d:
-        m = ia.PlanModel(sweep_plan(pw, d, name), 0, batch, ia.IVH_FLAG_NO_GRAPH)
+        m = ia.PlanModel(sweep_plan(pw, d, name), 0, batch, ia.IVH_FLAG_NO_GRAPH | flags)
         x0 = np.random.default_rng(0).random(m.inputNumel() * batch, dtype=np.float32)
         m.setInput(x0.astype(np.float16).view(np.uint16), batch)
         for _ in range(iters):
@@ -180,6 +180,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="launch node by node instead of replaying the captured HIP graph")
     ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer for --phase layer")
+    ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
+                    help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
     ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
                          "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE; "
@@ -200,7 +202,7 @@ def main():
         conv_sweep(ia, pw, args.batch, max(args.profile_iters, 10))
         return
     if args.phase == "layer":
-        layer_runs(ia, pw, args.layer, args.batch, args.steps)
+        layer_runs(ia, pw, args.layer, args.batch, args.steps, args.flags)
         return
     tmp = tempfile.TemporaryDirectory()
     path, flops_img = pw.MODELS[args.model](tmp.name, seed=0, imgsz=args.imgsz)

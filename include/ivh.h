@@ -53,6 +53,8 @@ extern "C" {
 #define IVH_FLAG_ASYNC 0x20u      /* ivh_run returns without waiting for the device */
 #define IVH_FLAG_NO_SPLITK 0x80u  /* never split the K loop of an implicit-GEMM conv */
 #define IVH_FLAG_NO_HALO 0x100u   /* 3x3 convs use the im2col path, never the LDS halo tile */
+#define IVH_FLAG_NO_RESIDENT 0x200u /* 3x3 stride-1 convs never keep their weights resident in
+                                       LDS (the halo tile or im2col path instead) */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 

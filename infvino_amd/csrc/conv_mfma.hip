@@ -320,6 +320,10 @@ void launch_conv_igemm(const ConvParams & p, hipStream_t s)
     for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_igemm(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
     return;
   }
+  if (p.res) {
+    launch_conv_res(p, s);
+    return;
+  }
   if (p.halo) {
     launch_conv_halo(p, s);
     return;

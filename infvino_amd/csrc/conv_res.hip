@@ -1,0 +1,469 @@
+// 3x3 stride-1 pad-1 convolution with Cin <= 64 on gfx950 fp16 MFMA, weights resident in LDS.
+//
+// Replaces, for the narrow layers that dominate the YOLO heads and C2f/C3k2 bottlenecks, the
+// reference's conv3x3_ov (kernels/conv_ov.cl:133-297), conv3x3_blk (conv_blk.cl:118-296) and
+// conv3x3_f16 (conv.cl:150-414):
+//   y[co][p] = act(sum_{tap,ci} W[co][ci][tap] x[ci][p + tap] + b[co]) (+ r[co][p]).
+//
+// With Cin <= 64 the whole K range (9 taps x Cin) of a BN-channel block is at most 74 KB of
+// fp16, so a work-group loads it into LDS once and keeps it there.  The grid is persistent
+// (about one work-group per CU); each work-group walks a contiguous range of output tiles of
+// the batch-as-one-tall-image (image b at rows [b*(H+1), b*(H+1)+H), a zero separator row
+// after each image, as in conv_halo.hip).  Per tile:
+//   * the (TH+2) x (TW+2) x CK input patch is in LDS; 9*CK/16 MFMA K slices run back to
+//     back with no barrier (every operand is already resident);
+//   * the next two tiles' patches are in flight in registers (buffer loads issued two tiles
+//     ahead, out-of-image pixels read zeros from past the buffer's range);
+//   * the previous tile's epilogue (bias, activation, fp16 rounding into an LDS staging
+//     tile) is interleaved with this tile's MFMAs, so its VALU work -- two transcendentals
+//     per SiLU output -- overlaps the matrix pipe instead of following it;
+//   * two barriers per tile: then the staged outputs go to HBM as 16-byte channels-last
+//     pieces (+ residual) and the next patch is written to LDS.
+// Wave layout: the 4 waves split the tile's pixels (TM 32-pixel blocks each) and share all
+// BN = TN*32 channels, so an A (weight) fragment feeds TM MFMAs and a B (pixel) fragment TN.
+#include <algorithm>
+
+#include "conv_common.hpp"
+#include "kernels.hpp"
+
+namespace ivh {
+
+typedef unsigned u2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+
+template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, int ACT, bool RES, bool CF>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const ConvParams p)
+{
+  using F = Mf<32>;
+  typedef F::acc_t acc_t;
+  constexpr int NT = 64 * WGM * WGN;         // threads
+  constexpr int BN = WGN * TN * 32;
+  constexpr int NS = CK / 16;              // MFMA K slices per tap
+  constexpr int NSL = 9 * NS;              // K slices per tile
+  constexpr int KROW = 9 * CK;             // weights per output channel kept in LDS
+  constexpr int LDK = KROW + 8;            // weight row pitch (halves): conflict-free reads
+  constexpr int CKP = CK + 8;              // patch pixel pitch (halves)
+  constexpr int CQ = CK / 8;               // 16-byte pieces per patch pixel
+  constexpr int P_IT = (PMAX * CQ + NT - 1) / NT;
+  constexpr int WQ = KROW / 8;             // 16-byte pieces per weight row
+  constexpr int W_IT = (BN * WQ + NT - 1) / NT;
+  constexpr int NG = TN * TM * 4;          // epilogue groups (4 accumulator values) per lane
+  __shared__ __attribute__((aligned(16))) _Float16 lds[BN * LDK + PMAX * CKP];
+  __shared__ __attribute__((aligned(16))) float bias_s[BN];
+  _Float16 * const Ws = lds;
+  _Float16 * const Ps = lds + BN * LDK;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WGM, wn = wave / WGM;
+  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW;
+  const int Hs = p.H + 1;                       // rows per image incl. separator
+  const int tiles_x = (p.W + TW - 1) / TW;
+  const int ntiles = ((p.batch * Hs - 1 + TH - 1) / TH) * tiles_x;
+  // this work-group's contiguous tile range; XCD-aware so neighbouring ranges (which share
+  // input rows at their ends) run on one XCD
+  const int G = gridDim.x;
+  const int r = xcd_tile(blockIdx.x, G);
+  const int t_lo = (int)((long)r * ntiles / G), t_hi = (int)((long)(r + 1) * ntiles / G);
+  const int ntl = t_hi - t_lo;
+  if (ntl <= 0) return;
+  const int n0 = blockIdx.y * BN;
+  const float inv_tw = __builtin_amdgcn_rcpf((float)TW), inv_pw = __builtin_amdgcn_rcpf((float)PW);
+
+  const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
+
+  // patch pieces of this thread: element e = tid + NT i -> patch pixel e / CQ (row, column
+  // packed as row << 16 | column; row 0x7fff past the patch), piece e % CQ = tid % CQ
+  const int q8 = (tid % CQ) * 8;
+  int pyx[P_IT];
+#pragma unroll
+  for (int i = 0; i < P_IT; ++i) {
+    const int pp = (tid + i * NT) / CQ;
+    const int py = idiv_small(pp, PW, inv_pw);
+    pyx[i] = pp < PP ? (py << 16) | (pp - py * PW) : 0x7fff0000;
+  }
+  // tile t -> first output row (image b0, row r0 of it) and column of the tall image
+  auto tile_origin = [&](int t, int & b0, int & r0, int & ox0) __attribute__((always_inline)) {
+    const int ty = t / tiles_x;
+    const int oy0 = ty * TH;
+    b0 = oy0 / Hs;
+    r0 = oy0 - b0 * Hs;
+    ox0 = (t - ty * tiles_x) * TW;
+  };
+  // input pixel (b0 + 1, r - Hs) is at (b0, r) + delta: crossing one image boundary
+  const int xcs = p.x.cs, xwcs = p.W * p.x.cs;
+  const int xdelta = (int)p.x.img - Hs * xwcs;
+  // patch of tile t into registers: branch-free offsets, out-of-image pixels read zeros
+  auto load_patch = [&](int t, h8 (&rp)[P_IT]) __attribute__((always_inline)) {
+    int b0, r0, ox0;
+    tile_origin(t, b0, r0, ox0);
+    // first patch row is output row - 1: step back one row (into the previous image's
+    // separator, or -1 above the first image)
+    int rb = r0 - 1, bb = b0;
+    if (rb < 0 && bb > 0) {
+      rb += Hs;
+      --bb;
+    }
+    const bool next_ok = bb + 1 < p.batch;
+    const int base = bb * (int)p.x.img + (rb * p.W + ox0 - 1) * xcs + q8;
+#pragma unroll
+    for (int i = 0; i < P_IT; ++i) {
+      const int py = pyx[i] >> 16, px = pyx[i] & 0xffff;
+      const int rr = rb + py;
+      const bool wrap = rr >= Hs;
+      const int rw = wrap ? rr - Hs : rr;
+      const int ix = ox0 - 1 + px;
+      const bool ok = (unsigned)rw < (unsigned)p.H && (unsigned)ix < (unsigned)p.W && (!wrap || next_ok);
+      const int off = base + __umul24(py, xwcs) + __umul24(px, xcs) + (wrap ? xdelta : 0);
+      const unsigned src = ok ? (unsigned)off * 2u : kBufOOB;
+      rp[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, src, 0, 0));
+    }
+  };
+  // ragged Cin: channels >= Cin of a piece are zeroed bitwise (padding channels or the next
+  // pixel's data never reach the MFMAs)
+  const bool ragged = (p.Cin % CK) != 0;
+  u16x8 keep;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) keep[k] = q8 + k < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+  auto store_patch = [&](const h8 (&rp)[P_IT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < P_IT; ++i) {
+      const int e = tid + i * NT;
+      if (i * NT + NT <= PMAX * CQ || e < PMAX * CQ) {
+        h8 v = rp[i];
+        if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
+        *reinterpret_cast<h8 *>(Ps + (e / CQ) * CKP + q8) = v;
+      }
+    }
+  };
+
+  h8 rpA[P_IT], rpB[P_IT];  // patches of tiles i + 1 and i + 2 in flight
+
+  // ---- prologue: bias and weights into LDS, first patch
+  if (tid < BN) bias_s[tid] = p.bias ? p.bias[n0 + tid] : 0.0f;
+  {
+    h8 rw[W_IT];
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i) {
+      const int e = tid + i * NT, row = e / WQ, q = e - row * WQ;
+      const unsigned src = e < BN * WQ ? (unsigned)((row * p.kpad + q * 8) * 2) : kBufOOB;
+      rw[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, src, 0, 0));
+    }
+    load_patch(t_lo, rpA);
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i) {
+      const int e = tid + i * NT, row = e / WQ, q = e - row * WQ;
+      if (e < BN * WQ) *reinterpret_cast<h8 *>(Ws + row * LDK + q * 8) = rw[i];
+    }
+    store_patch(rpA);
+  }
+  // the next two tiles' patches in flight (each is issued two tiles before it is needed)
+  load_patch(t_lo + (1 < ntl ? 1 : 0), rpA);
+  load_patch(t_lo + (2 < ntl ? 2 : 0), rpB);
+  __syncthreads();
+
+  // ---- per-lane fragment addresses and output slots (tile-independent)
+  int bl[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int pl = wm * TM * 32 + tm * 32 + F::col(lane);
+    const int pc = pl < TH * TW ? pl : 0;  // slot past the tile: computed on pixel 0, never stored
+    const int ty = idiv_small(pc, TW, inv_tw), tx = pc - ty * TW;
+    bl[tm] = (ty * PW + tx) * CKP + F::kq(lane);
+  }
+  const int arow = (wn * TN * 32 + (lane & 31)) * LDK + F::kq(lane);
+  int tapoff[9];
+#pragma unroll
+  for (int tap = 0; tap < 9; ++tap) tapoff[tap] = ((tap / 3) * PW + (tap % 3)) * CKP;
+
+  // output byte offsets of this lane's pixel blocks in tile t (past the buffer range: no
+  // output), for y and the residual view.  Stores and residual loads are buffer accesses
+  // whose out-of-range lanes are dropped / read zeros, so the epilogue has no branches.
+  int syx[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int pl = wm * TM * 32 + tm * 32 + F::col(lane);
+    const int ty = idiv_small(pl, TW, inv_tw);
+    syx[tm] = pl < TH * TW ? (ty << 16) | (pl - ty * TW) : 0x7fff0000;
+  }
+  auto out_offsets = [&](int t, unsigned (&yo)[TM], unsigned (&ro)[TM]) __attribute__((always_inline)) {
+    int b0, r0, ox0;
+    tile_origin(t, b0, r0, ox0);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      int rr = r0 + (syx[tm] >> 16), b = b0;
+      if (rr >= Hs) {  // TH + 2 <= Hs: at most one image boundary inside a tile
+        rr -= Hs;
+        ++b;
+      }
+      const int ox = ox0 + (syx[tm] & 0xffff);
+      const bool ok = rr < p.H && b < p.batch && ox < p.W;
+      const unsigned hw = (unsigned)(rr * p.W + ox);
+      yo[tm] = ok ? ((unsigned)b * (unsigned)p.y.img + hw * (unsigned)p.y.cs + (unsigned)n0) * 2u : kBufOOB;
+      if (RES) ro[tm] = ok ? ((unsigned)b * (unsigned)p.r.img + hw * (unsigned)p.r.cs + (unsigned)n0) * 2u : kBufOOB;
+    }
+  };
+  const int cl0 = wn * TN * 32 + F::row(lane, 0);  // lane's first channel in the block
+  // CF with Cout % 4 != 0: the last group also writes the view's padding channels (p.ypad)
+  const long y_last = (long)(p.batch - 1) * p.y.img + ((long)p.H * p.W - 1) * p.y.cs + (CF ? (p.Cout + 3) & ~3 : p.Cout);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(p.y.ptr, (short)0, (int)(y_last * 2), kBufDword3);
+  const long r_last = RES ? (long)(p.batch - 1) * p.r.img + ((long)p.H * p.W - 1) * p.r.cs + p.Cout : 0;
+  const __amdgpu_buffer_rsrc_t rr_ = __builtin_amdgcn_make_buffer_rsrc(RES ? p.r.ptr : p.y.ptr, (short)0,
+                                                                       (int)(r_last * 2), kBufDword3);
+  // lane channel cl (within the block) -> byte offset or out of range
+  auto chan_off = [&](unsigned base, int cl) __attribute__((always_inline)) {
+    return n0 + cl < p.Cout ? base + (unsigned)cl * 2u : kBufOOB;
+  };
+  // residual values of this lane's outputs in tile t (channels-last, 4 channels a load)
+  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
+      rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
+    }
+  };
+  // epilogue group g of tile accumulators ac: bias + activation in fp32, one rounding, then
+  // + residual (rounded again), stored as 4 channels-last fp16 values (CF), else element by
+  // element
+  auto epi_group = [&](const acc_t (&ac)[TN][TM], const unsigned (&yo)[TM], const h4 (&rv)[NG], int g)
+      __attribute__((always_inline)) {
+    const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
+    const int cl = tn * 32 + cl0 + 2 * v4;  // F::row(lane, v4)
+    const float4 b4 = *reinterpret_cast<const float4 *>(bias_s + cl);
+    // The fp32 results pass through an empty asm so that every copy of this code (there is
+    // one per accumulator set, and the last tile's) rounds them the same way: fp32, then
+    // one fp16 rounding, never a fused multiply-convert.  An image's outputs then do not
+    // depend on which tile, and so which batch size, computed them.
+    float o[4] = {act_fast<ACT>(ac[tn][tm][v4 + 0] + b4.x), act_fast<ACT>(ac[tn][tm][v4 + 1] + b4.y),
+                  act_fast<ACT>(ac[tn][tm][v4 + 2] + b4.z), act_fast<ACT>(ac[tn][tm][v4 + 3] + b4.w)};
+    h4 hv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      __asm__("" : "+v"(o[k]));
+      hv[k] = (_Float16)o[k];
+    }
+    if (RES) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = (_Float16)((float)hv[k] + (float)rv[g][k]);
+    }
+    if (CF) {
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, hv), yr, chan_off(yo[tm], cl), 0, 0);
+    } else {
+      // (bit-cast the whole vector: hipcc reads element 0 for a bit cast of hv[k])
+      const u16x4 hu = __builtin_bit_cast(u16x4, hv);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) __builtin_amdgcn_raw_buffer_store_b16(hu[k], yr, chan_off(yo[tm], cl + k), 0, 0);
+    }
+  };
+
+  // one tile: residual loads of this tile, MFMAs over the resident patch with the previous
+  // tile's epilogue interleaved (accp / yop / rvp; on the first tile they hold zeros and
+  // out-of-range offsets and store nothing), then the two-barrier patch hand-over
+  auto tile = [&](acc_t (&acc)[TN][TM], const acc_t (&accp)[TN][TM], unsigned (&yo)[TM], const unsigned (&yop)[TM],
+                  h4 (&rv)[NG], const h4 (&rvp)[NG], h8 (&rp)[P_IT], int i) __attribute__((always_inline)) {
+    unsigned ro[TM];
+    out_offsets(t_lo + i, yo, ro);
+    if (RES) load_res(ro, rv);
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b)
+#pragma unroll
+        for (int v = 0; v < F::NV; ++v) acc[a][b][v] = 0.0f;
+    // K slices with the fragments of slice s + 1 read from LDS while slice s's MFMAs run
+    // (two register sets); the epilogue groups spread evenly over the slices, with a
+    // residual from a third of the way in (its loads, issued at the tile's start, land)
+    h8 fa[2][TN], fb[2][TM];
+    auto frags = [&](int s, h8 (&a)[TN], h8 (&b)[TM]) __attribute__((always_inline)) {
+      const int tap = s / NS, j = s % NS;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        a[tn] = *reinterpret_cast<const h8 *>(Ws + arow + tn * 32 * LDK + tap * CK + j * 16);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) b[tm] = *reinterpret_cast<const h8 *>(Ps + bl[tm] + tapoff[tap] + j * 16);
+    };
+    constexpr int S0 = RES ? NSL / 3 : 0, SPAN = NSL - S0;
+    frags(0, fa[0], fb[0]);
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const int s = tap * NS + j;
+        if (s + 1 < NSL) frags(s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+          for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = F::mma(fa[s & 1][tn], fb[s & 1][tm], acc[tn][tm]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          if (S0 + g * SPAN / NG == s) epi_group(accp, yop, rvp, g);
+      }
+    }
+    __syncthreads();  // patch reads done
+    if (i + 1 < ntl) {
+      store_patch(rp);  // tile i + 1
+      load_patch(t_lo + (i + 3 < ntl ? i + 3 : i + 1), rp);
+      __syncthreads();  // next patch in LDS
+    }
+  };
+
+  acc_t accA[TN][TM], accB[TN][TM];
+  unsigned yoA[TM], yoB[TM];
+  h4 rvA[NG], rvB[NG];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int v = 0; v < F::NV; ++v) accB[a][b][v] = 0.0f;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) yoB[tm] = kBufOOB;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) rvB[g] = h4{};
+  for (int i = 0; i < ntl; i += 2) {
+    tile(accA, accB, yoA, yoB, rvA, rvB, rpA, i);
+    if (i + 1 < ntl) tile(accB, accA, yoB, yoA, rvB, rvA, rpB, i + 1);
+  }
+  // last tile's epilogue
+  if (ntl & 1) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) epi_group(accA, yoA, rvA, g);
+  } else {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) epi_group(accB, yoB, rvB, g);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+namespace {
+struct ResCfgDesc {
+  int bm, bn, pmax;
+};
+// Eight waves (two per SIMD, so one wave's epilogue VALU work overlaps the other's MFMAs):
+//   0: 4 x 2 waves of 2 x 1 blocks (BM 256, BN 64; Cout > 32)
+//   1: 8 x 1 waves of 2 x 1 blocks (BM 512, BN 32; Cout <= 32, Cin <= 32)
+//   2: 8 x 1 waves of 1 x 1 blocks (BM 256, BN 32; Cout <= 32, Cin > 32)
+// Patch sizes keep resident weights + patch within the 160 KB of LDS at Cin 64.
+constexpr int kResP0 = 352, kResP1 = 720, kResP2 = 352;
+constexpr ResCfgDesc kResCfg[3] = {{256, 64, kResP0}, {512, 32, kResP1}, {256, 32, kResP2}};
+constexpr int kResCUs = 256;  // one work-group per CU
+}  // namespace
+
+int res_ck(int cin) { return cin <= 32 ? 32 : 64; }
+int res_bn(int cfg) { return kResCfg[cfg].bn; }
+int res_bm(int cfg) { return kResCfg[cfg].bm; }
+int res_pmax(int cfg) { return kResCfg[cfg].pmax; }
+
+long res_tiles(const ConvParams & p)
+{
+  const long Htot = (long)p.batch * (p.H + 1) - 1;
+  return ((Htot + p.th - 1) / p.th) * ((p.W + p.tw - 1) / p.tw);
+}
+
+// Persistent grid: about one work-group per CU over all channel blocks, a multiple of the
+// 8 XCDs when it is that large.
+int res_grid_x(const ConvParams & p, int cfg)
+{
+  const int nblk = (p.Cout + kResCfg[cfg].bn - 1) / kResCfg[cfg].bn;
+  long g = std::max(1, kResCUs / nblk);
+  if (g >= 8) g = g / 8 * 8;
+  return (int)std::min<long>(g, res_tiles(p));
+}
+
+bool res_full_stores(const ConvParams & p) { return p.Cout % 4 == 0 || p.ypad >= 4 - p.Cout % 4; }
+
+bool res_views_ok(const ConvParams & p)
+{
+  auto ok = [&](const View & v) {
+    if (v.layout != kNHWC || (v.cs % 4) || (v.img % 4) || (reinterpret_cast<uintptr_t>(v.ptr) % 8)) return false;
+    const long last = (long)(p.batch - 1) * v.img + ((long)p.H * p.W - 1) * v.cs + p.Cout + 3;
+    return last * 2 < (1L << 31) && (long)p.batch * v.img < (1L << 31);
+  };
+  if (!ok(p.y)) return false;
+  if (p.r.ptr && (!ok(p.r) || p.Cout % 4)) return false;
+  return p.H == p.Ho && p.W == p.Wo && (long)p.W * p.x.cs < (1L << 23);
+}
+
+bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw)
+{
+  if (cin > 64 || cin <= 16 || H < 3 || W < 2 || (long)batch * (H + 1) >= (1L << 22) || W >= (1 << 22)) return false;
+  if (act != kActNone && act != kActSiLU && act != kActReLU && act != kActHSwish) return false;
+  const int ck = res_ck(cin);
+  const int c = cout > 32 ? 0 : (ck == 64 ? 2 : 1);
+  const ResCfgDesc & d = kResCfg[c];
+  const int nblk = (cout + d.bn - 1) / d.bn;
+  long g = std::max(1, kResCUs / nblk);
+  if (g >= 8) g = g / 8 * 8;
+  const long Htot = (long)batch * (H + 1) - 1;
+  // fewest rounds of tiles per work-group first (the critical path), then the least work
+  // over the chip: MFMA slots plus patch fill of every tile
+  long best_rounds = 1L << 40;
+  double best = 1e30;
+  for (int w = 1; w <= W && w <= d.bm; ++w) {
+    int h = std::min(d.bm / w, H - 1);           // TH + 2 <= H + 1
+    h = (int)std::min<long>(h, Htot);
+    h = std::min(h, d.pmax / (w + 2) - 2);
+    if (h < 1) continue;
+    const long ty = (Htot + h - 1) / h, tx = (W + w - 1) / w;
+    const int hh = (int)((Htot + ty - 1) / ty), ww = (int)((W + tx - 1) / tx);  // balanced
+    const long n = ty * tx;
+    const long rounds = (n + std::min<long>(g, n) - 1) / std::min<long>(g, n);
+    const double work = (double)n * (d.bm + 0.1 * (hh + 2) * (ww + 2));
+    if (rounds < best_rounds || (rounds == best_rounds && work < best)) {
+      best_rounds = rounds;
+      best = work;
+      *th = hh;
+      *tw = ww;
+    }
+  }
+  if (best >= 1e30) return false;
+  *cfg = c;
+  return true;
+}
+
+template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, bool RES, bool CF>
+static void launch_res_act(const ConvParams & p, int cfg, hipStream_t s)
+{
+  constexpr int BN = WGN * TN * 32;
+  dim3 grid((unsigned)res_grid_x(p, cfg), (unsigned)((p.Cout + BN - 1) / BN), 1), block(64 * WGM * WGN);
+  switch (p.act) {
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActSiLU, RES, CF>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActReLU, RES, CF>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActHSwish, RES, CF>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActNone, RES, CF>), grid, block, 0, s, p); break;
+  }
+}
+
+// residual adds need Cout % 4 == 0 (res_views_ok); CF: 4-channel stores (Cout % 4 == 0, or the
+// output view's padding channels absorb the rounding up)
+template <int WGM, int WGN, int TM, int TN, int CK, int PMAX>
+static void launch_res_cfg(const ConvParams & p, int cfg, hipStream_t s)
+{
+  if (p.r.ptr) launch_res_act<WGM, WGN, TM, TN, CK, PMAX, true, true>(p, cfg, s);
+  else if (res_full_stores(p)) launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, true>(p, cfg, s);
+  else launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, false>(p, cfg, s);
+}
+
+void launch_conv_res(const ConvParams & p, hipStream_t s)
+{
+  const int bc = conv_batch_chunk(p);
+  if (bc < p.batch) {
+    for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_res(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
+    return;
+  }
+  const int cfg = p.res - 1;
+  if (cfg == 0) {
+    if (p.ck == 32) launch_res_cfg<4, 2, 2, 1, 32, kResP0>(p, cfg, s);
+    else launch_res_cfg<4, 2, 2, 1, 64, kResP0>(p, cfg, s);
+  } else if (cfg == 1) {
+    launch_res_cfg<8, 1, 2, 1, 32, kResP1>(p, cfg, s);
+  } else {
+    launch_res_cfg<8, 1, 1, 1, 64, kResP2>(p, cfg, s);
+  }
+}
+
+}  // namespace ivh

@@ -861,6 +861,10 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     p.act = n.i("act");
     p.x = view(xt.name, batch);
     p.y = view(yt.name, batch);
+    if (p.y.layout == kNHWC && yt.kind != Tensor::kInit) {
+      const Root & yr = *roots_.at(yt.root);
+      if (yt.coff + p.Cout == yr.C) p.ypad = yr.cs - yr.C;
+    }
     if (has(3)) {
       const Tensor & rt = *T_[n.ins[3]];
       if (rt.numel != yt.numel) fail("residual numel mismatch");
@@ -1177,7 +1181,9 @@ void Model::validate(const Launch & l) const
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout, HWo), 2, "conv y");
+    // the resident-weight kernel writes 4-channel groups into the view's padding channels
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res && res_full_stores(p) ? (4 - p.Cout % 4) % 4 : 0), HWo), 2,
+          "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
     if (p.bias) check(p.bias, 0, (l.kind == Launch::kIgemm ? (p.Cout + 127) / 128 * 128 : p.Cout) - 1, 4, "conv bias");
@@ -1196,6 +1202,19 @@ void Model::validate(const Launch & l) const
         if (p.kpad != (p.Cin + ck - 1) / ck * halo_taps(ck) * ck) throw std::runtime_error("halo weight packing");
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("halo geometry too large");
       }
+      if (p.res) {
+        const int cfg = p.res - 1, ck = p.ck;
+        if (cfg < 0 || cfg > 2 || p.halo || p.s2 || ck != res_ck(p.Cin) || p.Cin > ck || p.K != 3 || p.S != 1 ||
+            p.P != 1 || p.ksplit != 1 || p.th < 1 || p.tw < 1 || p.Ho != p.H || p.Wo != p.W ||
+            p.th * p.tw > res_bm(cfg) || (p.th + 2) * (p.tw + 2) > res_pmax(cfg) || p.th + 2 > p.H + 1 ||
+            (cfg == 0) != (p.Cout > 32) || (cfg == 2) != (p.Cout <= 32 && ck == 64) || !res_views_ok(p))
+          throw std::runtime_error("resident-weight conv geometry");
+        if (p.kpad != halo_taps(ck) * ck) throw std::runtime_error("resident-weight packing");
+        if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("resident-weight geometry too large");
+        const long bn = res_bn(cfg), nrows = (p.Cout + bn - 1) / bn * bn;
+        check(p.w, 0, nrows * p.kpad - 1, 2, "resident-weight w");
+        if (res_grid_x(p, cfg) < 1 || res_grid_x(p, cfg) > 65535) throw std::runtime_error("resident-weight grid");
+      }
       if (p.s2) {
         const int cfg = p.s2 - 1;
         if (cfg < 0 || cfg > 1 || p.halo || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
@@ -1209,8 +1228,9 @@ void Model::validate(const Launch & l) const
         if ((size_t)p.ksplit * rows * M > ws_floats_) throw std::runtime_error("split-K workspace too small");
         check(p.ws, 0, (long)p.ksplit * rows * M - 1, 4, "igemm split-K workspace");
       }
-      if (p.kpad % kIgemmBK || (!p.halo && (p.bk != 32 && p.bk != 64))) throw std::runtime_error("kpad not a multiple of the K tile");
-      if (!p.halo && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
+      if (p.kpad % kIgemmBK && !p.res) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (!p.halo && !p.res && (p.bk != 32 && p.bk != 64)) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (!p.halo && !p.res && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
     } else if (l.kind == Launch::kDirect && p.stem_mfma) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
       check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");
@@ -1500,7 +1520,7 @@ std::string Model::nodeKernel(int i)
   const Launch & l = L[node_launch_begin_[i]];
   switch (l.kind) {
   case Launch::kIgemm:
-    return l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
+    return l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   default: return s.kernel;

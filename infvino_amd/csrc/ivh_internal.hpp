@@ -76,6 +76,12 @@ struct ConvParams {
   int halo = 0;
   int th = 0, tw = 0;
   int ck = 0;  // input-channel chunk of the halo weight packing (16 / 32 / 64)
+  // 3x3 stride-1 pad-1 resident-weight kernel (conv_res.hip, Cin <= ck): config + 1 (0: not
+  // used); th x tw and ck as for the halo kernel, w the single-chunk halo packing
+  int res = 0;
+  // channels after the output view's last one that belong to no tensor (the padding of a
+  // channels-last root whose last channel range this view is); a kernel may write there
+  int ypad = 0;
   // 3x3 stride-2 small-channel kernel (conv_s2.hip): config + 1 (0: not used); th x tw is
   // then the output tile of one image and w the implicit-GEMM packing
   int s2 = 0;

@@ -27,6 +27,21 @@ int halo_bn(int cfg);
 int halo_pmax(int cfg);
 void launch_conv_halo(const ConvParams & p, hipStream_t s);
 
+// conv_res.hip: 3x3 stride-1 pad-1 convs with 16 < Cin <= 64, weights resident in LDS
+int res_ck(int cin);                 // channel chunk (= Cin rounded up to 32 / 64)
+int res_bn(int cfg);
+int res_bm(int cfg);
+int res_pmax(int cfg);
+long res_tiles(const ConvParams & p);
+int res_grid_x(const ConvParams & p, int cfg);
+// config and output tile th x tw for a layer at a batch size; false: not eligible
+bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw);
+// the output (and residual) views suit the kernel's 8-byte channels-last buffer stores
+bool res_views_ok(const ConvParams & p);
+bool res_full_stores(const ConvParams & p);  // 4-channel stores (Cout % 4 == 0 or padding)
+constexpr int kResMinTiles = 1;      // fewer tiles: the halo / im2col kernels
+void launch_conv_res(const ConvParams & p, hipStream_t s);
+
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
 bool s2_plan(int cin, int cout, int Ho, int Wo, int * cfg, int * th, int * tw);
 int s2_patch(int th, int tw);  // patch pixels of a th x tw output tile

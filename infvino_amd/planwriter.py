@@ -555,15 +555,19 @@ def mobilenetv3_small(out_dir, seed=0, imgsz=224, num_classes=1000):
 # ------------------------------------------------------------- single ops
 
 def single_conv(out_dir, cin, cout, H, W, k=1, s=1, groups=1, act=ACT_SILU, seed=0,
-                bias=True, pre_relu=False):
+                bias=True, pre_relu=False, post_relu=False):
     """One conv node (the conv sweep configs).  Returns (plan path, FLOPs/image).
     pre_relu: a ReLU between the graph input and the conv, so that the conv reads an
-    internal tensor (channels-last in the HIP backend) as it does inside a model."""
+    internal tensor (channels-last in the HIP backend) as it does inside a model.
+    post_relu: a ReLU between the conv and the graph output, so that the conv writes an
+    internal tensor too (with act = 0 the ReLU folds into the conv)."""
     pb = PlanBuilder(out_dir, seed)
     x = pb.input("x", [1, cin, H, W])
     if pre_relu:
         x = pb.unary(x, UN_RELU)
     y = pb.conv(x, cout, k, s, groups=groups, act=act, bias=bias)
+    if post_relu:
+        y = pb.unary(y, UN_RELU)
     pb.output(y)
     return pb.write(), pb.flops
 

@@ -79,7 +79,7 @@ def test_conv1x1_config(tmp_path):
 
 SWEEP_KERNEL = {"stem": ("conv_stem",), "dw": ("dwconv",),
                 "conv3x3s2": ("conv_igemm", "conv_igemm_sk", "conv_s2"),
-                "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo")}
+                "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res")}
 
 
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
@@ -117,7 +117,7 @@ def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
     (the graph input)."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act, pre_relu=cin > 3)
     kern = _conv_kernel(path, 3)
-    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo")
+    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res")
     _check_f32(path, 3, lo=-1.0)
 
 
@@ -131,11 +131,57 @@ def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
 def test_halo_conv3x3(tmp_path, cin, cout, H, W, batch, s):
     """3x3 stride-1 convs through the LDS-patch kernel vs the oracle and vs the im2col path."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=s, act=pw.ACT_SILU, pre_relu=True)
-    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_SPLITK) == "conv_halo"
+    nr = ia.IVH_FLAG_NO_RESIDENT | ia.IVH_FLAG_NO_SPLITK
+    assert _conv_kernel(path, batch, nr) == "conv_halo"
     assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_HALO | ia.IVH_FLAG_NO_SPLITK) == "conv_igemm"
-    got = _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_SPLITK)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=nr)
     _, _, im2col = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_HALO | ia.IVH_FLAG_NO_SPLITK)
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(im2col[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (64, 64, 40, 40, 8, pw.ACT_SILU),     # BN 64 x CK 64 (the YOLO head / bottleneck class)
+    (64, 64, 40, 40, 64, pw.ACT_SILU),    # two tiles per work-group (persistent loop)
+    (32, 64, 40, 40, 96, pw.ACT_SILU),    # three rounds: odd and even tile counts per work-group
+    (51, 51, 24, 24, 8, pw.ACT_SILU),     # Cin, Cout % 8 != 0: masked patch, padding-channel stores
+    (32, 32, 40, 40, 6, pw.ACT_HSWISH),   # BN 32, 512-pixel tiles, HardSwish
+    (24, 24, 64, 64, 32, pw.ACT_SILU),    # ragged CK 32, BN 32, two rounds
+    (20, 64, 32, 32, 6, pw.ACT_SILU),     # ragged CK 32 with BN 64
+    (24, 40, 33, 35, 6, pw.ACT_SILU),     # ragged Cin and Cout, odd H and W
+    (64, 24, 40, 40, 6, pw.ACT_SILU),     # BN 32 with CK 64
+    (32, 96, 24, 24, 8, pw.ACT_SILU),     # two channel blocks
+])
+def test_res_conv3x3(tmp_path, cin, cout, H, W, batch, act):
+    """3x3 stride-1 convs with 16 < Cin <= 64 through the resident-weight kernel vs the oracle
+    and vs the LDS-patch kernel (input and output channels-last, as inside a model)."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=act, pre_relu=True, post_relu=True)
+    print(f"res conv {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    assert _conv_kernel(path, batch) == "conv_res"
+    nr = ia.IVH_FLAG_NO_RESIDENT | ia.IVH_FLAG_NO_SPLITK
+    assert _conv_kernel(path, batch, nr) in ("conv_halo", "conv_igemm")
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=nr)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def test_res_residual_chain(tmp_path):
+    """Bottleneck chain of 48 channels at batch 24 (3x3 SiLU, 3x3 + residual) and a 3x3
+    without activation + residual: the resident-weight kernel with the fused residual add."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, 48, 40, 40]), pw.UN_RELU)
+        t = pb.conv(x, 48, 3)
+        t = pb.conv(t, 48, 3)
+        y = pb.binary(x, t, 0)
+        u = pb.conv(y, 48, 3, act=pw.ACT_NONE)
+        z = pb.binary(y, u, 0)
+        return pb.unary(z, pw.UN_RELU)
+    path = _small_plan(tmp_path, build)
+    assert _kernels(path, 24).count("conv_res") == 3
+    got = _check_f32(path, 24, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, 24, lo=-1.0, flags=ia.IVH_FLAG_NO_RESIDENT)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
@@ -162,8 +208,9 @@ def test_halo_residual_chain(tmp_path):
         t = pb.conv(t, 32, 3)
         return pb.binary(x, t, 0)
     path = _small_plan(tmp_path, build)
-    assert _kernels(path, 2, ia.IVH_FLAG_NO_SPLITK).count("conv_halo") == 2
-    _check_f32(path, 2, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
+    nr = ia.IVH_FLAG_NO_RESIDENT | ia.IVH_FLAG_NO_SPLITK
+    assert _kernels(path, 2, nr).count("conv_halo") == 2
+    _check_f32(path, 2, lo=-1.0, flags=nr)
 
 
 @pytest.mark.parametrize("cin,cout,hw,k,s,batch", [

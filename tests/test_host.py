@@ -54,7 +54,8 @@ def test_dry_run_plans_and_bounds(plans, name):
 def test_kernel_choice_yolov8(plans):
     """Planner choices at batch 64: the stem kernel for the Cin = 3 conv, the stride-2
     LDS-patch kernel for the 16->32 downsample, the implicit GEMM for the 32->64 one, the
-    stride-1 LDS-patch kernel for the stride-1 3x3 convs."""
+    resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
+    Cin <= 32 ones with a fused residual) and the stride-1 LDS-patch kernel for the rest."""
     m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
@@ -62,18 +63,21 @@ def test_kernel_choice_yolov8(plans):
     assert by["conv3x3 3x640x640->16x320x320 k3 s2 g1 act1"] == "conv_stem"
     assert by["conv3x3 16x320x320->32x160x160 k3 s2 g1 act1"] == "conv_s2"
     assert by["conv3x3 32x160x160->64x80x80 k3 s2 g1 act1"] == "conv_igemm"
-    s1 = [i["kernel"] for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
-    assert s1.count("conv_halo") == len(s1)
+    s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), "+res" in i["desc"]) for i in info
+          if i["op"] == "conv3x3" and " s1 " in i["desc"]]
+    want = lambda cin, res: "conv_res" if 16 < cin <= 64 and not (res and cin <= 32) else "conv_halo"
+    assert s1 and all(k == want(cin, res) for k, cin, res in s1)
+    assert sum(k == "conv_res" for k, _, _ in s1) >= 20
     m.close()
 
 
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
 def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     """Each conv sweep layer at batch 64, as it runs inside a model, gets its kernel family."""
-    want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2", "conv3x3s2": "conv_igemm", "conv3x3s1": "conv_halo",
-            "dw": "dwconv"}
+    want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2", "conv3x3s2": "conv_igemm",
+            "conv3x3s1_64": "conv_res", "conv3x3s1": "conv_halo", "dw": "dwconv"}
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act,
-                             pre_relu=not name.startswith("stem"))
+                             pre_relu=not name.startswith("stem"), post_relu=True)
     m = ia.PlanModel(path, 0, 64, DRY)
     m.run(64)
     kern = next(m.nodeInfo(i)["kernel"] for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
