@@ -866,7 +866,10 @@ __global__ void __launch_bounds__(256) ew_vec8_kernel(const SmallParams q, int m
   st8(q.y.ptr, py, out);
 }
 
-// nearest resize / max pool, channels-last, one lane = one output pixel x 8 channels
+// nearest resize / max pool, channels-last, one lane = one output pixel x 8 channels.  KP > 0:
+// a KP x KP max pool with the window unrolled, so every tap's 16-byte load is issued before
+// the first maximum (out-of-image taps are skipped by predication, not by a loop exit).
+template <int KP>
 __global__ void __launch_bounds__(256) pool_vec8_kernel(const SmallParams q, int is_max)
 {
   const int C8 = q.C >> 3;
@@ -884,16 +887,21 @@ __global__ void __launch_bounds__(256) pool_vec8_kernel(const SmallParams q, int
     float m[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) m[e] = -3.4e38f;
-    for (int kh = 0; kh < q.K; ++kh) {
-      const int yy = oh * q.S - q.P + kh;
-      if ((unsigned)yy >= (unsigned)q.H) continue;
-      for (int kw = 0; kw < q.K; ++kw) {
-        const int xx = ow * q.S - q.P + kw;
-        if ((unsigned)xx >= (unsigned)q.W) continue;
+    auto tap = [&](int yy, int xx) {
+      if ((unsigned)yy < (unsigned)q.H && (unsigned)xx < (unsigned)q.W) {
         const h8 v = ld8(q.a.ptr, abase + (long)(yy * q.W + xx) * q.a.cs);
 #pragma unroll
         for (int e = 0; e < 8; ++e) m[e] = fmaxf(m[e], (float)v[e]);
       }
+    };
+    if (KP > 0) {
+#pragma unroll
+      for (int kh = 0; kh < KP; ++kh)
+#pragma unroll
+        for (int kw = 0; kw < KP; ++kw) tap(oh * q.S - q.P + kh, ow * q.S - q.P + kw);
+    } else {
+      for (int kh = 0; kh < q.K; ++kh)
+        for (int kw = 0; kw < q.K; ++kw) tap(oh * q.S - q.P + kh, ow * q.S - q.P + kw);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[e] = (_Float16)m[e];
@@ -927,6 +935,9 @@ __global__ void __launch_bounds__(256) rows_vec8_kernel(const SmallParams q, int
 }
 
 // ew_binary_bcast with 8 consecutive outputs per lane (output innermost extent % 8 == 0).
+// Coordinates by float-reciprocal divisions (outputs per image < 2^22); an operand whose
+// innermost stride is 1 (and 8-aligned start) is read as one 16-byte vector, a stride-0 one
+// as one scalar, anything else element by element.
 __global__ void __launch_bounds__(256) ew_bcast8_kernel(const SmallParams q)
 {
   const int t = blockIdx.x * 256 + threadIdx.x;
@@ -936,17 +947,33 @@ __global__ void __launch_bounds__(256) ew_bcast8_kernel(const SmallParams q)
   int rem = t * 8, ai = 0, bi = 0;
   for (int r = q.rank - 1; r >= 0; --r) {
     const int od = q.dims[r];
-    const int coord = rem % od;
-    rem /= od;
+    const int qt = idiv_small(rem, od, __builtin_amdgcn_rcpf((float)od));
+    const int coord = rem - qt * od;
+    rem = qt;
     ai += coord * q.dims[q.rank + r];
     bi += coord * q.dims[2 * q.rank + r];
   }
   const int sa = q.dims[2 * q.rank - 1], sb = q.dims[3 * q.rank - 1];
   const _Float16 * ap = reinterpret_cast<const _Float16 *>(q.a.ptr) + (long)b * q.a.img;
   const _Float16 * bp = reinterpret_cast<const _Float16 *>(q.b.ptr) + (long)b * q.b.img;
+  auto load8 = [](const _Float16 * base, int i0, int st) {
+    h8 v;
+    if (st == 1 && ((i0 | (int)(reinterpret_cast<uintptr_t>(base) >> 1)) & 7) == 0) {
+      v = *reinterpret_cast<const h8 *>(base + i0);
+    } else if (st == 0) {
+      const _Float16 x = base[i0];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = x;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = base[i0 + e * st];
+    }
+    return v;
+  };
+  const h8 av = load8(ap, ai, sa), bv = load8(bp, bi, sb);
   h8 out;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = (_Float16)binop((float)ap[ai + e * sa], (float)bp[bi + e * sb], q.op);
+  for (int e = 0; e < 8; ++e) out[e] = (_Float16)binop((float)av[e], (float)bv[e], q.op);
   st8(q.y.ptr, (long)b * q.y.img + (long)t * 8, out);
 }
 
@@ -1081,8 +1108,13 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
   case kMaxPool:
   case kResizeNN:
     if (!nhwc8(q, {&q.a, &q.y})) return false;
-    hipLaunchKernelGGL(pool_vec8_kernel, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q,
-                       kind == kMaxPool ? 1 : 0);
+    if (kind == kMaxPool && q.K == 5)
+      hipLaunchKernelGGL(pool_vec8_kernel<5>, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q, 1);
+    else if (kind == kMaxPool && q.K == 3)
+      hipLaunchKernelGGL(pool_vec8_kernel<3>, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q, 1);
+    else
+      hipLaunchKernelGGL(pool_vec8_kernel<0>, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q,
+                         kind == kMaxPool ? 1 : 0);
     return true;
   case kSliceAxis:
   case kConcatOuter:
@@ -1098,7 +1130,7 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
     return true;
   }
   case kEwBcast:
-    if (q.n % 8 || q.dims[q.rank - 1] % 8 || !al8(q.y)) return false;
+    if (q.n % 8 || q.dims[q.rank - 1] % 8 || !al8(q.y) || q.n >= (1L << 22)) return false;
     hipLaunchKernelGGL(ew_bcast8_kernel, dim3(nblk(q.n / 8, 256), B), blk, 0, s, q);
     return true;
   case kSoftmax:

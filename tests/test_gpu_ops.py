@@ -264,6 +264,13 @@ SMALL = {
     "concat_axis2": lambda pb: pb.concat([pb.reshape(pb.input("x", [1, 6, 4, 5]), [1, 6, 20]),
                                           pb.const(np.arange(60).reshape(1, 6, 10) / 7.0, "k")], axis=2),
     "ew_add_bcast": lambda pb: pb.binary(pb.input("x", [1, 17, 2, 30]), pb.const(np.linspace(-1, 1, 60).reshape(2, 30), "k"), 0),
+    # 8-wide broadcast kernel: vector loads of both operands, a scalar operand, a row operand
+    "ew_add_bcast8": lambda pb: pb.binary(pb.input("x", [1, 17, 2, 32]), pb.const(np.linspace(-1, 1, 64).reshape(2, 32), "k"), 0),
+    "ew_mul_scalar8": lambda pb: pb.binary(pb.input("x", [1, 17, 2, 40]), pb.const(np.array([2.0]), "k"), 2),
+    "ew_mul_row8": lambda pb: pb.binary(pb.input("x", [1, 17, 2, 40]), pb.const(np.linspace(1, 3, 40).reshape(1, 40), "k"), 2),
+    # channels-last pools (between two ReLUs both tensors are internal)
+    "maxpool5_nhwc": lambda pb: pb.unary(pb.maxpool(pb.unary(pb.input("x", [1, 24, 13, 17]), 2), 5, 1, 2), 2),
+    "maxpool3s2_nhwc": lambda pb: pb.unary(pb.maxpool(pb.unary(pb.input("x", [1, 16, 15, 15]), 2), 3, 2, 1), 2),
     "ew_mul_stride": lambda pb: pb.binary(pb.input("x", [1, 4, 30]), pb.const(np.linspace(1, 3, 30).reshape(1, 30), "k"), 2),
     "ew_div_scalar": lambda pb: pb.binary(pb.input("x", [1, 3, 9, 9]), pb.const(np.array([2.0]), "k"), 3),
     "ew_sub_same": lambda pb: pb.binary(pb.const(np.linspace(0, 5, 2 * 33).reshape(1, 2, 33), "k"), pb.input("x", [1, 2, 33]), 1),
@@ -275,7 +282,7 @@ SMALL = {
 }
 
 
-EXACT = {"maxpool5", "maxpool3s2", "resize2", "permute0213", "permute0132", "slice_axis2",
+EXACT = {"maxpool5", "maxpool3s2", "maxpool5_nhwc", "maxpool3s2_nhwc", "resize2", "permute0213", "permute0132", "slice_axis2",
          "concat_ch", "concat_axis2"}
 
 
