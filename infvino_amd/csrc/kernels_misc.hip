@@ -909,6 +909,53 @@ __global__ void __launch_bounds__(256) pool_vec8_kernel(const SmallParams q, int
   st8(q.y.ptr, (long)b * q.y.img + (long)p * q.y.cs + c, out);
 }
 
+// KP x KP stride-1 max pool, channels-last (SPPF's 5x5): one lane = RO consecutive output
+// rows of one column x 8 channels.  The horizontal maximum of each of the RO + KP - 1 input
+// rows is taken once (KP loads) and reused by the KP output rows whose window holds it, so an
+// output costs (RO + KP - 1) * KP / RO loads instead of KP * KP; every load is issued before
+// the first maximum (the window is unrolled, out-of-image taps are predicated off).
+template <int KP, int RO>
+__global__ void __launch_bounds__(256) maxpool_s1_cols_kernel(const SmallParams q)
+{
+  const int C8 = q.C >> 3, nrb = (q.Ho + RO - 1) / RO;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (i >= q.Wo * C8 * nrb) return;
+  const int cc = i / C8, c = (i - cc * C8) * 8;  // (row block, column) fastest after channels
+  const int rb = cc / q.Wo, ox = cc - rb * q.Wo;
+  const int oy0 = rb * RO;
+  const long abase = (long)b * q.a.img + c;
+  float hm[RO + KP - 1][8];
+#pragma unroll
+  for (int r = 0; r < RO + KP - 1; ++r) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hm[r][e] = -3.4e38f;
+    const int yy = oy0 - q.P + r;
+#pragma unroll
+    for (int kw = 0; kw < KP; ++kw) {
+      const int xx = ox - q.P + kw;
+      if ((unsigned)yy < (unsigned)q.H && (unsigned)xx < (unsigned)q.W) {
+        const h8 v = ld8(q.a.ptr, abase + (long)(yy * q.W + xx) * q.a.cs);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hm[r][e] = fmaxf(hm[r][e], (float)v[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 0; o < RO; ++o) {
+    if (oy0 + o >= q.Ho) break;
+    h8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float m = hm[o][e];
+#pragma unroll
+      for (int k = 1; k < KP; ++k) m = fmaxf(m, hm[o + k][e]);
+      out[e] = (_Float16)m;
+    }
+    st8(q.y.ptr, (long)b * q.y.img + (long)((oy0 + o) * q.Wo + ox) * q.y.cs + c, out);
+  }
+}
+
 // Row copies of `L` contiguous elements (L % 8 == 0): slice_axis, concat along an inner
 // axis, permute mode 0.  kind 0 slice, 1 concat part, 2 permute.
 __global__ void __launch_bounds__(256) rows_vec8_kernel(const SmallParams q, int kind, int L, int rows)
@@ -1108,7 +1155,11 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
   case kMaxPool:
   case kResizeNN:
     if (!nhwc8(q, {&q.a, &q.y})) return false;
-    if (kind == kMaxPool && q.K == 5)
+    if (kind == kMaxPool && q.K == 5 && q.S == 1 && q.Ho == q.H && q.Wo == q.W) {
+      constexpr int RO = 4;
+      hipLaunchKernelGGL((maxpool_s1_cols_kernel<5, RO>), dim3(nblk((long)((q.Ho + RO - 1) / RO) * q.Wo * (q.C / 8), 256), B),
+                         blk, 0, s, q);
+    } else if (kind == kMaxPool && q.K == 5)
       hipLaunchKernelGGL(pool_vec8_kernel<5>, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q, 1);
     else if (kind == kMaxPool && q.K == 3)
       hipLaunchKernelGGL(pool_vec8_kernel<3>, dim3(nblk((long)q.Ho * q.Wo * (q.C / 8), 256), B), blk, 0, s, q, 1);
