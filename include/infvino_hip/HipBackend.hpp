@@ -6,12 +6,15 @@
 //     reference's truncating f32 -> f16 conversion (done on the device), fp16 compute,
 //     f32 Tensors out; numel must equal prod(inputDims()) (throws "input numel mismatch"
 //     otherwise), or a multiple B <= maxBatch of it, in which case the outputs carry B
-//     images along dim 0;
+//     images along dim 0 (image(outputs, b, B) slices image b back out for per-image
+//     decoders);
 //   * infer serialised by a mutex so Sessions can share one backend (ClBackend.cpp:33).
 #ifndef INFVINO_HIP_BACKEND_HPP_
 #define INFVINO_HIP_BACKEND_HPP_
 
 #include <chrono>
+#include <cstddef>
+#include <stdexcept>
 #include <cstdlib>
 #include <memory>
 #include <mutex>
@@ -91,6 +94,28 @@ public:
       outputs.push_back(std::move(t));
     }
     return outputs;
+  }
+
+  /** Image b of outputs that infer() returned for a batch: every tensor's dim 0 back to one
+   *  image, so per-image consumers (the reference's PoseDecoder / nms, which read a
+   *  [1, C, N] tensor) run unchanged on each image of a batched inference. */
+  static std::vector<Tensor> image(const std::vector<Tensor> & batched, int b, int batch)
+  {
+    if (batch < 1 || b < 0 || b >= batch) throw std::runtime_error("HipBackend: image index out of range");
+    std::vector<Tensor> out;
+    out.reserve(batched.size());
+    for (const Tensor & t : batched) {
+      if (t.shape.empty() || t.shape[0] % batch != 0 || t.data.size() % static_cast<size_t>(batch) != 0)
+        throw std::runtime_error("HipBackend: tensor does not hold the batch");
+      const size_t per = t.data.size() / static_cast<size_t>(batch);
+      Tensor u;
+      u.shape = t.shape;
+      u.shape[0] /= batch;
+      u.data.assign(t.data.begin() + static_cast<std::ptrdiff_t>(per * b),
+                    t.data.begin() + static_cast<std::ptrdiff_t>(per * (b + 1)));
+      out.push_back(std::move(u));
+    }
+    return out;
   }
 
 private:

@@ -287,6 +287,23 @@ class HipBackend:
     def lastInferMs(self) -> float:
         return self._last
 
+    @staticmethod
+    def image(batched, b: int, batch: int):
+        """Image b of a B-image infer() result, each tensor with dim 0 divided by B, so
+        per-image consumers (the reference's PoseDecoder / nms read a [1, C, N] tensor)
+        run unchanged on each image of a batched inference."""
+        if batch < 1 or b < 0 or b >= batch:
+            raise RuntimeError("HipBackend: image index out of range")
+        out = []
+        for t in batched:
+            flat = np.asarray(t.data).ravel()
+            if not t.shape or flat.size % batch or t.shape[0] % batch:
+                raise RuntimeError("HipBackend: tensor does not hold the batch")
+            per = flat.size // batch
+            shape = [t.shape[0] // batch] + list(t.shape[1:])
+            out.append(Tensor(shape, flat[per * b:per * (b + 1)].reshape(shape)))
+        return out
+
     def infer(self, input_f32, numel: int | None = None):
         x = np.ascontiguousarray(input_f32, dtype=np.float32).ravel()
         numel = x.size if numel is None else numel

@@ -165,6 +165,39 @@ def test_rel_errors_definition():
     assert np.isclose(max_abs, 0.04) and np.isclose(scale_rel, 0.0125 / 4)
 
 
+def test_cpp_backend_image_slicing(tmp_path):
+    """HipBackend::image: outputs of a batched inference sliced back to one image each (the
+    per-image view the reference's decoders take), host code only."""
+    import subprocess
+    src = tmp_path / "t.cpp"
+    src.write_text(r"""
+#include "infvino_hip/HipBackend.hpp"
+#include <cstdio>
+using infvino_hip::HipBackend; using infvino_hip::Tensor;
+int main() {
+  Tensor a({3, 2, 4}, {}), c({3, 5}, {});
+  for (int i = 0; i < 24; ++i) a.data.push_back((float)i);
+  for (int i = 0; i < 15; ++i) c.data.push_back(100.0f + i);
+  for (int b = 0; b < 3; ++b) {
+    auto im = HipBackend::image({a, c}, b, 3);
+    if (im.size() != 2 || im[0].shape != std::vector<int64_t>{1, 2, 4} || im[1].shape != std::vector<int64_t>{1, 5}) return 1;
+    for (int i = 0; i < 8; ++i) if (im[0].data[i] != (float)(8 * b + i)) return 2;
+    for (int i = 0; i < 5; ++i) if (im[1].data[i] != 100.0f + 5 * b + i) return 3;
+  }
+  try { HipBackend::image({a}, 3, 3); return 4; } catch (const std::runtime_error &) {}
+  try { HipBackend::image({c}, 0, 2); return 5; } catch (const std::runtime_error &) {}
+  std::puts("ok");
+  return 0;
+}
+""")
+    exe = tmp_path / "t"
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout)
+
+
 def test_cpp_headers_compile(tmp_path):
     """include/infvino_hip/*.hpp compile as a C++17 translation unit against include/ivh.h."""
     import subprocess
@@ -176,3 +209,19 @@ def test_cpp_headers_compile(tmp_path):
     r = subprocess.run(["g++", "-std=c++17", "-Wall", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_py_backend_image_slicing():
+    """HipBackend.image (Python mirror): same slicing and errors as the C++ helper."""
+    from infvino_amd import HipBackend, Tensor
+    a = Tensor([3, 2, 4], np.arange(24, dtype=np.float32).reshape(3, 2, 4))
+    c = Tensor([3, 5], 100 + np.arange(15, dtype=np.float32).reshape(3, 5))
+    for b in range(3):
+        ia, ic = HipBackend.image([a, c], b, 3)
+        assert ia.shape == [1, 2, 4] and ic.shape == [1, 5]
+        np.testing.assert_array_equal(ia.data.ravel(), np.arange(8 * b, 8 * b + 8))
+        np.testing.assert_array_equal(ic.data.ravel(), 100 + np.arange(5 * b, 5 * b + 5))
+    with pytest.raises(RuntimeError):
+        HipBackend.image([a], 3, 3)
+    with pytest.raises(RuntimeError):
+        HipBackend.image([c], 0, 2)
