@@ -55,6 +55,9 @@ extern "C" {
 #define IVH_FLAG_NO_HALO 0x100u   /* 3x3 convs use the im2col path, never the LDS halo tile */
 #define IVH_FLAG_NO_RESIDENT 0x200u /* 3x3 stride-1 convs never keep their weights resident in
                                        LDS (the halo tile or im2col path instead) */
+#define IVH_FLAG_NO_FUSE_DECODE 0x400u /* keep a Detect / Pose head's decode tail (DFL,
+                                          dist2bbox, keypoint decode) node by node instead of
+                                          one fused kernel */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 

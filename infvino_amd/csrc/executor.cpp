@@ -22,6 +22,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <functional>
 #include <numeric>
 #include <set>
 #include <sstream>
@@ -149,6 +150,7 @@ Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t 
   plan_dir_ = pos == std::string::npos ? std::string(".") : plan_path.substr(0, pos);
   parse(plan_path);
   if (!(flags_ & IVH_FLAG_NO_FUSE)) {
+    fuseDecode();
     fuseResidual();
     fuseActivation();
     fusePermuteMatmul();
@@ -380,6 +382,280 @@ void Model::fusePermuteMatmul()
   nodes_ = std::move(kept);
 }
 
+// ============================================================= decode-tail fusion
+
+// The export form of a Detect / Pose head's decode (ultralytics head.py Detect._inference,
+// Pose.kpts_decode) as a plan holds it:
+//   box+cls per scale [4R + nc, H, W] -> reshape, concat over anchors -> copy_c box rows ->
+//   reshape [4, R, A] -> permute_0213 -> softmax over the R bins -> conv1x1 with the bin
+//   weights (DFL) -> copy_c lt / rb -> anchors - lt, anchors + rb -> centre = sum / 2 (or
+//   * 0.5), size = x2y2 - x1y1 -> concat -> * strides;  copy_c class rows -> sigmoid;
+//   keypoints per scale [3 nk, H, W] -> concat over anchors -> slice xy -> * 2 + (anchors -
+//   0.5) -> * strides; slice visibility -> sigmoid -> concat [nk, 3, A];
+//   output = concat [box (4), classes (nc), keypoints (3 nk)] over A anchors.
+// About 35 nodes, each streaming the anchors through memory, become one "pose_decode" node
+// whose kernel reads each head pixel once and writes the output once, rounding to fp16
+// after every step where a node would have stored its result.  The match runs from each
+// graph output backwards and checks every node's op, attributes, operand order and
+// broadcast index map; a tail of any other shape is left node by node.
+void Model::fuseDecode()
+{
+  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_DECODE)) return;
+  std::map<std::string, int> producer;
+  std::map<std::string, std::vector<int>> users;
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    for (const auto & o : nodes_[i].outs)
+      if (o != "-") producer[o] = (int)i;
+    for (const auto & in : nodes_[i].ins)
+      if (in != "-") users[in].push_back((int)i);
+  }
+  const std::set<std::string> gouts(outputs_.begin(), outputs_.end());
+
+  struct Match {
+    std::set<int> region;
+    std::vector<std::string> X, K;  // per-scale head tensors
+    std::vector<int> hw;            // pixels per scale
+    std::string wd, anc, st, ancm, cbox, ckpt;
+    int R = 0, nc = 0, nk = 0, box_div = 1;
+  };
+  for (const std::string & out : outputs_) {
+    Match m;
+    long A = 0;
+    const auto id = [](long i) { return i; };
+    const auto zero = [](long) { return 0L; };
+    auto peek = [&](const std::string & t) -> const PlanNode * {
+      auto it = producer.find(t);
+      return it == producer.end() ? nullptr : &nodes_[it->second];
+    };
+    // producer of t if it is a single-output `op` node (added to the region)
+    auto take = [&](const std::string & t, const char * op) -> const PlanNode * {
+      auto it = producer.find(t);
+      if (it == producer.end()) return nullptr;
+      const PlanNode & n = nodes_[it->second];
+      if (n.op != op || n.outs.size() != 1 || n.ins.empty()) return nullptr;
+      m.region.insert(it->second);
+      return &n;
+    };
+    auto unreshape = [&](std::string t) {
+      for (;;) {
+        auto it = producer.find(t);
+        if (it == producer.end()) return t;
+        const PlanNode & n = nodes_[it->second];
+        if ((n.op != "reshape" && n.op != "flatten") || n.ins.empty()) return t;
+        m.region.insert(it->second);
+        t = n.ins[0];
+      }
+    };
+    auto init_n = [&](const std::string & t, long n) {
+      auto it = T_.find(t);
+      return it != T_.end() && it->second->kind == Tensor::kInit && it->second->numel == n;
+    };
+    auto act_n = [&](const std::string & t, long n) {
+      auto it = T_.find(t);
+      return it != T_.end() && it->second->kind == Tensor::kAct && it->second->numel == n;
+    };
+    // an ew_binary `op` over n outputs whose operand indices are fa(i) and fb(i), by the
+    // ops.cl rules (b_scalar reads b[0]; bdims = out dims, a strides, b strides)
+    auto ew = [&](const PlanNode * e, int op, long n, const std::function<long(long)> & fa,
+                  const std::function<long(long)> & fb) -> bool {
+      if (!e || e->op != "ew_binary" || e->i("op") != op || e->ins.size() < 2 || !act_n(e->outs[0], n)) return false;
+      const bool scalar = e->i("b_scalar") == 1;
+      std::vector<long> d;
+      if (e->has("bdims") && !scalar)
+        for (const auto & v : split_csv(e->str("bdims"))) d.push_back(std::stol(v));
+      if (d.size() % 3) return false;
+      const int rank = (int)d.size() / 3;
+      long tot = 1;
+      for (int r = 0; r < rank; ++r) tot *= d[r];
+      if (rank && tot != n) return false;
+      const long na = T_.at(e->ins[0])->numel, nb = T_.at(e->ins[1])->numel;
+      for (long i = 0; i < n; ++i) {
+        long ai = i, bi = scalar ? 0 : i;
+        if (rank) {
+          long rem = i;
+          ai = bi = 0;
+          for (int r = rank - 1; r >= 0; --r) {
+            const long c = rem % d[r];
+            rem /= d[r];
+            ai += c * d[rank + r];
+            bi += c * d[2 * rank + r];
+          }
+        }
+        if (ai != fa(i) || bi != fb(i) || ai >= na || bi >= nb) return false;
+      }
+      return true;
+    };
+    auto sigmoid_of = [&](const std::string & t) -> const PlanNode * {
+      const PlanNode * u = take(t, "ew_unary");
+      return (u && unary_to_act(u->i("op")) == kActSigmoid) ? u : nullptr;
+    };
+    auto concat2 = [&](const PlanNode * c, int outer, long inner, int ca, int cb) {
+      return c && c->ins.size() >= 2 && c->i("outer", 1) == outer && c->i("inner", 1) == inner && c->i("ca") == ca &&
+             c->i("cb") == cb && c->i("cc") == 0 && c->i("cd") == 0;
+    };
+    auto copy_rows = [&](const PlanNode * c, int c0, int cnt) {
+      return c && c->i("HW", 1) == A && c->i("c0") == c0 && c->i("cnt") == cnt && c->i("dst_off") == 0;
+    };
+    // concat over anchors of per-scale [C, H_s, W_s] head tensors (through their reshapes)
+    auto scales = [&](const std::string & t, int C, std::vector<std::string> & xs) -> bool {
+      const PlanNode * c = take(t, "concat4");
+      if (!c || c->i("outer", 1) != C || c->i("inner", 1) != 1 || c->ins.size() < 4) return false;
+      const int cnt[4] = {c->i("ca"), c->i("cb"), c->i("cc"), c->i("cd")};
+      std::vector<int> hw;
+      long tot = 0;
+      for (int j = 0; j < 4; ++j) {
+        if (cnt[j] <= 0) {
+          if (cnt[j] < 0 || (j + 1 < 4 && cnt[j + 1] > 0)) return false;
+          continue;
+        }
+        const std::string s = unreshape(c->ins[j]);
+        const Tensor & st = *T_.at(s);
+        if (st.kind != Tensor::kAct || st.dims.size() != 4 || st.C != C || (long)st.H * st.W != cnt[j]) return false;
+        xs.push_back(s);
+        hw.push_back(cnt[j]);
+        tot += cnt[j];
+      }
+      if (tot != A || xs.empty()) return false;
+      if (m.hw.empty()) m.hw = hw;
+      return m.hw == hw;
+    };
+    // concat [dbox * strides (4), sigmoid(classes) (nc)] over A anchors
+    auto box = [&](const PlanNode * x) -> bool {
+      if (!x || x->ins.size() < 2 || x->i("ca") != 4 || x->i("cb") < 1 || !concat2(x, 1, A, 4, x->i("cb"))) return false;
+      m.nc = x->i("cb");
+      const PlanNode * bx = take(x->ins[0], "ew_binary");
+      if (!bx || !init_n(bx->ins.at(1), A) || !ew(bx, 2, 4 * A, id, [A](long i) { return i % A; })) return false;
+      m.st = bx->ins[1];
+      const PlanNode * db = take(bx->ins[0], "concat4");
+      if (!concat2(db, 1, A, 2, 2)) return false;
+      const PlanNode * cxy = take(db->ins[0], "ew_binary");
+      if (!cxy || cxy->ins.size() < 2 || !init_n(cxy->ins[1], 1)) return false;
+      m.box_div = cxy->i("op") == 3;
+      if (!ew(cxy, m.box_div ? 3 : 2, 2 * A, id, zero)) return false;
+      m.cbox = cxy->ins[1];
+      const PlanNode * sum = take(cxy->ins[0], "ew_binary");
+      const PlanNode * wh = take(db->ins[1], "ew_binary");
+      if (!ew(sum, 0, 2 * A, id, id) || !ew(wh, 1, 2 * A, id, id)) return false;
+      const std::string x2y2 = wh->ins[0], x1y1 = wh->ins[1];
+      if (!((sum->ins[0] == x1y1 && sum->ins[1] == x2y2) || (sum->ins[0] == x2y2 && sum->ins[1] == x1y1))) return false;
+      const PlanNode * n1 = take(x1y1, "ew_binary");  // anchors - lt
+      const PlanNode * n2 = take(x2y2, "ew_binary");  // anchors + rb (either order)
+      if (!ew(n1, 1, 2 * A, id, id) || !ew(n2, 0, 2 * A, id, id) || !init_n(n1->ins[0], 2 * A)) return false;
+      m.anc = n1->ins[0];
+      const std::string rbt = n2->ins[0] == m.anc ? n2->ins[1] : (n2->ins[1] == m.anc ? n2->ins[0] : std::string());
+      if (rbt.empty() || rbt == m.anc) return false;
+      const PlanNode * lt = take(n1->ins[1], "copy_c");
+      const PlanNode * rb = take(rbt, "copy_c");
+      if (!copy_rows(lt, 0, 2) || !copy_rows(rb, 2, 2) || lt->ins[0] != rb->ins[0] || !act_n(lt->ins[0], 4 * A)) return false;
+      const PlanNode * cv = take(unreshape(lt->ins[0]), "conv1x1");
+      if (!cv || cv->ins.size() < 2 || cv->i("act") != 0) return false;
+      if ((cv->ins.size() > 2 && cv->ins[2] != "-") || (cv->ins.size() > 3 && cv->ins[3] != "-")) return false;
+      const Tensor & wt = *T_.at(cv->ins[0]);
+      if (wt.kind != Tensor::kInit || wt.dims.empty() || wt.dims[0] != 1 || wt.numel < 1 || wt.numel > 64) return false;
+      m.R = (int)wt.numel;
+      m.wd = cv->ins[0];
+      if (!act_n(cv->outs[0], 4 * A) || !act_n(cv->ins[1], 4 * A * m.R)) return false;
+      const PlanNode * sm = take(cv->ins[1], "softmax_axis");
+      if (!sm || sm->i("outer", 1) != 1 || sm->i("axdim") != m.R || sm->i("inner", 1) != 4 * A) return false;
+      const PlanNode * pm = take(sm->ins[0], "permute_0213");
+      if (!pm || pm->i("mode") != 0 || pm->i("D1", 1) != 4 || pm->i("D2", 1) != m.R || pm->i("I", 1) != A) return false;
+      const PlanNode * bsl = take(unreshape(pm->ins[0]), "copy_c");
+      if (!copy_rows(bsl, 0, 4 * m.R)) return false;
+      const PlanNode * sg = sigmoid_of(x->ins[1]);
+      const PlanNode * csl = sg ? take(sg->ins[0], "copy_c") : nullptr;
+      if (!copy_rows(csl, 4 * m.R, m.nc) || csl->ins[0] != bsl->ins[0]) return false;
+      if (!act_n(x->ins[1], (long)m.nc * A) || !act_n(sg->ins[0], (long)m.nc * A)) return false;
+      return scales(bsl->ins[0], 4 * m.R + m.nc, m.X);
+    };
+    // [nk, 3, A] = concat [(xy * 2 + (anchors - 0.5)) * strides, sigmoid(visibility)]
+    auto keypoints = [&](const std::string & t) -> bool {
+      const PlanNode * kc = take(unreshape(t), "concat4");
+      if (!kc) return false;
+      m.nk = kc->i("outer", 1);
+      if (m.nk < 1 || !concat2(kc, m.nk, A, 2, 1)) return false;
+      const long nxy = 2L * m.nk * A;
+      const PlanNode * k3 = take(kc->ins[0], "ew_binary");
+      if (!k3 || k3->ins.size() < 2 || k3->ins[1] != m.st || !ew(k3, 2, nxy, id, [A](long i) { return i % A; }))
+        return false;
+      const PlanNode * k2 = take(k3->ins[0], "ew_binary");
+      if (!k2 || k2->ins.size() < 2 || !init_n(k2->ins[1], 2 * A) || !ew(k2, 0, nxy, id, [A](long i) { return i % (2 * A); }))
+        return false;
+      m.ancm = k2->ins[1];
+      const PlanNode * k1 = take(k2->ins[0], "ew_binary");
+      if (!k1 || k1->ins.size() < 2 || !init_n(k1->ins[1], 1) || !ew(k1, 2, nxy, id, zero)) return false;
+      m.ckpt = k1->ins[1];
+      const PlanNode * sxy = take(k1->ins[0], "slice_axis");
+      const PlanNode * vs = sigmoid_of(kc->ins[1]);
+      const PlanNode * sv = vs ? take(vs->ins[0], "slice_axis") : nullptr;
+      auto sl = [&](const PlanNode * s, int s0, int len) {
+        return s && s->i("outer", 1) == m.nk && s->i("axdim") == 3 && s->i("inner", 1) == A && s->i("start") == s0 &&
+               s->i("len") == len;
+      };
+      if (!sl(sxy, 0, 2) || !sl(sv, 2, 1) || sv->ins[0] != sxy->ins[0]) return false;
+      if (!act_n(kc->ins[1], (long)m.nk * A) || !act_n(vs->ins[0], (long)m.nk * A) || !act_n(sxy->outs[0], nxy)) return false;
+      return scales(unreshape(sxy->ins[0]), 3 * m.nk, m.K);
+    };
+
+    bool ok = false;
+    try {
+      const PlanNode * fin = take(out, "concat4");
+      if (fin && fin->i("outer", 1) == 1 && fin->ins.size() >= 2) {
+        A = fin->i("inner", 1);
+        const PlanNode * first = peek(fin->ins[0]);
+        if (A > 0 && first && first->op == "concat4") {  // pose: [box + classes, keypoints]
+          ok = box(take(fin->ins[0], "concat4")) && keypoints(fin->ins[1]) &&
+               concat2(fin, 1, A, 4 + m.nc, 3 * m.nk) && act_n(fin->ins[1], 3L * m.nk * A);
+        } else if (A > 0) {                               // detect: box + classes only
+          ok = box(fin);
+        }
+      }
+    } catch (const std::exception &) {
+      ok = false;
+    }
+    if (!ok || m.X.size() > 4 || m.X.empty() || (m.nk && m.K.size() != m.X.size())) continue;
+    // nothing outside the region may read what the region computes
+    for (int ni : m.region)
+      for (const auto & o : nodes_[ni].outs) {
+        if (o == out || o == "-") continue;
+        if (gouts.count(o)) ok = false;
+        for (int u : users[o])
+          if (!m.region.count(u)) ok = false;
+      }
+    if (!ok) continue;
+
+    PlanNode f;
+    f.op = "pose_decode";
+    f.ins = m.X;
+    if (m.nk) f.ins.insert(f.ins.end(), m.K.begin(), m.K.end());
+    for (const std::string & s : {m.wd, m.anc, m.st, m.nk ? m.ancm : std::string("-"), m.cbox,
+                                  m.nk ? m.ckpt : std::string("-")})
+      f.ins.push_back(s);
+    f.outs = {out};
+    f.attr["S"] = std::to_string(m.X.size());
+    f.attr["R"] = std::to_string(m.R);
+    f.attr["nc"] = std::to_string(m.nc);
+    f.attr["nk"] = std::to_string(m.nk);
+    f.attr["A"] = std::to_string(A);
+    f.attr["box_div"] = std::to_string(m.box_div);
+    for (size_t s = 0; s < m.hw.size(); ++s) f.attr["hw" + std::to_string(s)] = std::to_string(m.hw[s]);
+    const int last = *m.region.rbegin();
+    std::vector<PlanNode> kept;
+    for (size_t i = 0; i < nodes_.size(); ++i) {
+      if ((int)i == last) kept.push_back(f);
+      else if (!m.region.count((int)i)) kept.push_back(std::move(nodes_[i]));
+    }
+    nodes_ = std::move(kept);
+    producer.clear();
+    users.clear();
+    for (size_t i = 0; i < nodes_.size(); ++i) {
+      for (const auto & o : nodes_[i].outs)
+        if (o != "-") producer[o] = (int)i;
+      for (const auto & in : nodes_[i].ins)
+        if (in != "-") users[in].push_back((int)i);
+    }
+  }
+}
+
 // ====================================================================== planning
 
 // ew_binary whose smaller operand is one value per output channel ([.., C, 1, 1]), the
@@ -566,6 +842,7 @@ void Model::chooseLayouts()
     if (op == "maxpool" || op == "resize_nn" || op == "gap" || op == "ew_unary") return true;
     if (op == "copy_c") return n.i("dst_off") == 0;
     if (op == "concat4") return n.i("outer", 1) == 1;
+    if (op == "pose_decode") return slot < (size_t)n.i("S") * (n.i("nk") ? 2 : 1);  // head tensors
     if (op == "ew_binary") {
       const Tensor & y = *T_[n.outs[0]];
       if (!n.has("bdims") || n.i("b_scalar") == 1) return t.numel == y.numel;
@@ -828,6 +1105,64 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
   const Tensor & yt = *T_[n.outs[0]];
   auto has = [&](size_t i) { return i < n.ins.size() && n.ins[i] != "-"; };
   auto fail = [&](const std::string & m) { throw std::runtime_error("node " + n.op + " -> " + yt.name + ": " + m); };
+  if (n.op == "pose_decode") {
+    Launch L;
+    L.kind = Launch::kDecode;
+    DecodeParams & d = L.dp;
+    d.batch = batch;
+    d.nscale = n.i("S");
+    d.R = n.i("R");
+    d.nc = n.i("nc");
+    d.nk = n.i("nk");
+    d.A = n.i("A");
+    d.box_div = n.i("box_div");
+    if (d.nscale < 1 || d.nscale > 4 || d.R < 1 || d.R > 64 || d.nc < 1 || d.nk < 0 || d.A < 1) fail("decode attributes");
+    const int no = 4 * d.R + d.nc, nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
+    const size_t base = (size_t)d.nscale * (d.nk ? 2 : 1);
+    if (n.ins.size() != base + 6) fail("decode inputs");
+    // 16-byte pixel rows: channels-last, aligned, and the rounded-up channel count inside
+    // the pixel pitch
+    auto vec_ok = [&](const Tensor & t, const View & v, int C) {
+      return t.kind == Tensor::kAct && v.layout == kNHWC && v.cs % 8 == 0 && v.img % 8 == 0 && t.coff % 8 == 0 &&
+             t.coff + round_up(C, 8) <= v.cs && (reinterpret_cast<uintptr_t>(v.ptr) & 15) == 0;
+    };
+    long off = 0;
+    d.vec = 1;
+    for (int s = 0; s < d.nscale; ++s) {
+      const long hw = n.i(("hw" + std::to_string(s)).c_str());
+      d.off[s] = (int)off;
+      const Tensor & xt = *T_.at(n.ins[s]);
+      if (xt.C != no || (long)xt.H * xt.W != hw || xt.numel != no * hw) fail("decode head geometry");
+      d.x[s] = view(xt.name, batch);
+      if (!vec_ok(xt, d.x[s], no)) d.vec = 0;
+      if (d.nk) {
+        const Tensor & kt = *T_.at(n.ins[d.nscale + s]);
+        if (kt.C != nkc || (long)kt.H * kt.W != hw || kt.numel != nkc * hw) fail("decode keypoint geometry");
+        d.k[s] = view(kt.name, batch);
+        if (!vec_ok(kt, d.k[s], nkc)) d.vec = 0;
+      }
+      off += hw;
+    }
+    if (off != d.A || yt.numel != (long)ny * d.A) fail("decode anchor count");
+    auto konst = [&](size_t i, long numel) -> const __half * {
+      const Tensor & t = *T_.at(n.ins.at(i));
+      if (t.kind != Tensor::kInit || t.numel != numel) fail("decode constant " + t.name);
+      return static_cast<const __half *>(init_dev_.at(t.name));
+    };
+    d.dflw = konst(base, d.R);
+    d.anc = konst(base + 1, 2L * d.A);
+    d.st = konst(base + 2, d.A);
+    d.cbox = konst(base + 4, 1);
+    if (d.nk) {
+      d.ancm = konst(base + 3, 2L * d.A);
+      d.ckpt = konst(base + 5, 1);
+    }
+    d.y = view(yt.name, batch);
+    if (d.y.layout != kNCHW) fail("decode output must be NCHW");
+    d.y.cs = d.A;
+    out.push_back(L);
+    return;
+  }
   const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
   if (is1 || is3 || isg) {
     const Packed & pk = packed_[ni];
@@ -1177,6 +1512,29 @@ void Model::validate(const Launch & l) const
     if (C <= 0 || HW <= 0 || B <= 0) return -1;
     return (long)(B - 1) * v.img + (v.layout == kNHWC ? (HW - 1) * v.cs + (C - 1) : (C - 1) * v.cs + (HW - 1));
   };
+  if (l.kind == Launch::kDecode) {
+    const DecodeParams & d = l.dp;
+    if (d.batch < 1 || d.batch > 65535 || d.nscale < 1 || d.nscale > 4) throw std::runtime_error("decode grid");
+    const int no = 4 * d.R + d.nc, nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
+    for (int s = 0; s < d.nscale; ++s) {
+      const long hw = (s + 1 < d.nscale ? d.off[s + 1] : d.A) - d.off[s];
+      if (hw < 1) throw std::runtime_error("decode scale offsets");
+      // the channels-last path reads whole 16-byte pieces of a pixel's channels
+      check(d.x[s].ptr, 0, vlast(d.x[s], d.batch, d.vec ? (no + 7) / 8 * 8 : no, hw), 2, "decode head");
+      if (d.nk) check(d.k[s].ptr, 0, vlast(d.k[s], d.batch, d.vec ? (nkc + 7) / 8 * 8 : nkc, hw), 2, "decode keypoints");
+    }
+    check(d.dflw, 0, d.R - 1, 2, "decode bin weights");
+    check(d.anc, 0, 2L * d.A - 1, 2, "decode anchors");
+    check(d.st, 0, d.A - 1, 2, "decode strides");
+    check(d.cbox, 0, 0, 2, "decode box constant");
+    if (d.nk) {
+      check(d.ancm, 0, 2L * d.A - 1, 2, "decode keypoint anchors");
+      check(d.ckpt, 0, 0, 2, "decode keypoint constant");
+    }
+    if (d.y.layout != kNCHW || d.y.cs != d.A) throw std::runtime_error("decode output layout");
+    check(d.y.ptr, 0, vlast(d.y, d.batch, ny, d.A), 2, "decode y");
+    return;
+  }
   if (l.kind != Launch::kSmall) {
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
@@ -1335,6 +1693,7 @@ void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
     case Launch::kIgemm: launch_conv_igemm(l.cp, stream_); break;
     case Launch::kDirect: launch_conv_direct(l.cp, stream_); break;
     case Launch::kDw: launch_dwconv(l.cp, stream_); break;
+    case Launch::kDecode: launch_pose_decode(l.dp, stream_); break;
     default: launch_small(l.small, l.sp, stream_); break;
     }
   }
@@ -1523,6 +1882,7 @@ std::string Model::nodeKernel(int i)
     return l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
+  case Launch::kDecode: return "pose_decode";
   default: return s.kernel;
   }
 }
@@ -1565,7 +1925,11 @@ void Model::buildStats()
         const Tensor & bt = *T_[n.ins[1]];
         s.flops = 2.0 * at.numel * (double)bt.dims.back();
       }
-      std::snprintf(buf, sizeof(buf), "%s -> %s [%ld]", n.op.c_str(), y.name.c_str(), (long)y.numel);
+      if (n.op == "pose_decode")
+        std::snprintf(buf, sizeof(buf), "pose_decode %d scales, %d anchors, R %d, %d classes, %d keypoints -> %s",
+                      n.i("S"), n.i("A"), n.i("R"), n.i("nc"), n.i("nk"), y.name.c_str());
+      else
+        std::snprintf(buf, sizeof(buf), "%s -> %s [%ld]", n.op.c_str(), y.name.c_str(), (long)y.numel);
       s.desc = buf;
     }
   }

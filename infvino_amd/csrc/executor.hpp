@@ -26,10 +26,11 @@ struct PlanNode {
 
 // One kernel launch with everything resolved for a given batch size.
 struct Launch {
-  enum Kind { kIgemm, kDirect, kDw, kSmall } kind = kSmall;
+  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode } kind = kSmall;
   int small = 0;
   ConvParams cp;
   SmallParams sp;
+  DecodeParams dp;
 };
 
 struct NodeStat {
@@ -81,6 +82,7 @@ class Model {
   struct Tensor;
   struct Root;
   void parse(const std::string & path);
+  void fuseDecode();
   void fuseResidual();
   void fuseActivation();
   void fusePermuteMatmul();

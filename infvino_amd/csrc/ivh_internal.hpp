@@ -103,4 +103,22 @@ struct SmallParams {
   int dims[18] = {0};          // ew_binary broadcast spec (rank <= 6)
 };
 
+// Fused Detect / Pose head decode: per-scale head tensors in, [4 + nc + 3 nk][A] out per image
+// (the plan's decode tail, matched by the executor).  Anchor a of scale s is pixel a - off[s]
+// of that scale's tensors.
+struct DecodeParams {
+  View x[4];                      // per scale: box distributions (4R ch) + classes (nc ch)
+  View k[4];                      // per scale: keypoints (3 nk ch; unused when nk == 0)
+  View y;                         // [4 + nc + 3 nk][A], channel stride A
+  const __half * dflw = nullptr;  // R bin weights of the DFL projection
+  const __half * anc = nullptr;   // anchor centres [2][A]
+  const __half * st = nullptr;    // strides [A]
+  const __half * ancm = nullptr;  // keypoint offsets [2][A] (anchors - 0.5)
+  const __half * cbox = nullptr;  // scalar: centre = (x1y1 + x2y2) / cbox (box_div) or * cbox
+  const __half * ckpt = nullptr;  // scalar: keypoint xy multiplier
+  int off[4] = {0, 0, 0, 0};      // first anchor of each scale
+  int nscale = 0, batch = 1, A = 0, R = 0, nc = 0, nk = 0, box_div = 1;
+  int vec = 0;                    // every x / k view is channels-last with 16-byte pixel rows
+};
+
 }  // namespace ivh

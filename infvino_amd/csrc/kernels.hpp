@@ -76,6 +76,7 @@ enum SmallOp : int {
   kBiasAdd,        // NCHW flat: i0 HW
 };
 void launch_small(int kind, const SmallParams & p, hipStream_t s);
+void launch_pose_decode(const DecodeParams & p, hipStream_t s);  // fused head decode
 void launch_bmm_mfma(const SmallParams & q, hipStream_t s);  // bmm_mfma.hip
 
 // boundary conversions (include/infvino/Half.hpp semantics for the truncating one)

@@ -1241,6 +1241,133 @@ void launch_small(int kind, const SmallParams & q, hipStream_t s)
   }
 }
 
+// ------------------------------------------------------------------ fused head decode
+// The plan's Detect / Pose decode tail (DFL softmax + bin projection, dist2bbox x strides,
+// sigmoid classes, keypoints (xy * c + (anchors - 0.5)) x strides and sigmoid visibility)
+// for one anchor of one image per thread; the node chain it replaces is described at the
+// executor's fuseDecode pass.  Every value a node of the chain would store is rounded to
+// fp16 here too (rh), with each node's fp32 formula (softmax_kernel, the 1x1 projection,
+// binop, act_f), so the output is the chain's up to the order of the projection's fp32 sum.
+namespace {
+__device__ __forceinline__ float rh(float v) { return (float)(_Float16)v; }
+__device__ __forceinline__ float hv(const __half * p, long i) { return (float)reinterpret_cast<const _Float16 *>(p)[i]; }
+
+// R_ / NC_ / NK_ > 0: compile-time channel counts (loops unroll, fx / fk index registers);
+// 0: the run-time counts in p.
+template <int R_, int NC_, int NK_, class FX, class FK>
+__device__ __forceinline__ void decode_anchor(const DecodeParams & p, int b, int a, FX && fx, FK && fk)
+{
+  const int R = R_ > 0 ? R_ : p.R, nc = NC_ > 0 ? NC_ : p.nc, nk = NK_ > 0 ? NK_ : p.nk;
+  _Float16 * y = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + a;
+  const long ys = p.y.cs;
+  const float ax = hv(p.anc, a), ay = hv(p.anc, (long)p.A + a), st = hv(p.st, a);
+  float d[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float m = -3.4e38f;
+#pragma unroll
+    for (int k = 0; k < R; ++k) m = fmaxf(m, fx(j * R + k));
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < R; ++k) s += __expf(fx(j * R + k) - m);
+    const float inv = 1.0f / s;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < R; ++k) acc += hv(p.dflw, k) * rh(__expf(fx(j * R + k) - m) * inv);
+    d[j] = rh(acc);
+  }
+  const float x1 = rh(ax - d[0]), y1 = rh(ay - d[1]), x2 = rh(ax + d[2]), y2 = rh(ay + d[3]);
+  const float cb = hv(p.cbox, 0);
+  const float sx = rh(x1 + x2), sy = rh(y1 + y2);
+  const float cx = rh(p.box_div ? sx / cb : sx * cb), cy = rh(p.box_div ? sy / cb : sy * cb);
+  y[0] = (_Float16)(cx * st);
+  y[ys] = (_Float16)(cy * st);
+  y[2 * ys] = (_Float16)(rh(x2 - x1) * st);
+  y[3 * ys] = (_Float16)(rh(y2 - y1) * st);
+#pragma unroll
+  for (int c = 0; c < nc; ++c) y[(4 + c) * ys] = (_Float16)act_f(fx(4 * R + c), kActSigmoid);
+  if (nk > 0) {
+    const float ck = hv(p.ckpt, 0), mx = hv(p.ancm, a), my = hv(p.ancm, (long)p.A + a);
+    _Float16 * yk = y + (4 + nc) * ys;
+#pragma unroll
+    for (int k = 0; k < nk; ++k) {
+      yk[(3 * k) * ys] = (_Float16)(rh(rh(fk(3 * k) * ck) + mx) * st);
+      yk[(3 * k + 1) * ys] = (_Float16)(rh(rh(fk(3 * k + 1) * ck) + my) * st);
+      yk[(3 * k + 2) * ys] = (_Float16)act_f(fk(3 * k + 2), kActSigmoid);
+    }
+  }
+}
+
+__device__ __forceinline__ View pick_view(const View (&v)[4], int s)
+{
+  View r = v[0];
+  if (s >= 1) r = v[1];
+  if (s >= 2) r = v[2];
+  if (s >= 3) r = v[3];
+  return r;
+}
+
+__device__ __forceinline__ int decode_scale(const DecodeParams & p, int a)
+{
+  int s = 0;
+  if (p.nscale > 1 && a >= p.off[1]) s = 1;
+  if (p.nscale > 2 && a >= p.off[2]) s = 2;
+  if (p.nscale > 3 && a >= p.off[3]) s = 3;
+  return s;
+}
+
+// channels-last heads, compile-time channel counts: a pixel's channels are 16-byte loads
+template <int R, int NC, int NK>
+__global__ void __launch_bounds__(256) pose_decode_vec_kernel(const DecodeParams p)
+{
+  constexpr int GX = (4 * R + NC + 7) / 8, GK = (3 * NK + 7) / 8;
+  const int a = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+  if (a >= p.A) return;
+  const int s = decode_scale(p, a), i = a - p.off[s];
+  const View xv = pick_view(p.x, s);
+  const _Float16 * xp = reinterpret_cast<const _Float16 *>(xv.ptr) + (long)b * xv.img + (long)i * xv.cs;
+  h8 x[GX];
+#pragma unroll
+  for (int g = 0; g < GX; ++g) x[g] = *reinterpret_cast<const h8 *>(xp + 8 * g);
+  h8 k[GK > 0 ? GK : 1];
+  if (NK > 0) {
+    const View kv = pick_view(p.k, s);
+    const _Float16 * kp = reinterpret_cast<const _Float16 *>(kv.ptr) + (long)b * kv.img + (long)i * kv.cs;
+#pragma unroll
+    for (int g = 0; g < GK; ++g) k[g] = *reinterpret_cast<const h8 *>(kp + 8 * g);
+  }
+  decode_anchor<R, NC, NK>(
+      p, b, a, [&](int c) { return (float)x[c / 8][c % 8]; }, [&](int c) { return (float)k[c / 8][c % 8]; });
+}
+
+// any layout, run-time channel counts (decode_anchor's unroll requests cannot be met here)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
+__global__ void __launch_bounds__(256) pose_decode_kernel(const DecodeParams p)
+{
+  const int a = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+  if (a >= p.A) return;
+  const int s = decode_scale(p, a), i = a - p.off[s];
+  const View xv = pick_view(p.x, s), kv = pick_view(p.k, s);
+  auto at = [&](const View & v, int c) {
+    return hv(v.ptr, (long)b * v.img + (v.layout == kNHWC ? (long)i * v.cs + c : (long)c * v.cs + i));
+  };
+  decode_anchor<0, 0, 0>(p, b, a, [&](int c) { return at(xv, c); }, [&](int c) { return at(kv, c); });
+}
+#pragma clang diagnostic pop
+}  // namespace
+
+void launch_pose_decode(const DecodeParams & p, hipStream_t s)
+{
+  const dim3 grid((unsigned)((p.A + 255) / 256), (unsigned)p.batch), blk(256);
+  if (p.vec && p.R == 16 && p.nc == 1 && p.nk == 17)
+    hipLaunchKernelGGL((pose_decode_vec_kernel<16, 1, 17>), grid, blk, 0, s, p);
+  else if (p.vec && p.R == 16 && p.nc == 80 && p.nk == 0)
+    hipLaunchKernelGGL((pose_decode_vec_kernel<16, 80, 0>), grid, blk, 0, s, p);
+  else
+    hipLaunchKernelGGL(pose_decode_kernel, grid, blk, 0, s, p);
+}
+
 // ------------------------------------------------------------- boundary conversions
 // f32 -> f16 exactly as include/infvino/Half.hpp:14-24: truncate the mantissa, flush
 // results with exponent <= 0 to signed zero, saturate exponent >= 31 (NaN too) to inf.
