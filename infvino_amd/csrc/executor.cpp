@@ -842,7 +842,6 @@ void Model::chooseLayouts()
     if (op == "maxpool" || op == "resize_nn" || op == "gap" || op == "ew_unary") return true;
     if (op == "copy_c") return n.i("dst_off") == 0;
     if (op == "concat4") return n.i("outer", 1) == 1;
-    if (op == "pose_decode") return slot < (size_t)n.i("S") * (n.i("nk") ? 2 : 1);  // head tensors
     if (op == "ew_binary") {
       const Tensor & y = *T_[n.outs[0]];
       if (!n.has("bdims") || n.i("b_scalar") == 1) return t.numel == y.numel;
@@ -1120,26 +1119,22 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
     const int no = 4 * d.R + d.nc, nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
     const size_t base = (size_t)d.nscale * (d.nk ? 2 : 1);
     if (n.ins.size() != base + 6) fail("decode inputs");
-    // 16-byte pixel rows: channels-last, aligned, and the rounded-up channel count inside
-    // the pixel pitch
-    auto vec_ok = [&](const Tensor & t, const View & v, int C) {
-      return t.kind == Tensor::kAct && v.layout == kNHWC && v.cs % 8 == 0 && v.img % 8 == 0 && t.coff % 8 == 0 &&
-             t.coff + round_up(C, 8) <= v.cs && (reinterpret_cast<uintptr_t>(v.ptr) & 15) == 0;
-    };
+    // the heads stay NCHW (the decode is no channels-last reader): per-channel reads are
+    // coalesced and the narrow head convs (1 or 51 channels) write NCHW rows faster
     long off = 0;
-    d.vec = 1;
+    d.nchw = 1;
     for (int s = 0; s < d.nscale; ++s) {
       const long hw = n.i(("hw" + std::to_string(s)).c_str());
       d.off[s] = (int)off;
       const Tensor & xt = *T_.at(n.ins[s]);
       if (xt.C != no || (long)xt.H * xt.W != hw || xt.numel != no * hw) fail("decode head geometry");
       d.x[s] = view(xt.name, batch);
-      if (!vec_ok(xt, d.x[s], no)) d.vec = 0;
+      if (d.x[s].layout != kNCHW) d.nchw = 0;
       if (d.nk) {
         const Tensor & kt = *T_.at(n.ins[d.nscale + s]);
         if (kt.C != nkc || (long)kt.H * kt.W != hw || kt.numel != nkc * hw) fail("decode keypoint geometry");
         d.k[s] = view(kt.name, batch);
-        if (!vec_ok(kt, d.k[s], nkc)) d.vec = 0;
+        if (d.k[s].layout != kNCHW) d.nchw = 0;
       }
       off += hw;
     }
@@ -1519,9 +1514,8 @@ void Model::validate(const Launch & l) const
     for (int s = 0; s < d.nscale; ++s) {
       const long hw = (s + 1 < d.nscale ? d.off[s + 1] : d.A) - d.off[s];
       if (hw < 1) throw std::runtime_error("decode scale offsets");
-      // the channels-last path reads whole 16-byte pieces of a pixel's channels
-      check(d.x[s].ptr, 0, vlast(d.x[s], d.batch, d.vec ? (no + 7) / 8 * 8 : no, hw), 2, "decode head");
-      if (d.nk) check(d.k[s].ptr, 0, vlast(d.k[s], d.batch, d.vec ? (nkc + 7) / 8 * 8 : nkc, hw), 2, "decode keypoints");
+      check(d.x[s].ptr, 0, vlast(d.x[s], d.batch, no, hw), 2, "decode head");
+      if (d.nk) check(d.k[s].ptr, 0, vlast(d.k[s], d.batch, nkc, hw), 2, "decode keypoints");
     }
     check(d.dflw, 0, d.R - 1, 2, "decode bin weights");
     check(d.anc, 0, 2L * d.A - 1, 2, "decode anchors");

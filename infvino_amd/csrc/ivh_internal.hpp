@@ -118,7 +118,7 @@ struct DecodeParams {
   const __half * ckpt = nullptr;  // scalar: keypoint xy multiplier
   int off[4] = {0, 0, 0, 0};      // first anchor of each scale
   int nscale = 0, batch = 1, A = 0, R = 0, nc = 0, nk = 0, box_div = 1;
-  int vec = 0;                    // every x / k view is channels-last with 16-byte pixel rows
+  int nchw = 0;                   // every x / k view is NCHW (the compile-time-count kernels)
 };
 
 }  // namespace ivh

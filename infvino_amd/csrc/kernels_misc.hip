@@ -1316,28 +1316,28 @@ __device__ __forceinline__ int decode_scale(const DecodeParams & p, int a)
   return s;
 }
 
-// channels-last heads, compile-time channel counts: a pixel's channels are 16-byte loads
+// NCHW heads, compile-time channel counts: each channel is one 2-byte load per lane,
+// consecutive lanes on consecutive pixels (coalesced), every channel read once
 template <int R, int NC, int NK>
-__global__ void __launch_bounds__(256) pose_decode_vec_kernel(const DecodeParams p)
+__global__ void __launch_bounds__(256) pose_decode_nchw_kernel(const DecodeParams p)
 {
-  constexpr int GX = (4 * R + NC + 7) / 8, GK = (3 * NK + 7) / 8;
+  constexpr int NX = 4 * R + NC, NKC = 3 * NK;
   const int a = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
   if (a >= p.A) return;
   const int s = decode_scale(p, a), i = a - p.off[s];
   const View xv = pick_view(p.x, s);
-  const _Float16 * xp = reinterpret_cast<const _Float16 *>(xv.ptr) + (long)b * xv.img + (long)i * xv.cs;
-  h8 x[GX];
+  const _Float16 * xp = reinterpret_cast<const _Float16 *>(xv.ptr) + (long)b * xv.img + i;
+  _Float16 x[NX];
 #pragma unroll
-  for (int g = 0; g < GX; ++g) x[g] = *reinterpret_cast<const h8 *>(xp + 8 * g);
-  h8 k[GK > 0 ? GK : 1];
+  for (int c = 0; c < NX; ++c) x[c] = xp[(long)c * xv.cs];
+  _Float16 k[NKC > 0 ? NKC : 1];
   if (NK > 0) {
     const View kv = pick_view(p.k, s);
-    const _Float16 * kp = reinterpret_cast<const _Float16 *>(kv.ptr) + (long)b * kv.img + (long)i * kv.cs;
+    const _Float16 * kp = reinterpret_cast<const _Float16 *>(kv.ptr) + (long)b * kv.img + i;
 #pragma unroll
-    for (int g = 0; g < GK; ++g) k[g] = *reinterpret_cast<const h8 *>(kp + 8 * g);
+    for (int c = 0; c < NKC; ++c) k[c] = kp[(long)c * kv.cs];
   }
-  decode_anchor<R, NC, NK>(
-      p, b, a, [&](int c) { return (float)x[c / 8][c % 8]; }, [&](int c) { return (float)k[c / 8][c % 8]; });
+  decode_anchor<R, NC, NK>(p, b, a, [&](int c) { return (float)x[c]; }, [&](int c) { return (float)k[c]; });
 }
 
 // any layout, run-time channel counts (decode_anchor's unroll requests cannot be met here)
@@ -1360,10 +1360,10 @@ __global__ void __launch_bounds__(256) pose_decode_kernel(const DecodeParams p)
 void launch_pose_decode(const DecodeParams & p, hipStream_t s)
 {
   const dim3 grid((unsigned)((p.A + 255) / 256), (unsigned)p.batch), blk(256);
-  if (p.vec && p.R == 16 && p.nc == 1 && p.nk == 17)
-    hipLaunchKernelGGL((pose_decode_vec_kernel<16, 1, 17>), grid, blk, 0, s, p);
-  else if (p.vec && p.R == 16 && p.nc == 80 && p.nk == 0)
-    hipLaunchKernelGGL((pose_decode_vec_kernel<16, 80, 0>), grid, blk, 0, s, p);
+  if (p.nchw && p.R == 16 && p.nc == 1 && p.nk == 17)
+    hipLaunchKernelGGL((pose_decode_nchw_kernel<16, 1, 17>), grid, blk, 0, s, p);
+  else if (p.nchw && p.R == 16 && p.nc == 80 && p.nk == 0)
+    hipLaunchKernelGGL((pose_decode_nchw_kernel<16, 80, 0>), grid, blk, 0, s, p);
   else
     hipLaunchKernelGGL(pose_decode_kernel, grid, blk, 0, s, p);
 }

@@ -142,12 +142,31 @@ def test_decode_formula_matches_chain(plans):
 
 # ------------------------------------------------------------------ GPU: fused vs chain
 
+def _small_pose(out_dir, nc, nk):
+    """A 128x128 toy backbone (strides 8 / 16 / 32) under a pose head with nc classes and
+    nk keypoints: counts the decode kernel has no compile-time instance for."""
+    pb = pw.PlanBuilder(out_dir, seed=3)
+    x = pb.input("images", [1, 3, 128, 128])
+    x = pb.conv(pb.conv(x, 16, 3, 2), 32, 3, 2)
+    f3 = pb.conv(x, 32, 3, 2)
+    f4 = pb.conv(f3, 64, 3, 2)
+    f5 = pb.conv(f4, 64, 3, 2)
+    pb.output(pw._pose_head(pb, [f3, f4, f5], nc=nc, nk=(nk, 3)))
+    return pb.write()
+
+
+def test_decode_tail_fused_other_counts(tmp_path):
+    assert _kernels(_small_pose(str(tmp_path), 2, 5)).count("pose_decode") == 1
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,batch,flags", [("yolov8n-pose", 3, 0), ("yolo11n-pose", 2, 0),
-                                               ("yolov8n-pose", 2, ia.IVH_FLAG_NCHW_ONLY)])
-def test_decode_fused_vs_chain_gpu(plans, name, batch, flags):
-    """Channels-last heads take the vector kernel, NCHW_ONLY the generic one."""
-    path = plans(name)[0]
+                                               ("yolov8n-pose", 2, ia.IVH_FLAG_NCHW_ONLY),
+                                               ("small-nc2-nk5", 3, 0)])
+def test_decode_fused_vs_chain_gpu(plans, tmp_path, name, batch, flags):
+    """The YOLO heads take the compile-time-count kernel, the toy head (2 classes, 5
+    keypoints) the run-time-count one."""
+    path = _small_pose(str(tmp_path), 2, 5) if name.startswith("small") else plans(name)[0]
     p = O.Plan.load(path)
     x = O.f2h(np.random.default_rng(7).random(p.numel(p.input_name) * batch).astype(np.float32))
     res = {}
@@ -162,13 +181,13 @@ def test_decode_fused_vs_chain_gpu(plans, name, batch, flags):
     a, b = res[0], res[ia.IVH_FLAG_NO_FUSE_DECODE]
     u = _ulps(a, b)
     print(f"{name} b{batch} flags {flags:#x}: max {u.max()} ulp, exact {(u == 0).mean():.6f}")
+    ny, A = p.dims[p.outputs[0]][1:]
     for i in np.argsort(-u)[:8]:
         if u[i]:
-            print(f"  row {(i // 8400) % 56} anchor {i % 8400} image {i // (56 * 8400)}: fused {a[i]!r} chain {b[i]!r} ({u[i]} ulp)")
+            print(f"  row {(i // A) % ny} anchor {i % A} image {i // (ny * A)}: fused {a[i]!r} chain {b[i]!r} ({u[i]} ulp)")
     # A rare 1-ulp flip of a DFL distance (fp32 summation order) moves a box edge by one
     # distance ulp times the stride; where anchor - distance cancels that is many ulps of a
     # small output, so box rows are bounded in pixels (half a pixel), the rest in ulps.
-    rows = (np.arange(a.size) // 8400) % 56
-    boxr = rows < 4
+    boxr = (np.arange(a.size) // A) % ny < 4
     assert (u == 0).mean() > 0.9999
     assert np.abs(a - b)[boxr].max() <= 0.5 and u[~boxr].max() <= 2
