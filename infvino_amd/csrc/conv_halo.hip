@@ -43,8 +43,13 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
   constexpr int WCH = BK / 8;
   constexpr int W_IT = (BN * WCH + 255) / 256;
   constexpr bool W_FULL = W_IT * 256 == BN * WCH;
-  constexpr int ZROW = PMAX;                        // all-zero patch pixel
-  constexpr int L_PATCH = (PMAX + 1) * CKP;
+  // patch rows padded so each starts where a linear layout of the same pixels would, modulo
+  // 256 bytes: MFMA pixel fragments that wrap a tile row stay LDS bank-conflict free.  Not
+  // with 16-channel chunks: those layers are latency bound and the pad's LDS reserve would
+  // cost them two of eight resident work-groups per CU (measured slower)
+  constexpr int PADH = CK == 16 ? 0 : ((256 - (4 * CKP) % 256) % 256) / 2;
+  constexpr int ZOFF = PMAX * CKP + kHaloMaxRows * PADH;  // all-zero patch pixel
+  constexpr int L_PATCH = ZOFF + CKP;
   constexpr int L_MAIN = L_PATCH + 2 * BN * LDK;
   constexpr int L_ALL = L_MAIN > T::EPI ? L_MAIN : T::EPI;
   __shared__ __attribute__((aligned(16))) _Float16 lds[L_ALL];
@@ -53,7 +58,7 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
-  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW;
+  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW, RPH = PW * CKP + PADH;
   const int Hs = p.H + 1;                                  // rows per image incl. separator
   const int Htot = p.batch * Hs - 1;                       // tall-image rows
   const int tiles_x = (p.Wo + TW - 1) / TW;
@@ -81,12 +86,15 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
   // since 256 is a multiple of CQ).  Byte offset of the piece in chunk 0, or out of range.
   const int q8 = (tid % CQ) * 8;
   unsigned psrc[P_IT];
+  int pdst[P_IT];  // LDS offset of the piece, -1 past the patch
 #pragma unroll
   for (int i = 0; i < P_IT; ++i) {
     const int pp = (tid + i * 256) / CQ;
     psrc[i] = kBufOOB;
+    pdst[i] = -1;
     if (pp < PP) {
       const int py = idiv_small(pp, PW, inv_pw), px = pp - py * PW;
+      pdst[i] = py * RPH + px * CKP + q8;
       const int gy = oy0 - 1 + py, ix = ox0 - 1 + px;
       if (gy >= 0 && gy < Htot && (unsigned)ix < (unsigned)p.W) {
         const int b = idiv_small(gy, Hs, inv_hs), r = gy - b * Hs;
@@ -119,11 +127,10 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
     for (int k = 0; k < 8; ++k) keep[k] = c * CK + q8 + k < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
 #pragma unroll
     for (int i = 0; i < P_IT; ++i) {
-      const int e = tid + i * 256;
-      if (e < PP * CQ) {
+      if (pdst[i] >= 0) {
         h8 v = rp[i];
         if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
-        *reinterpret_cast<h8 *>(Ps + (e / CQ) * CKP + q8) = v;
+        *reinterpret_cast<h8 *>(Ps + pdst[i]) = v;
       }
     }
   };
@@ -148,11 +155,11 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
     int pl = wm * TM * MB + tm * MB + F::col(lane);
     if (pl >= TH * TW) pl = 0;
     const int ty = idiv_small(pl, TW, inv_tw), tx = pl - ty * TW;
-    bl[tm] = (ty * PW + tx) * CKP + (F::kq(lane) % CK);
+    bl[tm] = ty * RPH + tx * CKP + (F::kq(lane) % CK);
   }
   const int lane_tap = (CK == 16 && MB == 16) ? (F::kq(lane) >= 16 ? 1 : 0) : 0;
-  const int zbase = ZROW * CKP + (F::kq(lane) % CK);
-  auto tapoff = [&](int tap) { return ((tap / 3) * PW + (tap % 3)) * CKP; };
+  const int zbase = ZOFF + (F::kq(lane) % CK);
+  auto tapoff = [&](int tap) { return (tap / 3) * RPH + (tap % 3) * CKP; };
   const int arow = (wn * TN * MB + (lane % MB)) * LDK + F::kq(lane);
 
   acc_t acc[TN][TM];
@@ -163,7 +170,7 @@ __global__ void __launch_bounds__(256) conv3x3s1_kernel(const ConvParams p)
 #pragma unroll
       for (int v = 0; v < F::NV; ++v) acc[a][b][v] = 0.0f;
 
-  if (TAPS == 10 && tid < CQ) *reinterpret_cast<h8 *>(Ps + ZROW * CKP + tid * 8) = h8{};
+  if (TAPS == 10 && tid < CQ) *reinterpret_cast<h8 *>(Ps + ZOFF + tid * 8) = h8{};
   load_patch(0);
   load_w(0);
   store_patch(0);
@@ -260,6 +267,7 @@ static bool halo_tile(int cfg, int cout, int H, int W, int batch, long * wgs, in
     int h = d.bm / w;
     h = (int)std::min<long>(h, Htot);
     h = std::min(h, d.pmax / (w + 2) - 2);
+    h = std::min(h, kHaloMaxRows - 2);  // padded patch rows fit the LDS reserve
     if (h < 1) continue;
     const long ty = (Htot + h - 1) / h, tx = (W + w - 1) / w;
     const int hh = (int)((Htot + ty - 1) / ty), ww = (int)((W + tx - 1) / tx);  // balanced

@@ -43,19 +43,26 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   constexpr int KROW = 9 * CK;             // weights per output channel kept in LDS
   constexpr int LDK = KROW + 8;            // weight row pitch (halves): conflict-free reads
   constexpr int CKP = CK + 8;              // patch pixel pitch (halves)
+  // Patch rows are padded so that every row starts where an unpadded linear layout of the
+  // same pixels would start modulo 256 bytes: the 32 lanes of a B fragment (32 consecutive
+  // tile pixels, wrapping tile rows) then hit LDS banks exactly as consecutive pixels do,
+  // which is conflict-free (measured: a 32-pixel fragment over 8-wide tile rows read at half
+  // the LDS rate without the pad).
+  constexpr int PADH = ((256 - (4 * CKP) % 256) % 256) / 2;  // halves: -2 pixels mod 256 B
+  constexpr int L_PATCH = PMAX * CKP + kResMaxRows * PADH;
   constexpr int CQ = CK / 8;               // 16-byte pieces per patch pixel
   constexpr int P_IT = (PMAX * CQ + NT - 1) / NT;
   constexpr int WQ = KROW / 8;             // 16-byte pieces per weight row
   constexpr int W_IT = (BN * WQ + NT - 1) / NT;
   constexpr int NG = TN * TM * 4;          // epilogue groups (4 accumulator values) per lane
-  __shared__ __attribute__((aligned(16))) _Float16 lds[BN * LDK + PMAX * CKP];
+  __shared__ __attribute__((aligned(16))) _Float16 lds[BN * LDK + L_PATCH];
   __shared__ __attribute__((aligned(16))) float bias_s[BN];
   _Float16 * const Ws = lds;
   _Float16 * const Ps = lds + BN * LDK;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
-  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW;
+  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW, RPH = PW * CKP + PADH;
   const int Hs = p.H + 1;                       // rows per image incl. separator
   const int tiles_x = (p.W + TW - 1) / TW;
   const int ntiles = ((p.batch * Hs - 1 + TH - 1) / TH) * tiles_x;
@@ -131,11 +138,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   auto store_patch = [&](const h8 (&rp)[P_IT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < P_IT; ++i) {
-      const int e = tid + i * NT;
-      if (i * NT + NT <= PMAX * CQ || e < PMAX * CQ) {
+      if (pyx[i] != 0x7fff0000) {  // pixels past the patch are never read
         h8 v = rp[i];
         if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
-        *reinterpret_cast<h8 *>(Ps + (e / CQ) * CKP + q8) = v;
+        *reinterpret_cast<h8 *>(Ps + (pyx[i] >> 16) * RPH + (pyx[i] & 0xffff) * CKP + q8) = v;
       }
     }
   };
@@ -172,12 +178,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
     const int pl = wm * TM * 32 + tm * 32 + F::col(lane);
     const int pc = pl < TH * TW ? pl : 0;  // slot past the tile: computed on pixel 0, never stored
     const int ty = idiv_small(pc, TW, inv_tw), tx = pc - ty * TW;
-    bl[tm] = (ty * PW + tx) * CKP + F::kq(lane);
+    bl[tm] = ty * RPH + tx * CKP + F::kq(lane);
   }
   const int arow = (wn * TN * 32 + (lane & 31)) * LDK + F::kq(lane);
   int tapoff[9];
 #pragma unroll
-  for (int tap = 0; tap < 9; ++tap) tapoff[tap] = ((tap / 3) * PW + (tap % 3)) * CKP;
+  for (int tap = 0; tap < 9; ++tap) tapoff[tap] = (tap / 3) * RPH + (tap % 3) * CKP;
 
   // output byte offsets of this lane's pixel blocks in tile t (past the buffer range: no
   // output), for y and the residual view.  Stores and residual loads are buffer accesses
@@ -407,6 +413,7 @@ bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, in
     int h = std::min(d.bm / w, H - 1);           // TH + 2 <= H + 1
     h = (int)std::min<long>(h, Htot);
     h = std::min(h, d.pmax / (w + 2) - 2);
+    h = std::min(h, kResMaxRows - 2);            // padded patch rows fit the LDS reserve
     if (h < 1) continue;
     const long ty = (Htot + h - 1) / h, tx = (W + w - 1) / w;
     const int hh = (int)((Htot + ty - 1) / ty), ww = (int)((W + tx - 1) / tx);  // balanced

@@ -1548,7 +1548,7 @@ void Model::validate(const Launch & l) const
         const int cfg = p.halo - 1, ck = p.ck;
         if (cfg < 0 || cfg > 7 || ck != halo_cfg_ck(cfg, p.Cin)) throw std::runtime_error("halo chunk size");
         if (p.K != 3 || p.S != 1 || p.P != 1 || p.ksplit != 1 || cfg < 0 || cfg > 7 || p.th < 1 || p.tw < 1 ||
-            p.Ho != p.H || p.Wo != p.W || (p.th + 2) * (p.tw + 2) > halo_pmax(cfg) ||
+            p.Ho != p.H || p.Wo != p.W || (p.th + 2) * (p.tw + 2) > halo_pmax(cfg) || p.th + 2 > kHaloMaxRows ||
             p.th * p.tw > (cfg < 4 ? 256 : 128) || (p.Cout + halo_bn(cfg) - 1) / halo_bn(cfg) * halo_bn(cfg) > rows)
           throw std::runtime_error("halo geometry");
         if (p.kpad != (p.Cin + ck - 1) / ck * halo_taps(ck) * ck) throw std::runtime_error("halo weight packing");
@@ -1559,6 +1559,7 @@ void Model::validate(const Launch & l) const
         if (cfg < 0 || cfg > 2 || p.halo || p.s2 || ck != res_ck(p.Cin) || p.Cin > ck || p.K != 3 || p.S != 1 ||
             p.P != 1 || p.ksplit != 1 || p.th < 1 || p.tw < 1 || p.Ho != p.H || p.Wo != p.W ||
             p.th * p.tw > res_bm(cfg) || (p.th + 2) * (p.tw + 2) > res_pmax(cfg) || p.th + 2 > p.H + 1 ||
+            p.th + 2 > kResMaxRows ||
             (cfg == 0) != (p.Cout > 32) || (cfg == 2) != (p.Cout <= 32 && ck == 64) || !res_views_ok(p))
           throw std::runtime_error("resident-weight conv geometry");
         if (p.kpad != halo_taps(ck) * ck) throw std::runtime_error("resident-weight packing");

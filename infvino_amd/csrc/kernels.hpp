@@ -39,7 +39,9 @@ bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, in
 // the output (and residual) views suit the kernel's 8-byte channels-last buffer stores
 bool res_views_ok(const ConvParams & p);
 bool res_full_stores(const ConvParams & p);  // 4-channel stores (Cout % 4 == 0 or padding)
-constexpr int kResMinTiles = 1;      // fewer tiles: the halo / im2col kernels
+constexpr int kResMinTiles = 1;  // fewer tiles: the halo / im2col kernels
+constexpr int kResMaxRows = 34;  // patch rows (TH + 2) of the resident-weight kernel's tiles
+constexpr int kHaloMaxRows = 34;  // patch rows (TH + 2) of the LDS-patch kernel's tiles
 void launch_conv_res(const ConvParams & p, hipStream_t s);
 
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
