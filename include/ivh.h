@@ -58,8 +58,6 @@ extern "C" {
 #define IVH_FLAG_NO_FUSE_DECODE 0x400u /* keep a Detect / Pose head's decode tail (DFL,
                                           dist2bbox, keypoint decode) node by node instead of
                                           one fused kernel */
-#define IVH_FLAG_NO_FUSE_STEM 0x800u /* the stem conv and the stride-2 conv that reads it run
-                                        as two kernels (the stem's output goes to memory) */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 

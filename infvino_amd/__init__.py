@@ -33,7 +33,6 @@ IVH_FLAG_NO_SPLITK = 0x80
 IVH_FLAG_NO_HALO = 0x100
 IVH_FLAG_NO_RESIDENT = 0x200
 IVH_FLAG_NO_FUSE_DECODE = 0x400
-IVH_FLAG_NO_FUSE_STEM = 0x800
 
 # every symbol include/ivh.h declares, with (restype, argtypes)
 _vp, _i, _u32, _sz, _d = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_double

@@ -1098,68 +1098,7 @@ View Model::view(const std::string & name, int batch) const
   return v;
 }
 
-// Node ni is a stem (3x3 stride 2, Cin <= 3) whose output only the next node reads, and that
-// node is a 3x3 stride-2 conv without residual: the pair may run as one kernel
-// (conv_stem_s2.hip) when both resolve to the kernels it restates.
-bool Model::stemPair(size_t ni) const
-{
-  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_STEM) || ni + 1 >= nodes_.size() || skip_[ni] || skip_[ni + 1])
-    return false;
-  const PlanNode & a = nodes_[ni];
-  const PlanNode & b = nodes_[ni + 1];
-  if (a.op != "conv3x3" || b.op != "conv3x3" || a.outs.size() != 1 || b.ins.empty()) return false;
-  if (a.i("stride", 1) != 2 || a.i("pad", 1) != 1 || b.i("stride", 1) != 2 || b.i("pad", 1) != 1) return false;
-  if ((a.ins.size() > 3 && a.ins[3] != "-") || (b.ins.size() > 3 && b.ins[3] != "-")) return false;
-  const Tensor & t = *T_.at(a.outs[0]);
-  if (b.ins[0] != t.name || t.users.size() != 1 || t.users[0] != (int)ni + 1) return false;
-  for (const auto & o : outputs_)
-    if (o == t.name) return false;
-  return T_.at(a.ins[0])->C <= 3 && stem_s2_act_ok(a.i("act"), b.i("act"));
-}
-
 void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
-{
-  if (stemPair(ni)) {
-    std::vector<Launch> la, lb;
-    emitNodeBase(ni, batch, la);
-    emitNodeBase(ni + 1, batch, lb);
-    if (la.size() == 1 && lb.size() == 1 && la[0].kind == Launch::kDirect && la[0].cp.stem_mfma && la[0].cp.w2 &&
-        lb[0].kind == Launch::kIgemm && !lb[0].cp.halo && !lb[0].cp.res) {
-      const ConvParams & a = la[0].cp;
-      const ConvParams & c = lb[0].cp;
-      Launch L;
-      L.kind = Launch::kStemS2;
-      StemS2Params & q = L.ss;
-      q.x = a.x;
-      q.y = c.y;
-      q.w1 = a.w2;
-      q.b1 = a.bias;
-      q.w2 = c.w;
-      q.b2 = c.bias;
-      q.kpad2 = c.kpad;
-      q.batch = batch;
-      q.Cin = a.Cin;
-      q.C1 = a.Cout;
-      q.C2 = c.Cout;
-      q.H0 = a.H;
-      q.W0 = a.W;
-      q.H1 = a.Ho;
-      q.W1 = a.Wo;
-      q.H2 = c.Ho;
-      q.W2 = c.Wo;
-      q.act1 = a.act;
-      q.act2 = c.act;
-      q.nb = stem_s2_bands(batch, q.H2);
-      if (c.Cin == a.Cout && c.H == a.Ho && c.W == a.Wo && c.cin8 == 16 && stem_s2_supported(q)) {
-        out.push_back(L);
-        return;
-      }
-    }
-  }
-  emitNodeBase(ni, batch, out);
-}
-
-void Model::emitNodeBase(size_t ni, int batch, std::vector<Launch> & out)
 {
   const PlanNode & n = nodes_[ni];
   const Tensor & yt = *T_[n.outs[0]];
@@ -1534,8 +1473,7 @@ const std::vector<Launch> & Model::launches(int batch)
   std::vector<size_t> beg(nodes_.size()), end(nodes_.size());
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     beg[ni] = L.size();
-    const bool fused = ni > 0 && end[ni - 1] > beg[ni - 1] && L[end[ni - 1] - 1].kind == Launch::kStemS2;
-    if (!skip_[ni] && !fused) emitNode(ni, batch, L);
+    if (!skip_[ni]) emitNode(ni, batch, L);
     end[ni] = L.size();
   }
   node_launch_begin_ = beg;
@@ -1569,18 +1507,6 @@ void Model::validate(const Launch & l) const
     if (C <= 0 || HW <= 0 || B <= 0) return -1;
     return (long)(B - 1) * v.img + (v.layout == kNHWC ? (HW - 1) * v.cs + (C - 1) : (C - 1) * v.cs + (HW - 1));
   };
-  if (l.kind == Launch::kStemS2) {
-    const StemS2Params & q = l.ss;
-    if (q.batch < 1 || (long)q.batch * q.nb > (1L << 30) || q.nb < 1 || !stem_s2_supported(q))
-      throw std::runtime_error("stem + stride-2 geometry");
-    check(q.x.ptr, 0, vlast(q.x, q.batch, q.Cin, (long)q.H0 * q.W0), 2, "stem x");
-    check(q.y.ptr, 0, vlast(q.y, q.batch, q.C2, (long)q.H2 * q.W2), 2, "stride-2 y");
-    check(q.w1, 0, 16 * 64 - 1, 2, "stem w");
-    check(q.w2, 0, (long)(q.C2 - 1) * q.kpad2 + 143, 2, "stride-2 w");
-    if (q.b1) check(q.b1, 0, q.C1 - 1, 4, "stem bias");
-    if (q.b2) check(q.b2, 0, q.C2 - 1, 4, "stride-2 bias");
-    return;
-  }
   if (l.kind == Launch::kDecode) {
     const DecodeParams & d = l.dp;
     if (d.batch < 1 || d.batch > 65535 || d.nscale < 1 || d.nscale > 4) throw std::runtime_error("decode grid");
@@ -1763,7 +1689,6 @@ void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
     case Launch::kDirect: launch_conv_direct(l.cp, stream_); break;
     case Launch::kDw: launch_dwconv(l.cp, stream_); break;
     case Launch::kDecode: launch_pose_decode(l.dp, stream_); break;
-    case Launch::kStemS2: launch_stem_s2(l.ss, stream_); break;
     default: launch_small(l.small, l.sp, stream_); break;
     }
   }
@@ -1945,9 +1870,7 @@ std::string Model::nodeKernel(int i)
 {
   const NodeStat & s = stats_.at(i);
   const auto & L = launches(max_batch_);
-  if (node_launch_begin_.at(i) == node_launch_end_.at(i))
-    return (i > 0 && node_launch_end_[i - 1] > node_launch_begin_[i - 1] &&
-            L[node_launch_end_[i - 1] - 1].kind == Launch::kStemS2) ? "(fused)" : "(view)";
+  if (node_launch_begin_.at(i) == node_launch_end_.at(i)) return "(view)";
   const Launch & l = L[node_launch_begin_[i]];
   switch (l.kind) {
   case Launch::kIgemm:
@@ -1955,7 +1878,6 @@ std::string Model::nodeKernel(int i)
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";
-  case Launch::kStemS2: return "conv_stem_s2";
   default: return s.kernel;
   }
 }

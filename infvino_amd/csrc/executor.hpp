@@ -26,12 +26,11 @@ struct PlanNode {
 
 // One kernel launch with everything resolved for a given batch size.
 struct Launch {
-  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode, kStemS2 } kind = kSmall;
+  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode } kind = kSmall;
   int small = 0;
   ConvParams cp;
   SmallParams sp;
   DecodeParams dp;
-  StemS2Params ss;
 };
 
 struct NodeStat {
@@ -98,8 +97,6 @@ class Model {
   View view(const std::string & name, int batch) const;
   void enqueue(const std::vector<Launch> & L, size_t b, size_t e);
   void emitNode(size_t ni, int batch, std::vector<Launch> & out);
-  void emitNodeBase(size_t ni, int batch, std::vector<Launch> & out);
-  bool stemPair(size_t ni) const;
   void validate(const Launch & l) const;
   void * devAlloc(size_t bytes, bool zero);
   void devUpload(void * d, const void * src, size_t bytes);

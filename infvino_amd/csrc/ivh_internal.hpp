@@ -103,20 +103,6 @@ struct SmallParams {
   int dims[18] = {0};          // ew_binary broadcast spec (rank <= 6)
 };
 
-// A stem (3x3 stride 2, Cin <= 3) and the stride-2 3x3 conv that is its only reader, as one
-// kernel (conv_stem_s2.hip).  nb = bands of output rows per image (one work-group each).
-struct StemS2Params {
-  View x, y;                      // image (NCHW, Cin planes), output (channels-last)
-  const __half * w1 = nullptr;    // stem weights fp16 [16][64], k = tap * 4 + ci
-  const float * b1 = nullptr;     // stem bias (C1) or null
-  const __half * w2 = nullptr;    // second conv's weights, implicit-GEMM packing [C2][kpad2], k = tap * 16 + ci
-  const float * b2 = nullptr;     // second conv's bias (C2) or null
-  int kpad2 = 0;
-  int batch = 1, Cin = 3, C1 = 16, C2 = 32;
-  int H0 = 0, W0 = 0, H1 = 0, W1 = 0, H2 = 0, W2 = 0;
-  int act1 = 0, act2 = 0, nb = 1;
-};
-
 // Fused Detect / Pose head decode: per-scale head tensors in, [4 + nc + 3 nk][A] out per image
 // (the plan's decode tail, matched by the executor).  Anchor a of scale s is pixel a - off[s]
 // of that scale's tensors.

@@ -79,11 +79,6 @@ enum SmallOp : int {
 };
 void launch_small(int kind, const SmallParams & p, hipStream_t s);
 void launch_pose_decode(const DecodeParams & p, hipStream_t s);  // fused head decode
-// conv_stem_s2.hip: stem + the stride-2 conv reading it, one kernel
-bool stem_s2_supported(const StemS2Params & q);
-bool stem_s2_act_ok(int a1, int a2);
-int stem_s2_bands(int batch, int H2);
-void launch_stem_s2(const StemS2Params & q, hipStream_t s);
 void launch_bmm_mfma(const SmallParams & q, hipStream_t s);  // bmm_mfma.hip
 
 // boundary conversions (include/infvino/Half.hpp semantics for the truncating one)

@@ -166,30 +166,6 @@ def test_res_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
-@pytest.mark.parametrize("H,W,c1,c2,batch,act", [
-    (640, 640, 16, 32, 2, pw.ACT_SILU),   # the YOLO input pair
-    (64, 48, 16, 32, 3, pw.ACT_SILU),     # several bands per image
-    (34, 40, 16, 16, 2, pw.ACT_HSWISH),   # odd stem height (a zero stem row at the bottom), 16 out
-    (40, 56, 12, 24, 1, pw.ACT_SILU),     # ragged stem channels, 24 outputs (a partial channel block)
-])
-def test_stem_s2_fused(tmp_path, H, W, c1, c2, batch, act):
-    """Stem (3x3 s2, 3 channels) + the 3x3 s2 conv reading it as one kernel: against the oracle
-    and against the two stand-alone kernels (IVH_FLAG_NO_FUSE_STEM)."""
-    def build(pb):
-        x = pb.input("x", [1, 3, H, W])
-        y = pb.conv(pb.conv(x, c1, 3, 2, act=act), c2, 3, 2, act=act)
-        return pb.unary(y, pw.UN_RELU)
-    path = _small_plan(tmp_path, build)
-    print(f"stem+s2 {H}x{W} {c1}->{c2} batch {batch}", flush=True)
-    ks = _kernels(path, batch)
-    assert ks[:2] == ["conv_stem_s2", "(fused)"], ks
-    assert _kernels(path, batch, ia.IVH_FLAG_NO_FUSE_STEM)[0] == "conv_stem"
-    got = _check_f32(path, batch, lo=0.0, ref_mode=False)
-    _, _, other = _run(path, batch, lo=0.0, flags=ia.IVH_FLAG_NO_FUSE_STEM)
-    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
-    assert mean_rel < 1e-4 and max_rel < 2e-3, (mean_rel, max_rel)
-
-
 def test_res_residual_chain(tmp_path):
     """Bottleneck chain of 48 channels at batch 24 (3x3 SiLU, 3x3 + residual) and a 3x3
     without activation + residual: the resident-weight kernel with the fused residual add."""
