@@ -1098,7 +1098,23 @@ View Model::view(const std::string & name, int batch) const
   return v;
 }
 
-void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
+// Nodes ni, ni + 1, ni + 2 are SPPF's chained max pools: 5x5, stride 1, pad 2, each reading
+// the previous one's output (which may have other readers), same geometry.
+bool Model::sppfChain(size_t ni) const
+{
+  if ((flags_ & IVH_FLAG_NO_FUSE) || ni + 2 >= nodes_.size()) return false;
+  for (size_t k = ni; k < ni + 3; ++k) {
+    const PlanNode & n = nodes_[k];
+    if (n.op != "maxpool" || skip_[k] || n.i("K", 5) != 5 || n.i("S", 1) != 1 || n.i("P", 2) != 2 ||
+        n.i("Hout") != n.i("H") || n.i("Wout") != n.i("W") || n.i("C") != nodes_[ni].i("C") ||
+        n.i("H") != nodes_[ni].i("H") || n.i("W") != nodes_[ni].i("W") || n.ins.empty() || n.outs.size() != 1)
+      return false;
+    if (k > ni && n.ins[0] != nodes_[k - 1].outs[0]) return false;
+  }
+  return true;
+}
+
+void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vector<char> & covered)
 {
   const PlanNode & n = nodes_[ni];
   const Tensor & yt = *T_[n.outs[0]];
@@ -1403,6 +1419,25 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out)
       fail("pool/resize channels-last geometry");
     if (q.a.layout == kNCHW) q.a.cs = q.H * q.W;
     if (q.y.layout == kNCHW) q.y.cs = q.Ho * q.Wo;
+    // SPPF: the three chained pools as one launch when every view is 16-byte channels-last
+    // and the plane's four LDS copies fit in 64 KB
+    if (op == "maxpool" && sppfChain(ni)) {
+      Launch F = L;
+      SmallParams & f = F.sp;
+      f.b = view(nodes_[ni + 1].outs[0], batch);
+      f.c = view(nodes_[ni + 2].outs[0], batch);
+      auto v8 = [&](const View & v, const std::string & t) {
+        return v.layout == kNHWC && v.cs % 8 == 0 && v.img % 8 == 0 && T_.at(t)->coff % 8 == 0 &&
+               (reinterpret_cast<uintptr_t>(v.ptr) & 15) == 0;
+      };
+      if (q.C % 8 == 0 && (long)q.H * q.W <= 1024 && v8(f.a, n.ins[0]) && v8(f.y, n.outs[0]) &&
+          v8(f.b, nodes_[ni + 1].outs[0]) && v8(f.c, nodes_[ni + 2].outs[0])) {
+        F.small = kMaxPoolSppf;
+        out.push_back(F);
+        covered[ni + 1] = covered[ni + 2] = 1;
+        return;
+      }
+    }
     out.push_back(L);
     return;
   }
@@ -1471,13 +1506,15 @@ const std::vector<Launch> & Model::launches(int batch)
   if (it != launch_cache_.end()) return it->second;
   std::vector<Launch> L;
   std::vector<size_t> beg(nodes_.size()), end(nodes_.size());
+  std::vector<char> covered(nodes_.size(), 0);
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     beg[ni] = L.size();
-    if (!skip_[ni]) emitNode(ni, batch, L);
+    if (!skip_[ni] && !covered[ni]) emitNode(ni, batch, L, covered);
     end[ni] = L.size();
   }
   node_launch_begin_ = beg;
   node_launch_end_ = end;
+  node_covered_ = covered;
   for (size_t ni = 0; ni < nodes_.size(); ++ni)
     for (size_t i = beg[ni]; i < end[ni]; ++i) {
       try {
@@ -1648,6 +1685,15 @@ void Model::validate(const Launch & l) const
   case kResizeNN:
     check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "pool x");
     check(q.y.ptr, 0, vlast(q.y, B, q.C, (long)q.Ho * q.Wo), 2, "pool y");
+    break;
+  case kMaxPoolSppf:
+    if (q.C % 8 || HW > 1024 || q.Ho != q.H || q.Wo != q.W) throw std::runtime_error("SPPF pool geometry");
+    for (const View * v : {&q.a, &q.y, &q.b, &q.c})
+      if (v->layout != kNHWC || v->cs % 8 || v->img % 8) throw std::runtime_error("SPPF pool views");
+    check(q.a.ptr, 0, vlast(q.a, B, q.C, HW), 2, "SPPF pool x");
+    check(q.y.ptr, 0, vlast(q.y, B, q.C, HW), 2, "SPPF pool 5x5");
+    check(q.b.ptr, 0, vlast(q.b, B, q.C, HW), 2, "SPPF pool 9x9");
+    check(q.c.ptr, 0, vlast(q.c, B, q.C, HW), 2, "SPPF pool 13x13");
     break;
   case kSoftmax:
   case kPermute:
@@ -1870,7 +1916,7 @@ std::string Model::nodeKernel(int i)
 {
   const NodeStat & s = stats_.at(i);
   const auto & L = launches(max_batch_);
-  if (node_launch_begin_.at(i) == node_launch_end_.at(i)) return "(view)";
+  if (node_launch_begin_.at(i) == node_launch_end_.at(i)) return node_covered_.at(i) ? "(fused)" : "(view)";
   const Launch & l = L[node_launch_begin_[i]];
   switch (l.kind) {
   case Launch::kIgemm:
@@ -1878,6 +1924,9 @@ std::string Model::nodeKernel(int i)
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";
+  case Launch::kSmall:
+    if (l.small == kMaxPoolSppf) return "maxpool_sppf";
+    return s.kernel;
   default: return s.kernel;
   }
 }

@@ -96,7 +96,9 @@ class Model {
   const std::vector<Launch> & launches(int batch);
   View view(const std::string & name, int batch) const;
   void enqueue(const std::vector<Launch> & L, size_t b, size_t e);
-  void emitNode(size_t ni, int batch, std::vector<Launch> & out);
+  // `covered`: nodes whose work a launch of node ni already does (they emit nothing)
+  void emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vector<char> & covered);
+  bool sppfChain(size_t ni) const;
   void validate(const Launch & l) const;
   void * devAlloc(size_t bytes, bool zero);
   void devUpload(void * d, const void * src, size_t bytes);
@@ -134,6 +136,7 @@ class Model {
   std::map<int, std::vector<Launch>> launch_cache_;
   std::vector<size_t> node_launch_begin_;   // per node: [begin, end) into launches(batch)
   std::vector<size_t> node_launch_end_;
+  std::vector<char> node_covered_;          // node's work done by an earlier node's launch
   std::map<int, hipGraphExec_t> graphs_;
   std::vector<NodeStat> stats_;
   double last_run_ms_ = 0.0;

@@ -92,6 +92,7 @@ struct ConvParams {
 // Generic small-op descriptor (elementwise / pooling / data movement).
 struct SmallParams {
   View a, b, y;
+  View c;                      // a third output (kMaxPoolSppf)
   int batch = 1;
   int C = 0, H = 0, W = 0;     // per-image geometry of the iteration space
   int Ho = 0, Wo = 0;

@@ -76,6 +76,8 @@ enum SmallOp : int {
   kBmm,            // NCHW flat: i0 BB, i1 M, i2 K, i3 N  (a: [BB][M][K], b: [BB][K][N]);
                    // op bit 0: a stored [BB][K][M], bit 1: b stored [BB][N][K]
   kBiasAdd,        // NCHW flat: i0 HW
+  kMaxPoolSppf,    // NHWC, C % 8 == 0, H * W <= 1024: a -> y, b, c = 5x5, 9x9, 13x13 max
+                   // pools (stride 1, clipped windows): three chained 5x5 pad-2 pools
 };
 void launch_small(int kind, const SmallParams & p, hipStream_t s);
 void launch_pose_decode(const DecodeParams & p, hipStream_t s);  // fused head decode

@@ -956,6 +956,56 @@ __global__ void __launch_bounds__(256) maxpool_s1_cols_kernel(const SmallParams 
   }
 }
 
+// SPPF's three chained max pools (5x5, stride 1, pad 2, each reading the previous one's
+// output) from one read of the first input: the chain's outputs are the 5x5, 9x9 and 13x13
+// max pools of that input with windows clipped at the borders (a max over maxima is the max
+// over the union of their windows, and clipping composes the same way).  One work-group per
+// (image, 8 channels): the plane into LDS, row maxima of widths 5 / 9 / 13, then column
+// maxima.  Maxima of fp16 values are fp16 values: packed fp16 max (IEEE maxNum, as fmaxf)
+// gives every output bit for bit as the chained pools compute it.
+__global__ void __launch_bounds__(256) maxpool_sppf3_kernel(const SmallParams q)
+{
+  extern __shared__ h8 pl[];  // 4 planes of H * W pixels: input, row maxima 5 / 9 / 13
+  const int HW = q.H * q.W;
+  const int b = blockIdx.y, c = blockIdx.x * 8;
+  const h8 ninf = (h8)(_Float16)(-__builtin_inff());
+  for (int p = threadIdx.x; p < HW; p += 256) pl[p] = ld8(q.a.ptr, (long)b * q.a.img + (long)p * q.a.cs + c);
+  __syncthreads();
+  for (int p = threadIdx.x; p < HW; p += 256) {
+    const int y = p / q.W, x = p - y * q.W;
+    h8 m5 = ninf, m9 = ninf, m13 = ninf;
+#pragma unroll
+    for (int d = -6; d <= 6; ++d) {
+      const int xx = x + d;
+      if ((unsigned)xx >= (unsigned)q.W) continue;
+      const h8 v = pl[y * q.W + xx];
+      m13 = __builtin_elementwise_max(m13, v);
+      if (d >= -4 && d <= 4) m9 = __builtin_elementwise_max(m9, v);
+      if (d >= -2 && d <= 2) m5 = __builtin_elementwise_max(m5, v);
+    }
+    pl[HW + p] = m5;
+    pl[2 * HW + p] = m9;
+    pl[3 * HW + p] = m13;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < HW; p += 256) {
+    const int y = p / q.W, x = p - y * q.W;
+    h8 m5 = ninf, m9 = ninf, m13 = ninf;
+#pragma unroll
+    for (int d = -6; d <= 6; ++d) {
+      const int yy = y + d;
+      if ((unsigned)yy >= (unsigned)q.H) continue;
+      const int i = yy * q.W + x;
+      m13 = __builtin_elementwise_max(m13, pl[3 * HW + i]);
+      if (d >= -4 && d <= 4) m9 = __builtin_elementwise_max(m9, pl[2 * HW + i]);
+      if (d >= -2 && d <= 2) m5 = __builtin_elementwise_max(m5, pl[HW + i]);
+    }
+    st8(q.y.ptr, (long)b * q.y.img + (long)p * q.y.cs + c, m5);
+    st8(q.b.ptr, (long)b * q.b.img + (long)p * q.b.cs + c, m9);
+    st8(q.c.ptr, (long)b * q.c.img + (long)p * q.c.cs + c, m13);
+  }
+}
+
 // Row copies of `L` contiguous elements (L % 8 == 0): slice_axis, concat along an inner
 // axis, permute mode 0.  kind 0 slice, 1 concat part, 2 permute.
 __global__ void __launch_bounds__(256) rows_vec8_kernel(const SmallParams q, int kind, int L, int rows)
@@ -1206,6 +1256,11 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
 
 void launch_small(int kind, const SmallParams & q, hipStream_t s)
 {
+  if (kind == kMaxPoolSppf) {
+    hipLaunchKernelGGL(maxpool_sppf3_kernel, dim3((unsigned)(q.C / 8), (unsigned)q.batch), dim3(256),
+                       (size_t)4 * q.H * q.W * 16, s, q);
+    return;
+  }
   if (launch_small_vec(kind, q, s)) return;
   const dim3 blk(256);
   const unsigned B = (unsigned)q.batch;

@@ -250,6 +250,13 @@ def _small_plan(d, build):
     return pb.write()
 
 
+def _sppf_pools(pb, x):
+    y = [x]
+    for _ in range(3):
+        y.append(pb.maxpool(y[-1], 5, 1, 2))
+    return pb.concat(y)
+
+
 SMALL = {
     "maxpool5": lambda pb: pb.maxpool(pb.input("x", [1, 24, 13, 17]), 5, 1, 2),
     "maxpool3s2": lambda pb: pb.maxpool(pb.input("x", [1, 8, 15, 15]), 3, 2, 1),
@@ -271,6 +278,9 @@ SMALL = {
     # channels-last pools (between two ReLUs both tensors are internal)
     "maxpool5_nhwc": lambda pb: pb.unary(pb.maxpool(pb.unary(pb.input("x", [1, 24, 13, 17]), 2), 5, 1, 2), 2),
     "maxpool3s2_nhwc": lambda pb: pb.unary(pb.maxpool(pb.unary(pb.input("x", [1, 16, 15, 15]), 2), 3, 2, 1), 2),
+    # SPPF: three chained 5x5 pools into a channel concat, one fused launch (odd 13x19 map:
+    # windows clipped on every side)
+    "sppf3": lambda pb: pb.unary(_sppf_pools(pb, pb.unary(pb.input("x", [1, 24, 13, 19]), 2)), 2),
     "ew_mul_stride": lambda pb: pb.binary(pb.input("x", [1, 4, 30]), pb.const(np.linspace(1, 3, 30).reshape(1, 30), "k"), 2),
     "ew_div_scalar": lambda pb: pb.binary(pb.input("x", [1, 3, 9, 9]), pb.const(np.array([2.0]), "k"), 3),
     "ew_sub_same": lambda pb: pb.binary(pb.const(np.linspace(0, 5, 2 * 33).reshape(1, 2, 33), "k"), pb.input("x", [1, 2, 33]), 1),
@@ -283,12 +293,14 @@ SMALL = {
 
 
 EXACT = {"maxpool5", "maxpool3s2", "maxpool5_nhwc", "maxpool3s2_nhwc", "resize2", "permute0213", "permute0132", "slice_axis2",
-         "concat_ch", "concat_axis2"}
+         "concat_ch", "concat_axis2", "sppf3"}
 
 
 @pytest.mark.parametrize("name", sorted(SMALL))
 def test_small_ops(tmp_path, name):
     path = _small_plan(tmp_path, SMALL[name])
+    if name == "sppf3":
+        assert _kernels(path, 3).count("maxpool_sppf") == 1
     p, x, got = _run(path, 3, lo=-3.0, hi=3.0)
     ref = O.run_plan(p, x, 3)[0].ravel()
     g = got[0]
