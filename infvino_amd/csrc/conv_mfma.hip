@@ -34,8 +34,8 @@ namespace ivh {
 // register stages, so a work-group with a short K loop has its whole K range in flight at
 // once instead of waiting one memory latency per step.  RAG: Cin is not a multiple of 8
 // (the compile-time switch keeps the masking out of the common case).
-template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG>
-__global__ void __launch_bounds__(256) conv_igemm_kernel(const ConvParams p)
+template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG, int OCC = 1>
+__global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p)
 {
   using F = Mf<32>;
   using T = TileShape<32, WGM, WGN, TM, TN>;
@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const ConvParams p, 
 // Tile table: a small CDNA4 choice per op (BN from Cout; BM = 128 pixels).
 int igemm_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
 
-template <int WGM, int WGN, int TM, int TN, int BK, int PF>
+template <int WGM, int WGN, int TM, int TN, int BK, int PF, int OCC = 1>
 static void launch_t(const ConvParams & p, hipStream_t s)
 {
   using T = TileShape<32, WGM, WGN, TM, TN>;
@@ -244,12 +244,19 @@ static void launch_t(const ConvParams & p, hipStream_t s)
   q.dv_wo = fastdiv_make((unsigned)p.Wo);
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
   if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, true>), grid, dim3(256), 0, s, q);
-  else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false>), grid, dim3(256), 0, s, q);
+  else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, OCC>), grid, dim3(256), 0, s, q);
   if (p.ksplit > 1) {
     const long n = M * p.Cout;
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p,
                        (int)grid.y * T::BN);
   }
+}
+
+// Output tiles of a layer (BM = 128 pixels x BN channels) over the batch
+static long igemm_tiles(const ConvParams & p)
+{
+  const int bn = igemm_bn(p.Cout);
+  return ((long)p.batch * p.Ho * p.Wo + 127) / 128 * ((p.Cout + bn - 1) / bn);
 }
 
 // Register prefetch depth (K steps in flight) per tile width (measured on MI355X over
@@ -261,7 +268,18 @@ static void launch_bk(const ConvParams & p, hipStream_t s)
   switch (igemm_bn(p.Cout)) {
   case 32: launch_t<4, 1, 1, 1, BK, PF32>(p, s); break;
   case 64: launch_t<2, 2, 2, 1, BK, PF64>(p, s); break;
-  default: launch_t<2, 2, 2, 2, BK, PF128>(p, s); break;
+  default:
+    // 1x1 convs whose tiles overflow three resident work-groups per CU (at 144 VGPRs) but
+    // fit four: the 128-VGPR build of the same tile (40x40 maps at batch 64, 800 tiles:
+    // 22-34 -> 20-30 us).  3x3 convs lose more to the register cap than they gain (measured).
+    if constexpr (BK == 32) {
+      if (p.K == 1 && !(p.Cin & 7) && p.ksplit == 1 && igemm_tiles(p) > 3 * 256 && igemm_tiles(p) <= 4 * 256) {
+        launch_t<2, 2, 2, 2, BK, PF128, 4>(p, s);
+        break;
+      }
+    }
+    launch_t<2, 2, 2, 2, BK, PF128>(p, s);
+    break;
   }
 }
 
