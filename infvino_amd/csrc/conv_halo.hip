@@ -244,10 +244,11 @@ namespace {
 struct HaloCfgDesc {
   int bm, bn, pmax;
 };
-// configs: 0..3 BM 256 (BN 16/32/64/128), 4..7 BM 128 (BN 16/32/64/128)
-constexpr HaloCfgDesc kHaloCfg[8] = {
+// configs: 0..3 BM 256 (BN 16/32/64/128), 4..7 BM 128 (BN 16/32/64/128), 8 BM 64 BN 64
+constexpr HaloCfgDesc kHaloCfg[kHaloCfgs] = {
     {256, 16, 360}, {256, 32, 360}, {256, 64, 360}, {256, 128, 360},
     {128, 16, 216}, {128, 32, 216}, {128, 64, 216}, {128, 128, 216},
+    {64, 64, 144},
 };
 }  // namespace
 
@@ -307,6 +308,14 @@ bool halo_plan(int cin, int cout, int H, int W, int batch, int * cfg, int * th, 
   *cfg = c;
   *th = c == big ? hb : hs;
   *tw = c == big ? tb : ts;
+  // a grid of fewer work-groups than CUs (wide layers on small maps): BM 64 x BN 64 tiles
+  long wq = 0;
+  int hq = 0, tq = 0;
+  if (cout > 32 && (c == big ? wb : ws) < 256 && halo_tile(8, cout, H, W, batch, &wq, &hq, &tq)) {
+    *cfg = 8;
+    *th = hq;
+    *tw = tq;
+  }
   return true;
 }
 
@@ -345,7 +354,8 @@ void launch_conv_halo(const ConvParams & p, hipStream_t s)
   case 4: launch_hc<16, 4, 1, 2, 1, 216>(p, s); break;
   case 5: launch_hc<32, 4, 1, 1, 1, 216>(p, s); break;
   case 6: launch_hc<32, 2, 2, 2, 1, 216>(p, s); break;
-  default: launch_hc<32, 2, 2, 2, 2, 216>(p, s); break;
+  case 7: launch_hc<32, 2, 2, 2, 2, 216>(p, s); break;
+  default: launch_hc<32, 2, 2, 1, 1, 144>(p, s); break;
   }
 }
 

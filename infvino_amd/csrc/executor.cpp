@@ -1583,10 +1583,10 @@ void Model::validate(const Launch & l) const
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
       if (p.halo) {
         const int cfg = p.halo - 1, ck = p.ck;
-        if (cfg < 0 || cfg > 7 || ck != halo_cfg_ck(cfg, p.Cin)) throw std::runtime_error("halo chunk size");
-        if (p.K != 3 || p.S != 1 || p.P != 1 || p.ksplit != 1 || cfg < 0 || cfg > 7 || p.th < 1 || p.tw < 1 ||
+        if (cfg < 0 || cfg >= kHaloCfgs || ck != halo_cfg_ck(cfg, p.Cin)) throw std::runtime_error("halo chunk size");
+        if (p.K != 3 || p.S != 1 || p.P != 1 || p.ksplit != 1 || cfg >= kHaloCfgs || p.th < 1 || p.tw < 1 ||
             p.Ho != p.H || p.Wo != p.W || (p.th + 2) * (p.tw + 2) > halo_pmax(cfg) || p.th + 2 > kHaloMaxRows ||
-            p.th * p.tw > (cfg < 4 ? 256 : 128) || (p.Cout + halo_bn(cfg) - 1) / halo_bn(cfg) * halo_bn(cfg) > rows)
+            p.th * p.tw > (cfg < 4 ? 256 : cfg < 8 ? 128 : 64) || (p.Cout + halo_bn(cfg) - 1) / halo_bn(cfg) * halo_bn(cfg) > rows)
           throw std::runtime_error("halo geometry");
         if (p.kpad != (p.Cin + ck - 1) / ck * halo_taps(ck) * ck) throw std::runtime_error("halo weight packing");
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("halo geometry too large");

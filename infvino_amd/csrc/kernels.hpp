@@ -18,6 +18,7 @@ ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb);  // images [b
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
 
 // conv_halo.hip: 3x3 stride-1 pad-1 convs with an LDS input patch
+constexpr int kHaloCfgs = 9;         // tile configs of the LDS-patch kernel
 int halo_cfg_ck(int cfg, int cin);  // input-channel chunk a tile config uses (16 / 32 / 64)
 int halo_taps(int ck);               // taps per chunk in the packing (9, or 10 with a zero tap)
 // tile config (cfg) and output tile th x tw for a layer at a batch size; false: not eligible
