@@ -86,6 +86,7 @@ ConvPacking conv_packing(const ConvSpec & s)
     pk.w = seg(((size_t)s.G * cin_g * s.K * s.K * (s.Cout / s.G) + 32) * 4);
   } else {
     pk.w = seg(((size_t)s.K * s.K * s.Cout + 8) * 4);
+    pk.dw_w16 = seg(((size_t)s.K * s.K * s.Cout + 8) * 2);
   }
   pk.bytes = off;
   return pk;
@@ -135,8 +136,12 @@ void conv_pack(const ConvSpec & s, const ConvPacking & pk, const uint16_t * W, c
     }
   } else {
     float * P = reinterpret_cast<float *>(blob.data() + pk.w);
+    uint16_t * P16 = reinterpret_cast<uint16_t *>(blob.data() + pk.dw_w16);
     for (int c = 0; c < Cout; ++c)
-      for (int t = 0; t < K * K; ++t) P[(size_t)t * Cout + c] = h2f_bits(W[(size_t)c * K * K + t]);
+      for (int t = 0; t < K * K; ++t) {
+        P[(size_t)t * Cout + c] = h2f_bits(W[(size_t)c * K * K + t]);
+        P16[(size_t)t * Cout + c] = W[(size_t)c * K * K + t];
+      }
   }
 }
 
@@ -146,7 +151,10 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   const char * base = static_cast<const char *>(dev_blob);
   p.bias = pk.bias != kNoSeg ? reinterpret_cast<const float *>(base + pk.bias) : nullptr;
   p.w = reinterpret_cast<const __half *>(base + pk.w);
-  if (pk.family == kFamDw) return kLaunchDw;
+  if (pk.family == kFamDw) {
+    p.w2 = reinterpret_cast<const __half *>(base + pk.dw_w16);
+    return kLaunchDw;
+  }
   if (pk.family == kFamDirect) {
     p.stem_mfma = pk.stem ? 1 : 0;
     if (pk.stem && pk.stem_w2 != kNoSeg) p.w2 = reinterpret_cast<const __half *>(base + pk.stem_w2);

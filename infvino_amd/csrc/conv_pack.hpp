@@ -41,6 +41,7 @@ struct ConvPacking {
   int kpad_halo[3] = {0, 0, 0};
   bool stem = false;                 // Cin <= 3 3x3: fp16 [ceil(Cout/16)*16][32] ...
   size_t stem_w2 = kNoSeg;           // ... then (Cout <= 16) fp16 [16][64], k = tap*4 + ci
+  size_t dw_w16 = kNoSeg;            // depthwise: the same [K][K][C] weights as fp16
   size_t bytes = 0;
 };
 

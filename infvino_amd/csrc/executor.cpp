@@ -1636,6 +1636,7 @@ void Model::validate(const Launch & l) const
     } else {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "dw x");
       check(p.w, 0, (long)p.K * p.K * p.Cin - 1, 4, "dw w");
+      check(p.w2, 0, (long)p.K * p.K * p.Cin - 1, 2, "dw w16");
     }
     return;
   }

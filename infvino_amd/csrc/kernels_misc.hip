@@ -420,8 +420,9 @@ void launch_conv_direct(const ConvParams & p, hipStream_t s)
 // ------------------------------------------------------------------- depthwise
 // Restates depthwise_f16 / depthwise_v / depthwise_blk (kernels/conv_general.cl:85-187,
 // depthwise_blk.cl:118-228): y[c] = act(sum_k x[c]*w[c] + b[c]), K in {3,5}, S in {1,2}.
-// NHWC vector path: one lane = one output pixel x 8 channels, 16-byte loads/stores,
-// fp32 accumulation.  Weights packed fp32 [K][K][C].
+// NHWC vector path: one lane = a strip of output pixels x 8 channels, 16-byte loads/stores,
+// fp32 accumulation.  Weights [K][K][C] as fp16 (the plan's values; one 16-byte load per tap
+// for 8 channels) for this kernel, as fp32 for the any-layout one.
 template <int K, int S, int PX, int ACT>
 __global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p, FastDiv d_c8, FastDiv d_strip, FastDiv d_ho)
 {
@@ -435,7 +436,7 @@ __global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p, FastDi
   const int c8 = (int)(idx - q * C8), strip = (int)(q - rowi * nstrip), oy = (int)(rowi - b * p.Ho);
   const int c = c8 * 8, ox0 = strip * PX, ix0 = ox0 * S - p.P;
   const _Float16 * xb = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img + c;
-  const float * W = reinterpret_cast<const float *>(p.w) + c;
+  const _Float16 * W = reinterpret_cast<const _Float16 *>(p.w2) + c;
   float acc[PX][8];
 #pragma unroll
   for (int j = 0; j < PX; ++j)
@@ -454,15 +455,12 @@ __global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p, FastDi
     }
 #pragma unroll
     for (int kx = 0; kx < K; ++kx) {
-      const float4 w0 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin);
-      const float4 w1 = *reinterpret_cast<const float4 *>(W + (ky * K + kx) * p.Cin + 4);
+      const h8 wv = *reinterpret_cast<const h8 *>(W + (ky * K + kx) * p.Cin);
 #pragma unroll
       for (int j = 0; j < PX; ++j) {
         const h8 v = xv[j * S + kx];
-        acc[j][0] += (float)v[0] * w0.x; acc[j][1] += (float)v[1] * w0.y;
-        acc[j][2] += (float)v[2] * w0.z; acc[j][3] += (float)v[3] * w0.w;
-        acc[j][4] += (float)v[4] * w1.x; acc[j][5] += (float)v[5] * w1.y;
-        acc[j][6] += (float)v[6] * w1.z; acc[j][7] += (float)v[7] * w1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] += (float)v[e] * (float)wv[e];
       }
     }
   }
@@ -522,7 +520,8 @@ bool dwconv_vectorizable(const ConvParams & p)
   auto al = [](const View & v) {
     return v.layout == kNHWC && ((v.cs | (int)v.img | (int)(reinterpret_cast<uintptr_t>(v.ptr) >> 1)) & 7) == 0;
   };
-  return (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2) && al(p.x) && al(p.y) &&
+  return p.w2 && (reinterpret_cast<uintptr_t>(p.w2) & 15) == 0 && (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) &&
+         (p.S == 1 || p.S == 2) && al(p.x) && al(p.y) &&
          (!p.r.ptr || al(p.r)) && (long)p.batch * p.Ho * p.Wo * (p.Cin / 8) < (1L << 31);
 }
 
