@@ -25,6 +25,10 @@
  *   ivh_profile_nodes     PlanModel::profile() per-node GPU time, PlanModel.hpp:201-224
  *   ivh_node_info         PlanModel::PlanProfile::NodeRow (op, tag, signature), PlanModel.hpp:203-211
  *   ivh_device_info       ClBackend::device() / describeDevice, ClBackend.hpp:46, include/infvino/Device.hpp
+ *   ivh_runtime_version   DeviceInfo::opencl_version, include/infvino/Device.hpp:23
+ *   ivh_node_times        PlanModel::profile() / opProfile() accumulated under profiling=true,
+ *                         PlanModel.hpp:176-224; src/PlanModel.cpp:3183-3196
+ *   ivh_clear_profile     PlanModel::clearProfile, PlanModel.hpp:226-233
  * The batch argument is new: the reference runs one image per call (src/PlanModel.cpp:3561-3564
  * read C,H,W from the last three dims).  Here a call processes `batch` images stored back to
  * back (image stride = the plan's per-image numel); batch == 1 is the reference behaviour.
@@ -60,6 +64,9 @@ extern "C" {
                                           one fused kernel */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
+#define IVH_FLAG_PROFILE 0x800u   /* PlanModel's profiling=true: every run launches node by node
+                                     with a HIP event between nodes, waits, and adds each node's
+                                     time to the totals ivh_node_times reports (no graph) */
 
 typedef struct ivh_model ivh_model;
 
@@ -68,6 +75,9 @@ int ivh_version(int * major, int * minor);
 int ivh_device_count(int * n);
 /* name / compute units / peak clock of a device (ClBackend::device(), src/Device.cpp) */
 int ivh_device_info(int device, char * name, size_t name_len, int * compute_units, int * clock_mhz);
+/* "HIP <runtime version>, driver <driver version>": the runtime string DeviceInfo carries in
+   the reference's opencl_version slot (include/infvino/Device.hpp:16-26) */
+int ivh_runtime_version(char * buf, size_t len);
 
 int ivh_create(const char * plan_path, int device, int max_batch, uint32_t flags, ivh_model ** out);
 int ivh_destroy(ivh_model * m);
@@ -96,6 +106,11 @@ int ivh_last_run_ms(const ivh_model * m, double * ms);
    HIP events on the model stream, mean per run; a full pass afterwards restores all tensors */
 int ivh_node_count(ivh_model * m, int * n);
 int ivh_profile_nodes(ivh_model * m, int batch, int iters, double * ms, int cap);
+/* totals over the runs of an IVH_FLAG_PROFILE model since creation or ivh_clear_profile:
+   per node the summed device time (ms) and the number of runs that launched it
+   (PlanModel::profile().nodes / opProfile() accumulate the same way, PlanModel.hpp:176-234) */
+int ivh_node_times(const ivh_model * m, double * ms, int * calls, int cap);
+int ivh_clear_profile(ivh_model * m);  /* PlanModel::clearProfile, PlanModel.hpp:226-233 */
 /* node i: op, kernel family and shape text; algorithmic FLOPs and fp16 bytes per image */
 int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel, size_t kernel_len,
                   char * desc, size_t desc_len, double * flops, double * bytes);

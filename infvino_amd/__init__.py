@@ -33,6 +33,7 @@ IVH_FLAG_NO_SPLITK = 0x80
 IVH_FLAG_NO_HALO = 0x100
 IVH_FLAG_NO_RESIDENT = 0x200
 IVH_FLAG_NO_FUSE_DECODE = 0x400
+IVH_FLAG_PROFILE = 0x800
 
 # every symbol include/ivh.h declares, with (restype, argtypes)
 _vp, _i, _u32, _sz, _d = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_double
@@ -50,6 +51,7 @@ SIGNATURES = {
     "ivh_version": (_i, [_ip, _ip]),
     "ivh_device_count": (_i, [_ip]),
     "ivh_device_info": (_i, [_i, C.c_char_p, _sz, _ip, _ip]),
+    "ivh_runtime_version": (_i, [C.c_char_p, _sz]),
     "ivh_create": (_i, [C.c_char_p, _i, _i, _u32, C.POINTER(_vp)]),
     "ivh_destroy": (_i, [_vp]),
     "ivh_input_dims": (_i, [_vp, _i64p, _ip]),
@@ -69,6 +71,8 @@ SIGNATURES = {
     "ivh_last_run_ms": (_i, [_vp, _dp]),
     "ivh_node_count": (_i, [_vp, _ip]),
     "ivh_profile_nodes": (_i, [_vp, _i, _i, _dp, _i]),
+    "ivh_node_times": (_i, [_vp, _dp, _ip, _i]),
+    "ivh_clear_profile": (_i, [_vp]),
     "ivh_node_info": (_i, [_vp, _i, C.c_char_p, _sz, C.c_char_p, _sz, C.c_char_p, _sz, _dp, _dp]),
     "ivh_memory_info": (_i, [_vp, _i, _szp, _szp]),
     # single-op entry points (device pointers as integers, stream None = null stream)

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <stdexcept>
@@ -191,6 +192,20 @@ int ivh_device_info(int device, char * name, size_t name_len, int * compute_unit
   });
 }
 
+int ivh_runtime_version(char * buf, size_t len)
+{
+  return guard([&] {
+    if (!buf || len == 0) throw std::invalid_argument("null buffer");
+    int rt = 0, drv = 0;
+    if (hipRuntimeGetVersion(&rt) != hipSuccess || hipDriverGetVersion(&drv) != hipSuccess)
+      throw std::runtime_error("HIP error: no HIP runtime / driver version");
+    // HIP_VERSION encoding: major * 10^7 + minor * 10^5 + patch
+    const std::string v = "HIP " + std::to_string(rt / 10000000) + "." + std::to_string(rt / 100000 % 100) + "." +
+                          std::to_string(rt % 100000) + ", driver " + std::to_string(drv);
+    std::snprintf(buf, len, "%s", v.c_str());
+  });
+}
+
 int ivh_create(const char * plan_path, int device, int max_batch, uint32_t flags, ivh_model ** out)
 {
   return guard([&] {
@@ -312,6 +327,25 @@ int ivh_profile_nodes(ivh_model * m, int batch, int iters, double * ms, int cap)
     for (size_t i = 0; i < v.size(); ++i) ms[i] = v[i];
   });
 }
+int ivh_node_times(const ivh_model * m, double * ms, int * calls, int cap)
+{
+  return guard([&] {
+    std::vector<double> t;
+    std::vector<int> c;
+    M(m).nodeTimes(t, c);
+    if (cap < (int)t.size()) throw std::invalid_argument("node_times capacity too small");
+    for (size_t i = 0; i < t.size(); ++i) {
+      if (ms) ms[i] = t[i];
+      if (calls) calls[i] = c[i];
+    }
+  });
+}
+
+int ivh_clear_profile(ivh_model * m)
+{
+  return guard([&] { M(m).clearProfile(); });
+}
+
 int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel, size_t kernel_len, char * desc,
                   size_t desc_len, double * flops, double * bytes)
 {

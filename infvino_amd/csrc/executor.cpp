@@ -168,6 +168,7 @@ Model::~Model()
   (void)hipSetDevice(device_);
   if (stream_) (void)hipStreamSynchronize(stream_);
   for (auto & g : graphs_) (void)hipGraphExecDestroy(g.second);
+  for (auto & e : prof_ev_) (void)hipEventDestroy(e);
   for (const auto & a : allocs_) (void)hipFree(reinterpret_cast<void *>(a.first));
   if (stream_) (void)hipStreamDestroy(stream_);
 }
@@ -943,6 +944,20 @@ void Model::allocate()
     }
   }
   for (const auto & o : outputs_) roots_[T_[o]->root]->last = N + 1;
+  // SPPF's three chained pools may run as one launch at node ni (emitNode): it reads x and
+  // writes y1, y2 and y3 together, so all four must be live over [ni, ni + 2] and none may
+  // take another's bytes.  The chain is a structural property of the plan; whether the
+  // launch fuses also depends on alignment, and the wider intervals are harmless if not.
+  for (int ni = 0; ni + 2 < N; ++ni) {
+    if (!sppfChain((size_t)ni)) continue;
+    for (const std::string * t : {&nodes_[ni].ins[0], &nodes_[ni].outs[0], &nodes_[ni + 1].outs[0], &nodes_[ni + 2].outs[0]}) {
+      const Tensor & tt = *T_[*t];
+      if (tt.root < 0 || tt.kind == Tensor::kInit) continue;
+      Root & r = *roots_[tt.root];
+      r.first = std::min(r.first, ni);
+      r.last = std::max(r.last, ni + 2);
+    }
+  }
   // best-fit placement, largest first, on closed [first, last] intervals
   std::vector<int> order;
   for (size_t i = 0; i < roots_.size(); ++i) {
@@ -975,10 +990,36 @@ void Model::allocate()
     placed.push_back(id);
   }
   arena_elems1_ = total;
+  verifyArena();
   arena_ = devAlloc((size_t)std::max<long>(total, 64) * max_batch_ * 2, true);
   const Tensor & in = *T_[input_name_];
   const long in_img = roots_[in.root]->per_image;
   input_buf_ = devAlloc((size_t)in_img * max_batch_ * 2, true);
+}
+
+// The memory plan's invariant (the reference checks the same for its pool,
+// src/PlanModel.cpp:1083-1101): two arena roots whose closed live intervals intersect
+// occupy disjoint [off1, off1 + per_image) ranges, and every root lies inside the arena.
+void Model::verifyArena() const
+{
+  std::vector<int> placed;
+  for (size_t i = 0; i < roots_.size(); ++i) {
+    const Root & r = *roots_[i];
+    if (r.parent >= 0 || r.is_input || r.first == INT_MAX) continue;
+    if (r.off1 < 0 || r.off1 + r.per_image > arena_elems1_)
+      throw std::runtime_error("activation arena: root " + std::to_string(i) + " outside the arena");
+    placed.push_back((int)i);
+  }
+  for (size_t a = 0; a < placed.size(); ++a)
+    for (size_t b = a + 1; b < placed.size(); ++b) {
+      const Root & p = *roots_[placed[a]];
+      const Root & q = *roots_[placed[b]];
+      const bool live = !(p.last < q.first || q.last < p.first);
+      const bool share = p.off1 < q.off1 + q.per_image && q.off1 < p.off1 + p.per_image;
+      if (live && share && p.per_image > 0 && q.per_image > 0)
+        throw std::runtime_error("activation arena: roots " + std::to_string(placed[a]) + " and " +
+                                 std::to_string(placed[b]) + " are live together and share memory");
+    }
 }
 
 void Model::uploadWeights()
@@ -1500,30 +1541,28 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
   throw std::runtime_error("PlanModel: unknown op: " + op);
 }
 
-const std::vector<Launch> & Model::launches(int batch)
+const Model::LaunchPlan & Model::launches(int batch)
 {
   auto it = launch_cache_.find(batch);
   if (it != launch_cache_.end()) return it->second;
-  std::vector<Launch> L;
-  std::vector<size_t> beg(nodes_.size()), end(nodes_.size());
-  std::vector<char> covered(nodes_.size(), 0);
+  LaunchPlan P;
+  P.begin.assign(nodes_.size(), 0);
+  P.end.assign(nodes_.size(), 0);
+  P.covered.assign(nodes_.size(), 0);
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
-    beg[ni] = L.size();
-    if (!skip_[ni] && !covered[ni]) emitNode(ni, batch, L, covered);
-    end[ni] = L.size();
+    P.begin[ni] = P.L.size();
+    if (!skip_[ni] && !P.covered[ni]) emitNode(ni, batch, P.L, P.covered);
+    P.end[ni] = P.L.size();
   }
-  node_launch_begin_ = beg;
-  node_launch_end_ = end;
-  node_covered_ = covered;
   for (size_t ni = 0; ni < nodes_.size(); ++ni)
-    for (size_t i = beg[ni]; i < end[ni]; ++i) {
+    for (size_t i = P.begin[ni]; i < P.end[ni]; ++i) {
       try {
-        validate(L[i]);
+        validate(P.L[i]);
       } catch (const std::exception & e) {
         throw std::runtime_error("node " + nodes_[ni].op + " -> " + nodes_[ni].outs[0] + ": " + e.what());
       }
     }
-  return launch_cache_[batch] = std::move(L);
+  return launch_cache_[batch] = std::move(P);
 }
 
 // Host-side bounds check of one launch: every element a kernel may touch (including the
@@ -1789,8 +1828,11 @@ void Model::run(int batch)
   if (dry_) { dryRun(batch); return; }
   HIPCHECK(hipSetDevice(device_));
   const auto t0 = std::chrono::steady_clock::now();
-  const auto & L = launches(batch);
-  if (flags_ & IVH_FLAG_NO_GRAPH) {
+  const LaunchPlan & P = launches(batch);
+  const auto & L = P.L;
+  if (flags_ & IVH_FLAG_PROFILE) {
+    runProfiled(P);
+  } else if (flags_ & IVH_FLAG_NO_GRAPH) {
     enqueue(L, 0, L.size());
   } else {
     auto it = graphs_.find(batch);
@@ -1812,10 +1854,52 @@ void Model::run(int batch)
     }
     HIPCHECK(hipGraphLaunch(it->second, stream_));
   }
-  if (!(flags_ & IVH_FLAG_ASYNC)) {
+  if (!(flags_ & IVH_FLAG_ASYNC) || (flags_ & IVH_FLAG_PROFILE)) {
     HIPCHECK(hipStreamSynchronize(stream_));
     last_run_ms_ = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   }
+  if (flags_ & IVH_FLAG_PROFILE) {
+    // the run is complete: add each node's time between its two events
+    for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+      if (P.begin[ni] == P.end[ni]) continue;
+      float t = 0;
+      HIPCHECK(hipEventElapsedTime(&t, prof_ev_[ni], prof_ev_[ni + 1]));
+      prof_ms_[ni] += t;
+      prof_calls_[ni] += 1;
+    }
+  }
+}
+
+// One run node by node, a HIP event recorded before the first node and after every node
+// (the reference's profiling runs time every kernel with its own event,
+// src/PlanModel.cpp:3166-3205).
+void Model::runProfiled(const LaunchPlan & P)
+{
+  if (prof_ev_.empty()) {
+    prof_ev_.assign(nodes_.size() + 1, nullptr);
+    for (auto & e : prof_ev_) HIPCHECK(hipEventCreate(&e));
+    prof_ms_.assign(nodes_.size(), 0.0);
+    prof_calls_.assign(nodes_.size(), 0);
+  }
+  HIPCHECK(hipEventRecord(prof_ev_[0], stream_));
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    enqueue(P.L, P.begin[ni], P.end[ni]);
+    HIPCHECK(hipEventRecord(prof_ev_[ni + 1], stream_));
+  }
+}
+
+void Model::nodeTimes(std::vector<double> & ms, std::vector<int> & calls) const
+{
+  ms = prof_ms_;
+  calls = prof_calls_;
+  ms.resize(nodes_.size(), 0.0);
+  calls.resize(nodes_.size(), 0);
+}
+
+void Model::clearProfile()
+{
+  std::fill(prof_ms_.begin(), prof_ms_.end(), 0.0);
+  std::fill(prof_calls_.begin(), prof_calls_.end(), 0);
 }
 
 void Model::sync()
@@ -1887,7 +1971,8 @@ std::vector<double> Model::profileNodes(int batch, int iters)
 {
   check_batch(batch, max_batch_);
   HIPCHECK(hipSetDevice(device_));
-  const auto & L = launches(batch);
+  const LaunchPlan & P = launches(batch);
+  const auto & L = P.L;
   iters = std::max(iters, 1);
   std::vector<double> ms(nodes_.size(), 0.0);
   std::vector<hipEvent_t> ev(2 * nodes_.size());
@@ -1899,7 +1984,7 @@ std::vector<double> Model::profileNodes(int batch, int iters)
   enqueue(L, 0, L.size());
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     HIPCHECK(hipEventRecord(ev[2 * ni], stream_));
-    for (int it = 0; it < iters; ++it) enqueue(L, node_launch_begin_[ni], node_launch_end_[ni]);
+    for (int it = 0; it < iters; ++it) enqueue(L, P.begin[ni], P.end[ni]);
     HIPCHECK(hipEventRecord(ev[2 * ni + 1], stream_));
   }
   enqueue(L, 0, L.size());
@@ -1907,7 +1992,7 @@ std::vector<double> Model::profileNodes(int batch, int iters)
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     float t = 0;
     HIPCHECK(hipEventElapsedTime(&t, ev[2 * ni], ev[2 * ni + 1]));
-    ms[ni] = node_launch_begin_[ni] == node_launch_end_[ni] ? 0.0 : t / iters;
+    ms[ni] = P.begin[ni] == P.end[ni] ? 0.0 : t / iters;
   }
   for (auto & e : ev) (void)hipEventDestroy(e);
   return ms;
@@ -1916,9 +2001,9 @@ std::vector<double> Model::profileNodes(int batch, int iters)
 std::string Model::nodeKernel(int i)
 {
   const NodeStat & s = stats_.at(i);
-  const auto & L = launches(max_batch_);
-  if (node_launch_begin_.at(i) == node_launch_end_.at(i)) return node_covered_.at(i) ? "(fused)" : "(view)";
-  const Launch & l = L[node_launch_begin_[i]];
+  const LaunchPlan & P = launches(max_batch_);
+  if (P.begin.at(i) == P.end.at(i)) return P.covered.at(i) ? "(fused)" : "(view)";
+  const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
   case Launch::kIgemm:
     return l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));

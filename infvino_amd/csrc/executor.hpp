@@ -71,6 +71,10 @@ class Model {
   // Per-node device time (ms, averaged over iters) measured with HIP events on the
   // model's stream around each node's launches.
   std::vector<double> profileNodes(int batch, int iters);
+  // Time and run count accumulated per node over the runs of a model created with
+  // IVH_FLAG_PROFILE (each run launches node by node with HIP events between nodes).
+  void nodeTimes(std::vector<double> & ms, std::vector<int> & calls) const;
+  void clearProfile();
   int nodeCount() const { return (int)nodes_.size(); }
   const NodeStat & nodeStat(int i) const { return stats_.at(i); }
   // kernel family node i launches at the largest batch (conv_halo / conv_igemm / conv_stem ...)
@@ -81,6 +85,7 @@ class Model {
  private:
   struct Tensor;
   struct Root;
+  struct LaunchPlan;
   void parse(const std::string & path);
   void fuseDecode();
   void fuseResidual();
@@ -93,7 +98,10 @@ class Model {
   void allocate();
   void uploadWeights();
   void buildStats();
-  const std::vector<Launch> & launches(int batch);
+  const LaunchPlan & launches(int batch);
+  void runProfiled(const LaunchPlan & P);
+  // throws when two roots whose closed live intervals intersect share arena bytes
+  void verifyArena() const;
   View view(const std::string & name, int batch) const;
   void enqueue(const std::vector<Launch> & L, size_t b, size_t e);
   // `covered`: nodes whose work a launch of node ni already does (they emit nothing)
@@ -133,10 +141,19 @@ class Model {
   float * ws_ = nullptr;                    // split-K partials
   size_t ws_floats_ = 0;
 
-  std::map<int, std::vector<Launch>> launch_cache_;
-  std::vector<size_t> node_launch_begin_;   // per node: [begin, end) into launches(batch)
-  std::vector<size_t> node_launch_end_;
-  std::vector<char> node_covered_;          // node's work done by an earlier node's launch
+  // The resolved launches of one batch size and, per node, its [begin, end) range in them.
+  // Kept together per batch: launch counts can differ between batch sizes (a fusion that
+  // needs 16-byte aligned views may hold at one batch and not at another).
+  struct LaunchPlan {
+    std::vector<Launch> L;
+    std::vector<size_t> begin, end;
+    std::vector<char> covered;              // node's work done by an earlier node's launch
+  };
+  std::map<int, LaunchPlan> launch_cache_;
+  // accumulated per-node device time of IVH_FLAG_PROFILE runs (PlanModel::profile())
+  std::vector<double> prof_ms_;
+  std::vector<int> prof_calls_;
+  std::vector<hipEvent_t> prof_ev_;
   std::map<int, hipGraphExec_t> graphs_;
   std::vector<NodeStat> stats_;
   double last_run_ms_ = 0.0;

@@ -225,3 +225,44 @@ def test_py_backend_image_slicing():
         HipBackend.image([a], 3, 3)
     with pytest.raises(RuntimeError):
         HipBackend.image([c], 0, 2)
+
+
+def pool_chain_plan(d, C=16, H=20):
+    """Three chained 5x5 stride-1 max pools with no concat after them: pool i reads only the
+    previous pool's output, so each intermediate dies one node after it is born."""
+    pb = pw.PlanBuilder(d, seed=0)
+    x = pb.input("x", [1, C, H, H])
+    a = pb.conv(x, C, 1)
+    b = pb.maxpool(a, 5, 1, 2)
+    c = pb.maxpool(b, 5, 1, 2)
+    e = pb.maxpool(c, 5, 1, 2)
+    pb.output(pb.conv(e, C, 1))
+    return pb.write()
+
+
+def test_sppf_chain_lifetimes(tmp_path):
+    """The fused SPPF launch reads the chain input and writes all three pool outputs at once,
+    so the memory plan must keep all four apart even where each pool output has a single
+    reader (the chain input dies at the first pool node otherwise and a later pool output
+    would take its bytes).  The arena therefore holds four 20x20x16 channels-last buffers."""
+    m = ia.PlanModel(pool_chain_plan(str(tmp_path)), 0, 2, DRY)
+    m.run(2)
+    kinds = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    assert kinds.count("maxpool_sppf") == 1 and kinds.count("(fused)") == 2, kinds
+    arena, _ = m.memoryInfo(1)
+    assert arena >= 4 * 20 * 20 * 16 * 2, arena
+    m.close()
+
+
+def test_launch_plans_per_batch(plans):
+    """Launch lists and their per-node ranges are kept per batch size: labelling and
+    re-running alternate batch sizes sees each batch's own plan."""
+    m = ia.PlanModel(plans("yolov8n-pose", imgsz=320)[0], 0, 5, DRY)
+    m.run(1)
+    k1 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    m.run(5)
+    m.run(3)
+    m.run(1)
+    k2 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    assert k1 == k2
+    m.close()
