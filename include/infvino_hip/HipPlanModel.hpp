@@ -6,7 +6,8 @@
 //
 // Differences from PlanModel, all additive:
 //   * the constructor takes a device index, a maximum batch and ivh.h flags instead of an
-//     OpenCL kernel directory / platform;
+//     OpenCL kernel directory / platform; `profiling` keeps its meaning: per-node device
+//     times accumulate over run() calls (profile(), opProfile(), clearProfile());
 //   * setInput / run / readOutput / readTensor take a batch count B (default 1): B images
 //     stored back to back, each laid out exactly as the plan's batch-1 tensor.
 // Single-threaded, like PlanModel (PlanModel.hpp:36); HipBackend adds the mutex.
@@ -33,9 +34,11 @@ inline void check(int rc)
 class HipPlanModel
 {
 public:
-  explicit HipPlanModel(const std::string & plan_path, int device = 0, int max_batch = 1, uint32_t flags = 0)
-  : plan_path_(plan_path)
+  explicit HipPlanModel(const std::string & plan_path, int device = 0, int max_batch = 1, uint32_t flags = 0,
+                        bool profiling = false)
+  : plan_path_(plan_path), profiling_(profiling)
   {
+    if (profiling) flags |= IVH_FLAG_PROFILE;
     check(ivh_create(plan_path.c_str(), device, max_batch, flags, &m_));
     input_dims_ = dims([&](int64_t * d, int * r) { return ivh_input_dims(m_, d, r); });
     int n = 0;
@@ -92,19 +95,65 @@ public:
     return ms;
   }
 
+  bool profiling() const { return profiling_; }
+
   struct NodeRow
   {
     int index = 0;
     std::string op, kernel, tag;
     double ms = 0.0, flops = 0.0, bytes = 0.0;
+    int calls = 0;
   };
-  /** Per-node device time (HIP events), the counterpart of PlanModel::profile().nodes. */
-  std::vector<NodeRow> profile(int batch = 1, int iters = 5)
+  /** PlanModel::profile().nodes: per-node device time summed over the run() calls since
+   *  construction or clearProfile() (profiling models only; zeros otherwise), with the
+   *  number of runs that launched the node. */
+  std::vector<NodeRow> profile() const
+  {
+    int n = 0;
+    check(ivh_node_count(m_, &n));
+    std::vector<double> ms(n);
+    std::vector<int> calls(n);
+    check(ivh_node_times(m_, ms.data(), calls.data(), n));
+    std::vector<NodeRow> rows = describeNodes(n);
+    for (int i = 0; i < n; ++i) {
+      rows[i].ms = ms[i];
+      rows[i].calls = calls[i];
+    }
+    return rows;
+  }
+  /** PlanModel::opProfile(): plan op -> {summed ms, summed launches} over profiled runs. */
+  std::map<std::string, std::pair<double, int>> opProfile() const
+  {
+    std::map<std::string, std::pair<double, int>> out;
+    for (const NodeRow & r : profile()) {
+      if (r.calls == 0) continue;
+      auto & e = out[r.op];
+      e.first += r.ms;
+      e.second += r.calls;
+    }
+    return out;
+  }
+  void clearProfile() { check(ivh_clear_profile(m_)); }
+
+  /** Measured on demand: each node `iters` times back to back between two HIP events on the
+   *  model stream (any model), mean ms per run. */
+  std::vector<NodeRow> profile(int batch, int iters = 5)
   {
     int n = 0;
     check(ivh_node_count(m_, &n));
     std::vector<double> ms(n);
     check(ivh_profile_nodes(m_, batch, iters, ms.data(), n));
+    std::vector<NodeRow> rows = describeNodes(n);
+    for (int i = 0; i < n; ++i) {
+      rows[i].ms = ms[i];
+      rows[i].calls = iters;
+    }
+    return rows;
+  }
+
+private:
+  std::vector<NodeRow> describeNodes(int n) const
+  {
     std::vector<NodeRow> rows(n);
     for (int i = 0; i < n; ++i) {
       char op[64], kern[64], desc[256];
@@ -113,12 +162,10 @@ public:
       rows[i].op = op;
       rows[i].kernel = kern;
       rows[i].tag = desc;
-      rows[i].ms = ms[i];
     }
     return rows;
   }
 
-private:
   template <class F>
   static std::vector<int64_t> dims(F f)
   {
@@ -139,6 +186,7 @@ private:
   std::vector<int64_t> input_dims_;
   std::vector<std::vector<int64_t>> output_dims_;
   int max_batch_ = 1;
+  bool profiling_ = false;
 };
 
 }  // namespace infvino_hip

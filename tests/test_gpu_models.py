@@ -278,3 +278,32 @@ def test_read_output_f32_exact_every_half(tmp_path):
     assert np.isnan(f32[nan]).all()
     ref = h[~nan].view(np.float16).astype(np.float32)
     assert np.array_equal(f32[~nan].view(np.uint32), ref.view(np.uint32))
+
+
+def test_profiling_mode_accumulates(tmp_path):
+    """IVH_FLAG_PROFILE (ClBackend / PlanModel profiling=true): every run adds each node's
+    device time; outputs equal those of graph replay; clearProfile resets the totals."""
+    import ctypes as C
+    path, _ = pw.yolov8n_pose(str(tmp_path), seed=0, imgsz=256)
+    p = O.Plan.load(path)
+    x = _inputs(p, 2, 4)
+    ref = ia.PlanModel(path, 0, 2)
+    ref.setInput(x, 2)
+    ref.run(2)
+    want = ref.readOutput(0, 2)
+    ref.close()
+    m = ia.PlanModel(path, 0, 2, ia.IVH_FLAG_PROFILE)
+    m.setInput(x, 2)
+    for _ in range(3):
+        m.run(2)
+    assert np.array_equal(m.readOutput(0, 2), want)
+    n = m.nodeCount()
+    ms, calls = (C.c_double * n)(), (C.c_int * n)()
+    assert ia.lib().ivh_node_times(m._h, ms, calls, n) == 0
+    launching = [i for i in range(n) if m.nodeInfo(i)["kernel"] not in ("(view)", "(fused)")]
+    assert all(calls[i] == 3 and ms[i] > 0 for i in launching)
+    assert all(calls[i] == 0 for i in range(n) if i not in launching)
+    assert ia.lib().ivh_clear_profile(m._h) == 0
+    assert ia.lib().ivh_node_times(m._h, ms, calls, n) == 0
+    assert sum(calls) == 0
+    m.close()

@@ -341,3 +341,13 @@ def test_c2f_zero_copy_concat(tmp_path):
         _, _, alt = _run(path, 2, lo=-1.0, flags=flags)
         mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(alt[0]), O.h2f(base[0]))
         assert mean_rel < F32_MEAN and max_rel < F32_MAX, flags
+
+
+def test_pool_chain_without_concat(tmp_path):
+    """Three chained 5x5 max pools whose outputs each have one reader: the fused SPPF launch
+    reads the chain input while writing all three outputs, which the memory plan keeps
+    apart (a pool output placed over the chain input would corrupt it)."""
+    from tests.test_host import pool_chain_plan
+    path = pool_chain_plan(str(tmp_path))
+    assert _kernels(path, 2).count("maxpool_sppf") == 1
+    _check_f32(path, 2, lo=-1.0, ref_mode=False)

@@ -266,3 +266,57 @@ def test_launch_plans_per_batch(plans):
     k2 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
     assert k1 == k2
     m.close()
+
+
+REF_INCLUDE = "/root/reference/include"
+
+
+@pytest.mark.skipif(not os.path.isdir(os.path.join(REF_INCLUDE, "infvino")), reason="reference headers absent")
+def test_cpp_backend_binds_reference_types(tmp_path):
+    """Built inside the reference tree (INFVINO_HIP_USE_INFVINO_TENSOR), HipBackend returns the
+    reference's own infvino::Tensor and infvino::DeviceInfo (include/infvino/Tensor.hpp,
+    Device.hpp), takes ClBackend's (ModelInfo, bool profiling) constructor, and serves the
+    calls InferenceEngine (InferenceEngine.hpp:60), infvino_bench.cpp:89-97 and
+    infvino_numtest.cpp:84-98 make on a ClBackend.  Compiled and linked against the library;
+    nothing runs on a device."""
+    import subprocess
+    src = tmp_path / "bind.cpp"
+    src.write_text(r'''
+#include <cstdio>
+#include <memory>
+#include "infvino_hip/HipBackend.hpp"
+#include "infvino/Device.hpp"
+#include "infvino/Tensor.hpp"
+struct ModelInfo { std::string plan, device = "AUTO"; };  // the members ClBackend reads
+template <class Backend> int use(Backend & be, const std::vector<float> & buf)
+{
+  const infvino::DeviceInfo & dev = be.device();
+  for (const auto & d : dev.available) std::printf(" %s", d.c_str());
+  std::printf("%s -> %s%s (%s) %s %u %u\n", dev.requested.c_str(), dev.resolved.c_str(),
+              dev.fell_back_to_cpu ? " [CPU FALLBACK]" : "", dev.full_name.c_str(), dev.opencl_version.c_str(),
+              dev.eu, dev.clock_mhz);
+  std::vector<infvino::Tensor> outputs = be.infer(buf.data(), buf.size());
+  const std::vector<int64_t> & in = be.inputDims();
+  const std::vector<std::vector<int64_t>> & shapes = be.outputShapes();
+  return (int)(outputs.size() + in.size() + shapes.size() + (be.lastInferMs() > 0));
+}
+int main(int argc, char **)
+{
+  ModelInfo info{"m.plan", "GPU.0"};
+  if (argc > 5) {
+    infvino_hip::HipBackend be(info, false);
+    auto shared = std::make_shared<infvino_hip::HipBackend>(info, true);
+    return use(be, {}) + use(*shared, {});
+  }
+  std::printf("ok\n");
+  return 0;
+}
+''')
+    exe = tmp_path / "bind"
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-DINFVINO_HIP_USE_INFVINO_TENSOR",
+                        "-I", os.path.join(ROOT, "include"), "-I", REF_INCLUDE, str(src), "-o", str(exe),
+                        "-L", os.path.join(ROOT, "infvino_amd"), "-linfvino_hip",
+                        "-Wl,-rpath," + os.path.join(ROOT, "infvino_amd")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
