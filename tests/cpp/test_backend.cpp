@@ -70,7 +70,7 @@ int main(int argc, char ** argv)
   EXPECT(std::memcmp(img1[0].data.data(), one1[0].data.data(), one1[0].data.size() * 4) == 0);
   // profiling = true (ClBackend(info, true)): per-node device times accumulate over infers
   {
-    infvino_hip::HipBackend prof(info, true);
+    infvino_hip::HipBackend prof(info, true, 1, IVH_FLAG_NO_SPLITK);
     prof.infer(x.data(), n);
     prof.infer(x.data(), n);
     auto rows = prof.model().profile();
