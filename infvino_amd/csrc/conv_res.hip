@@ -14,11 +14,15 @@
 //     back with no barrier (every operand is already resident);
 //   * the next two tiles' patches are in flight in registers (buffer loads issued two tiles
 //     ahead, out-of-image pixels read zeros from past the buffer's range);
-//   * the previous tile's epilogue (bias, activation, fp16 rounding into an LDS staging
-//     tile) is interleaved with this tile's MFMAs, so its VALU work -- two transcendentals
-//     per SiLU output -- overlaps the matrix pipe instead of following it;
-//   * two barriers per tile: then the staged outputs go to HBM as 16-byte channels-last
-//     pieces (+ residual) and the next patch is written to LDS.
+//   * the previous tile's epilogue (bias, activation, fp16 rounding, stores) is interleaved
+//     with this tile's MFMAs, so its VALU work -- two transcendentals per SiLU output -- can
+//     overlap the matrix pipe instead of following it;
+//   * two barriers per tile, around the write of the next patch to LDS.
+// Outputs go straight from the accumulators to HBM: with 8-channel stores (SM 2) the two
+// 4-channel runs a lane holds of a pixel and the two its partner lane (lane +- 32) holds are
+// exchanged with v_permlane32_swap, so every lane writes 8 consecutive channels (16 bytes):
+// half the store instructions of 4-channel (8-byte) stores, each touching the same number of
+// 128-byte lines with twice the bytes.
 // Wave layout: the 4 waves split the tile's pixels (TM 32-pixel blocks each) and share all
 // BN = TN*32 channels, so an A (weight) fragment feeds TM MFMAs and a B (pixel) fragment TN.
 #include <algorithm>
@@ -29,9 +33,11 @@
 namespace ivh {
 
 typedef unsigned u2 __attribute__((ext_vector_type(2)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
-template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, int ACT, bool RES, bool CF>
+// SM: output stores of 8 channels (2), 4 channels (1) or single elements (0)
+template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, int ACT, bool RES, int SM>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const ConvParams p)
 {
   using F = Mf<32>;
@@ -55,6 +61,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   constexpr int WQ = KROW / 8;             // 16-byte pieces per weight row
   constexpr int W_IT = (BN * WQ + NT - 1) / NT;
   constexpr int NG = TN * TM * 4;          // epilogue groups (4 accumulator values) per lane
+  constexpr int NE = SM == 2 ? NG / 2 : NG;  // epilogue steps (a step is two groups with SM 2)
   __shared__ __attribute__((aligned(16))) _Float16 lds[BN * LDK + L_PATCH];
   __shared__ __attribute__((aligned(16))) float bias_s[BN];
   _Float16 * const Ws = lds;
@@ -147,6 +154,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   };
 
   h8 rpA[P_IT], rpB[P_IT];  // patches of tiles i + 1 and i + 2 in flight
+  // start of this work-group's weight-load order: work-groups w, w + 8, ... share an XCD (and
+  // its L2); rotating their orders spreads their first requests over the whole weight block
+  // instead of every CU asking for the same lines at once
+  const int wrot = (int)(((long)((blockIdx.x / kXcds) % 32) * (BN * WQ / 32)) % (BN * WQ));
 
   // ---- prologue: bias and weights into LDS, first patch
   if (tid < BN) bias_s[tid] = p.bias ? p.bias[n0 + tid] : 0.0f;
@@ -154,14 +165,16 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
     h8 rw[W_IT];
 #pragma unroll
     for (int i = 0; i < W_IT; ++i) {
-      const int e = tid + i * NT, row = e / WQ, q = e - row * WQ;
+      const int e0 = tid + i * NT;
+      const int e = e0 < BN * WQ ? (e0 + wrot) % (BN * WQ) : e0, row = e / WQ, q = e - row * WQ;
       const unsigned src = e < BN * WQ ? (unsigned)((row * p.kpad + q * 8) * 2) : kBufOOB;
       rw[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, src, 0, 0));
     }
     load_patch(t_lo, rpA);
 #pragma unroll
     for (int i = 0; i < W_IT; ++i) {
-      const int e = tid + i * NT, row = e / WQ, q = e - row * WQ;
+      const int e0 = tid + i * NT;
+      const int e = e0 < BN * WQ ? (e0 + wrot) % (BN * WQ) : e0, row = e / WQ, q = e - row * WQ;
       if (e < BN * WQ) *reinterpret_cast<h8 *>(Ws + row * LDK + q * 8) = rw[i];
     }
     store_patch(rpA);
@@ -213,8 +226,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
     }
   };
   const int cl0 = wn * TN * 32 + F::row(lane, 0);  // lane's first channel in the block
-  // CF with Cout % 4 != 0: the last group also writes the view's padding channels (p.ypad)
-  const long y_last = (long)(p.batch - 1) * p.y.img + ((long)p.H * p.W - 1) * p.y.cs + (CF ? (p.Cout + 3) & ~3 : p.Cout);
+  // SM 1 / 2 with Cout % 4 / % 8 != 0: the last piece also writes the view's padding channels
+  // (p.ypad of them, checked on the host)
+  const long y_last = (long)(p.batch - 1) * p.y.img + ((long)p.H * p.W - 1) * p.y.cs +
+                      (SM == 2 ? (p.Cout + 7) & ~7 : SM == 1 ? (p.Cout + 3) & ~3 : p.Cout);
   const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(p.y.ptr, (short)0, (int)(y_last * 2), kBufDword3);
   const long r_last = RES ? (long)(p.batch - 1) * p.r.img + ((long)p.H * p.W - 1) * p.r.cs + p.Cout : 0;
   const __amdgpu_buffer_rsrc_t rr_ = __builtin_amdgcn_make_buffer_rsrc(RES ? p.r.ptr : p.y.ptr, (short)0,
@@ -231,11 +246,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
       rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
     }
   };
-  // epilogue group g of tile accumulators ac: bias + activation in fp32, one rounding, then
-  // + residual (rounded again), stored as 4 channels-last fp16 values (CF), else element by
-  // element
-  auto epi_group = [&](const acc_t (&ac)[TN][TM], const unsigned (&yo)[TM], const h4 (&rv)[NG], int g)
-      __attribute__((always_inline)) {
+  // epilogue group g of tile accumulators ac (4 values: 4 consecutive channels of one pixel):
+  // bias + activation in fp32, one rounding, then + residual (rounded again)
+  auto epi_vals = [&](const acc_t (&ac)[TN][TM], const h4 (&rv)[NG], int g) __attribute__((always_inline)) {
     const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
     const int cl = tn * 32 + cl0 + 2 * v4;  // F::row(lane, v4)
     const float4 b4 = *reinterpret_cast<const float4 *>(bias_s + cl);
@@ -255,13 +268,37 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
 #pragma unroll
       for (int k = 0; k < 4; ++k) hv[k] = (_Float16)((float)hv[k] + (float)rv[g][k]);
     }
-    if (CF) {
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, hv), yr, chan_off(yo[tm], cl), 0, 0);
+    return hv;
+  };
+  // epilogue step e: group e (SM 0 / 1), or groups 2e and 2e + 1 (SM 2: accumulator values
+  // v4 and v4 + 4 of one block, channels c..c+3 and c+8..c+11 on lanes < 32, c+4..c+7 and
+  // c+12..c+15 on lanes >= 32), computed and stored
+  auto epi_step = [&](const acc_t (&ac)[TN][TM], const unsigned (&yo)[TM], const h4 (&rv)[NG], int e)
+      __attribute__((always_inline)) {
+    if (SM == 2) {
+      const int g = 2 * e;
+      const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;  // v4 = 0 or 8
+      const u2 a = __builtin_bit_cast(u2, epi_vals(ac, rv, g));
+      const u2 b = __builtin_bit_cast(u2, epi_vals(ac, rv, g + 1));
+      // lanes < 32 keep their channels c..c+3 and take c+4..c+7 from lane + 32; lanes >= 32
+      // take c+8..c+11 from lane - 32 and keep c+12..c+15
+      const auto s0 = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+      const u4 q = {s0[0], s1[0], s0[1], s1[1]};
+      const int cl = tn * 32 + cl0 + 2 * v4 + 4 * (lane >> 5);  // first of the lane's 8 channels
+      __builtin_amdgcn_raw_buffer_store_b128(q, yr, chan_off(yo[tm], cl), 0, 0);
     } else {
-      // (bit-cast the whole vector: hipcc reads element 0 for a bit cast of hv[k])
-      const u16x4 hu = __builtin_bit_cast(u16x4, hv);
+      const int tn = e / (TM * 4), tm = (e / 4) % TM, v4 = (e % 4) * 4;
+      const int cl = tn * 32 + cl0 + 2 * v4;
+      const h4 hv = epi_vals(ac, rv, e);
+      if (SM == 1) {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, hv), yr, chan_off(yo[tm], cl), 0, 0);
+      } else {
+        // (bit-cast the whole vector: hipcc reads element 0 for a bit cast of hv[k])
+        const u16x4 hu = __builtin_bit_cast(u16x4, hv);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) __builtin_amdgcn_raw_buffer_store_b16(hu[k], yr, chan_off(yo[tm], cl + k), 0, 0);
+        for (int k = 0; k < 4; ++k) __builtin_amdgcn_raw_buffer_store_b16(hu[k], yr, chan_off(yo[tm], cl + k), 0, 0);
+      }
     }
   };
 
@@ -304,8 +341,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
 #pragma unroll
           for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = F::mma(fa[s & 1][tn], fb[s & 1][tm], acc[tn][tm]);
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
-          if (S0 + g * SPAN / NG == s) epi_group(accp, yop, rvp, g);
+        for (int e = 0; e < NE; ++e)
+          if (S0 + e * SPAN / NE == s) epi_step(accp, yop, rvp, e);
       }
     }
     __syncthreads();  // patch reads done
@@ -336,10 +373,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   // last tile's epilogue
   if (ntl & 1) {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) epi_group(accA, yoA, rvA, g);
+    for (int e = 0; e < NE; ++e) epi_step(accA, yoA, rvA, e);
   } else {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) epi_group(accB, yoB, rvB, g);
+    for (int e = 0; e < NE; ++e) epi_step(accB, yoB, rvB, e);
   }
 }
 
@@ -380,7 +417,15 @@ int res_grid_x(const ConvParams & p, int cfg)
   return (int)std::min<long>(g, res_tiles(p));
 }
 
-bool res_full_stores(const ConvParams & p) { return p.Cout % 4 == 0 || p.ypad >= 4 - p.Cout % 4; }
+// 8-channel stores when every 8-channel piece is inside the view or runs into its own padding
+// channels, else 4-channel stores under the same condition, else single elements
+int res_store_mode(const ConvParams & p)
+{
+  if (p.Cout % 8 == 0 || p.ypad >= 8 - p.Cout % 8) return 2;
+  if (p.Cout % 4 == 0 || p.ypad >= 4 - p.Cout % 4) return 1;
+  return 0;
+}
+int res_store_width(const ConvParams & p) { return res_store_mode(p) == 2 ? 8 : res_store_mode(p) == 1 ? 4 : 1; }
 
 bool res_views_ok(const ConvParams & p)
 {
@@ -432,27 +477,34 @@ bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, in
   return true;
 }
 
-template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, bool RES, bool CF>
+template <int WGM, int WGN, int TM, int TN, int CK, int PMAX, bool RES, int SM>
 static void launch_res_act(const ConvParams & p, int cfg, hipStream_t s)
 {
   constexpr int BN = WGN * TN * 32;
   dim3 grid((unsigned)res_grid_x(p, cfg), (unsigned)((p.Cout + BN - 1) / BN), 1), block(64 * WGM * WGN);
   switch (p.act) {
-  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActSiLU, RES, CF>), grid, block, 0, s, p); break;
-  case kActReLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActReLU, RES, CF>), grid, block, 0, s, p); break;
-  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActHSwish, RES, CF>), grid, block, 0, s, p); break;
-  default: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActNone, RES, CF>), grid, block, 0, s, p); break;
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActSiLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActReLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActHSwish, RES, SM>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s1_res_kernel<WGM, WGN, TM, TN, CK, PMAX, kActNone, RES, SM>), grid, block, 0, s, p); break;
   }
 }
 
-// residual adds need Cout % 4 == 0 (res_views_ok); CF: 4-channel stores (Cout % 4 == 0, or the
-// output view's padding channels absorb the rounding up)
+// residual adds need Cout % 4 == 0 (res_views_ok); the store width follows res_store_mode
 template <int WGM, int WGN, int TM, int TN, int CK, int PMAX>
 static void launch_res_cfg(const ConvParams & p, int cfg, hipStream_t s)
 {
-  if (p.r.ptr) launch_res_act<WGM, WGN, TM, TN, CK, PMAX, true, true>(p, cfg, s);
-  else if (res_full_stores(p)) launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, true>(p, cfg, s);
-  else launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, false>(p, cfg, s);
+  const int sm = res_store_mode(p);
+  if (p.r.ptr) {
+    if (sm == 2) launch_res_act<WGM, WGN, TM, TN, CK, PMAX, true, 2>(p, cfg, s);
+    else launch_res_act<WGM, WGN, TM, TN, CK, PMAX, true, 1>(p, cfg, s);
+  } else if (sm == 2) {
+    launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, 2>(p, cfg, s);
+  } else if (sm == 1) {
+    launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, 1>(p, cfg, s);
+  } else {
+    launch_res_act<WGM, WGN, TM, TN, CK, PMAX, false, 0>(p, cfg, s);
+  }
 }
 
 void launch_conv_res(const ConvParams & p, hipStream_t s)

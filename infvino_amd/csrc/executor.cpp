@@ -1610,7 +1610,7 @@ void Model::validate(const Launch & l) const
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
     // the resident-weight kernel writes 4-channel groups into the view's padding channels
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res && res_full_stores(p) ? (4 - p.Cout % 4) % 4 : 0), HWo), 2,
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
           "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels

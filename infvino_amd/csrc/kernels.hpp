@@ -39,7 +39,7 @@ int res_grid_x(const ConvParams & p, int cfg);
 bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw);
 // the output (and residual) views suit the kernel's 8-byte channels-last buffer stores
 bool res_views_ok(const ConvParams & p);
-bool res_full_stores(const ConvParams & p);  // 4-channel stores (Cout % 4 == 0 or padding)
+int res_store_width(const ConvParams & p);  // channels per output store: 8, 4 or 1 (padding absorbs the rounding up)
 constexpr int kResMinTiles = 1;  // fewer tiles: the halo / im2col kernels
 constexpr int kResMaxRows = 34;  // patch rows (TH + 2) of the resident-weight kernel's tiles
 constexpr int kHaloMaxRows = 34;  // patch rows (TH + 2) of the LDS-patch kernel's tiles
