@@ -9,12 +9,22 @@ table goes to stderr.
   roofline       dominant kernel (largest device time per batch-64 step): algorithmic FLOPs
                  (or bytes) per launch / its mean launch time, HIP events on the model stream
   conv_mfma_frac all conv FLOPs of a step / conv device time / dense fp16 MFMA peak
-  conv_sweep     the conv operator sweep (stem, strided / stride-1 3x3, depthwise) at the
-                 same batch: per layer time, TFLOP/s, GB/s and fraction of its binding roof
-  other_models   MobileNetV3-small 224 (batch 1 / 32 / 256) and YOLO11n-pose 640 (batch 1 /
-                 64): images/s of graph replays and batch-1 latency
+  roofline_step  the whole step against its roofline: sum over nodes of the node's ideal time
+                 (max of algorithmic FLOPs / MFMA peak and bytes / HBM peak) over the sum of
+                 the nodes' measured times -- the time-weighted mean of the per-node fractions
+  config1        the single pointwise conv (64->128 at 80x80, SiLU) at batch 1 and 64, with
+                 its roofline (HBM bound)
+  conv_sweep     the conv operator sweep (stem, strided / stride-1 3x3, depthwise) at batch
+                 64 and batch 1: per layer time, TFLOP/s, GB/s and fraction of its binding roof
+  attention      the C2PSA attention block at 256 channels, 4 heads, head_dim 64, 400 tokens
+                 (q^T k, softmax, v attn^T) at batch 64 and 1, with its roofline
+  other_models   YOLOv8n-pose 640 (batch 16 / 64), MobileNetV3-small 224 (batch 1 / 32 / 256)
+                 and YOLO11n-pose 640 (batch 1 / 64): images/s of graph replays and batch-1
+                 latency
   cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
-                 workload on this host's cores -- a reported baseline, not a target
+                 workload on this host's cores -- a reported baseline, not a target; it
+                 records the probe for a CPU OpenCL runtime that could run the reference's own
+                 kernels instead
 """
 import argparse
 import json
@@ -106,6 +116,107 @@ def conv_sweep(ia, pw, batch, iters):
         log(f"[sweep] {name:24s} b{batch} {inf['kernel']:12s} {t * 1e6:8.2f} us {tf:7.1f} TFLOP/s "
             f"{gbs:7.1f} GB/s -> {rows[-1]['bound']} {rows[-1]['frac'] * 100:.1f}%")
     return rows
+
+
+def roof_of(flops, nbytes, t_s):
+    """Achieved rate of one launch against the roof that binds it (MFMA when its arithmetic
+    intensity is above the ridge, HBM otherwise)."""
+    ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if flops > 0 and flops / max(nbytes, 1) >= ridge:
+        a = flops / t_s / 1e12
+        return {"bound": "mfma", "achieved": round(a, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(a / PEAK_FP16_TFLOPS, 4)}
+    a = nbytes / t_s / 1e9
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(a / PEAK_HBM_GBS, 4)}
+
+
+def ideal_s(flops, nbytes):
+    return max(flops / (PEAK_FP16_TFLOPS * 1e12), nbytes / (PEAK_HBM_GBS * 1e9))
+
+
+def config1(ia, pw, iters):
+    """The single pointwise conv of the plan's conv1x1 op, 64->128 at 80x80 with SiLU, at
+    batch 1 and 64 (HIP-event time of the conv node, eager launches)."""
+    out = {}
+    for b in (1, 64):
+        with tempfile.TemporaryDirectory() as d:
+            path, _ = pw.conv1x1_config(d)
+            m = ia.PlanModel(path, 0, b, ia.IVH_FLAG_NO_GRAPH)
+            x0 = np.random.default_rng(0).random(m.inputNumel() * b, dtype=np.float32)
+            m.setInput(x0.astype(np.float16).view(np.uint16), b)
+            m.run(b)
+            inf = m.nodeInfo(0)
+            t = float(m.profileNodes(b, iters)[0]) * 1e-3
+            m.close()
+        fl, by = inf["flops"] * b, inf["bytes"] * b
+        row = {"batch": b, "kernel": inf["kernel"], "us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 4),
+               "mbytes": round(by / 1e6, 3), "roofline": roof_of(fl, by, t)}
+        out[f"b{b}"] = row
+        log(f"[config1] conv1x1 64->128 @80x80 SiLU batch {b}: {row['us']} us, {row['roofline']}")
+    return out
+
+
+def attention(ia, pw, iters):
+    """The C2PSA attention block (256 channels, 4 heads, head_dim 64, 20x20 = 400 tokens) at
+    batch 64 and 1: time of the attention core (the two batched matmuls, the scale and the
+    softmax) and of the whole block, each node timed with HIP events."""
+    out = {}
+    for b in (64, 1):
+        with tempfile.TemporaryDirectory() as d:
+            path, core_flops = pw.c2psa_attention(d)
+            m = ia.PlanModel(path, 0, b, ia.IVH_FLAG_NO_GRAPH)
+            x0 = np.random.default_rng(0).random(m.inputNumel() * b, dtype=np.float32)
+            m.setInput(x0.astype(np.float16).view(np.uint16), b)
+            m.run(b)
+            prof = m.profileNodes(b, iters)
+            infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
+            m.close()
+        first = next(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
+        last = max(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
+        core = range(first, last + 1)
+        t_core = float(sum(prof[i] for i in core)) * 1e-3
+        by_core = sum(infos[i]["bytes"] for i in core) * b
+        t_block = float(sum(prof[i] for i, inf in enumerate(infos) if inf["op"] != "ew_unary" or i > 0)) * 1e-3
+        row = {"batch": b, "core_us": round(t_core * 1e6, 2), "block_us": round(t_block * 1e6, 2),
+               "core_gflop": round(core_flops * b / 1e9, 3), "core_mbytes": round(by_core / 1e6, 2),
+               "core_tflops": round(core_flops * b / t_core / 1e12, 2),
+               "roofline": roof_of(core_flops * b, by_core, t_core),
+               "nodes": {infos[i]["desc"]: round(float(prof[i]) * 1e3, 2) for i in core}}
+        out[f"b{b}"] = row
+        log(f"[attention] C2PSA 256ch 4 heads 400 tokens batch {b}: core {row['core_us']} us "
+            f"({row['core_tflops']} TFLOP/s, {row['roofline']['bound']} {row['roofline']['frac'] * 100:.1f}%), "
+            f"block {row['block_us']} us")
+    return out
+
+
+def opencl_probe():
+    """Whether this host can run the reference's own OpenCL kernels on its CPU cores: the ICD
+    files present and, through the OpenCL loader, every platform and its CPU devices."""
+    import ctypes as C
+    import glob
+    icds = sorted(os.path.basename(f) for f in glob.glob("/etc/OpenCL/vendors/*.icd"))
+    res = {"icd_files": icds, "platforms": [], "cpu_devices": 0}
+    try:
+        cl = C.CDLL("libOpenCL.so.1")
+    except OSError as e:
+        res["loader"] = f"absent ({e})"
+        return res
+    res["loader"] = "libOpenCL.so.1"
+    n = C.c_uint(0)
+    if cl.clGetPlatformIDs(0, None, C.byref(n)) != 0 or n.value == 0:
+        return res
+    plats = (C.c_void_p * n.value)()
+    cl.clGetPlatformIDs(n.value, plats, None)
+    for pf in plats:
+        name = C.create_string_buffer(256)
+        cl.clGetPlatformInfo(C.c_void_p(pf), C.c_uint(0x0902), C.c_size_t(256), name, None)  # CL_PLATFORM_NAME
+        nd = C.c_uint(0)
+        rc = cl.clGetDeviceIDs(C.c_void_p(pf), C.c_ulong(1 << 1), 0, None, C.byref(nd))  # CL_DEVICE_TYPE_CPU
+        ndev = nd.value if rc == 0 else 0
+        res["platforms"].append({"name": name.value.decode(errors="replace"), "cpu_devices": ndev})
+        res["cpu_devices"] += ndev
+    return res
 
 
 def model_lines(ia, pw, specs, steps, warmup):
@@ -257,10 +368,25 @@ def main():
         achieved = d["bytes"] * B / t_dom / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    roof.update({"traffic": measured_traffic(d["desc"], B), "kernel": d["kernel"], "node": d["desc"],
+    traffic = measured_traffic(d["desc"], B)
+    roof.update({"traffic": traffic,
+                 "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE of this node, scaled by a calibration "
+                                    "kernel: profiles/traffic_dominant_kernel.md (committed, not measured in "
+                                    "this run)") if traffic else None,
+                 "kernel": d["kernel"], "node": d["desc"],
                  "launch_ms": round(t_dom * 1e3, 4),
                  "flops_per_launch": d["flops"] * B, "bytes_per_launch": d["bytes"] * B})
     conv_frac = conv_f / (conv_t * 1e-3) / 1e12 / PEAK_FP16_TFLOPS if conv_t > 0 else 0.0
+    # the whole step against its roofline: every launching node's ideal time (its binding
+    # roof at the published peaks) over its measured time, weighted by the measured time
+    t_meas = float(prof.sum()) * 1e-3
+    t_ideal = sum(ideal_s(inf["flops"] * B, inf["bytes"] * B) for t, inf in zip(prof, infos) if t > 0)
+    roof_step = {"frac": round(t_ideal / t_meas, 4), "ideal_ms": round(t_ideal * 1e3, 4),
+                 "node_sum_ms": round(t_meas * 1e3, 4),
+                 "definition": "sum over launching nodes of max(FLOPs / 2500 TFLOP/s, bytes / 8000 GB/s) "
+                               "over the sum of their HIP-event times, batch 64"}
+    log(f"[bench] step roofline: ideal {t_ideal * 1e3:.3f} ms of {t_meas * 1e3:.3f} ms node time "
+        f"-> {roof_step['frac'] * 100:.1f}%")
     m.close()
 
     # ---- batch-1 latency: synchronous runs (graph replay), mean wall time
@@ -283,9 +409,12 @@ def main():
         log(f"  {prof1[i]:8.4f} ms  {inf1[i]['kernel']:12s} {inf1[i]['desc']}")
     m1.close()
 
-    sweep = None if args.no_sweep else conv_sweep(ia, pw, B, max(args.profile_iters, 10))
+    c1 = None if args.no_sweep else config1(ia, pw, max(args.profile_iters, 10))
+    sweep = None if args.no_sweep else {f"b{b}": conv_sweep(ia, pw, b, max(args.profile_iters, 10)) for b in (B, 1)}
+    attn = None if args.no_sweep else attention(ia, pw, max(args.profile_iters, 10))
     others = None if args.no_models else model_lines(
-        ia, pw, [("mobilenetv3-small", 224, (1, 32, 256)), ("yolo11n-pose", 640, (1, 64))], 20, 5)
+        ia, pw, [("yolov8n-pose", 640, (16, 64)), ("mobilenetv3-small", 224, (1, 32, 256)),
+                 ("yolo11n-pose", 640, (1, 64))], 20, 5)
 
     # ---- CPU baseline: the oracle on a bounded sample of the same workload
     cpu = None
@@ -300,9 +429,14 @@ def main():
         t = time.perf_counter()
         O.run_plan(p, x[:n_in * k], k)
         el = time.perf_counter() - t
+        probe = opencl_probe()
         cpu = {"value": round(k / el, 3), "unit": "images/s", "cores": cores, "kind": "port",
                "sample": f"{k} images of {args.model} 3x{args.imgsz}x{args.imgsz} through the C oracle "
-                         f"(fp32 accumulate, OpenMP over output channels), {el:.1f} s"}
+                         f"(fp32 accumulate, OpenMP over output channels), {el:.1f} s",
+               "reference_kernels": ("unavailable: no OpenCL CPU device on this host (the reference's .cl "
+                                     "kernels need one; see opencl_probe)") if probe["cpu_devices"] == 0 else
+                                    "an OpenCL CPU device exists (opencl_probe); not used by this bench",
+               "opencl_probe": probe}
         log(f"[bench] cpu oracle: {k / el:.3f} images/s on {cores} threads")
 
     out = {
@@ -325,7 +459,10 @@ def main():
         "conv_mfma_frac": round(conv_frac, 4),
         "tflops_effective": round(flops_img * ips / 1e12, 2),
         "roofline": roof,
+        "roofline_step": roof_step,
+        "config1": c1,
         "conv_sweep": sweep,
+        "attention": attn,
         "other_models": others,
         "cpu_baseline": cpu,
     }

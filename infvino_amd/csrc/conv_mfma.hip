@@ -33,8 +33,11 @@ namespace ivh {
 // Both are double buffered in LDS and prefetched PF steps ahead through a ring of PF
 // register stages, so a work-group with a short K loop has its whole K range in flight at
 // once instead of waiting one memory latency per step.  RAG: Cin is not a multiple of 8
-// (the compile-time switch keeps the masking out of the common case).
-template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG, int OCC = 1>
+// (the compile-time switch keeps the masking out of the common case).  XT: a 1x1 conv on
+// NCHW channel planes (p.xt): a thread's A piece is 8 consecutive pixels of one channel (one
+// 16-byte load along the plane), written transposed into the pixel rows of the LDS tile, so
+// the MFMA loop and the epilogue are those of the channels-last case.
+template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG, int OCC = 1, bool XT = false>
 __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p)
 {
   using F = Mf<32>;
@@ -48,6 +51,10 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
   constexpr int STAGE = BM * LDK + BN * LDK;
   constexpr int L_ALL = 2 * STAGE > T::EPI ? 2 * STAGE : T::EPI;
   static_assert(BM % RPI == 0, "tile rows");
+  constexpr int PG = BM / 8;                  // XT: 8-pixel pieces per tile row of a channel
+  constexpr int X_IT = BK * PG / 256;         // XT: A pieces per thread and step
+  static_assert(!XT || X_IT * 256 == BK * PG, "planar tile pieces");
+  constexpr int A_N = XT ? X_IT : A_IT;       // A register pieces per stage
   __shared__ __attribute__((aligned(16))) _Float16 lds[L_ALL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -62,7 +69,10 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
   const int n0 = by * BN;
   const int kc = tid % KC, r0 = tid / KC;
 
-  const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  // end of the input view: the last pixel's channel pieces (channels-last), or the end of the
+  // last channel plane (XT)
+  const long x_last = (long)(p.batch - 1) * p.x.img +
+                      (XT ? (long)(p.Cin - 1) * p.x.cs + (long)p.H * p.W : ((long)p.H * p.W - 1) * p.x.cs + p.cin8);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
@@ -83,6 +93,25 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
       abase[i] = 0;
       aiy[i] = -0x4000000;  // never inside the image
       aix[i] = 0;
+    }
+  }
+  // XT: piece i of this thread is channel xc[i] of the step, pixels m0 + 8 xg[i] .. + 7
+  // (one image: its plane holds a multiple of 8 pixels); byte offset of the piece in step
+  // 0, or past the buffer range for pixels past the batch
+  int xc[XT ? X_IT : 1], xg[XT ? X_IT : 1];
+  unsigned xoff[XT ? X_IT : 1];
+  if constexpr (XT) {
+#pragma unroll
+    for (int i = 0; i < X_IT; ++i) {
+      const int e = tid + i * 256;
+      xc[i] = e / PG;
+      xg[i] = e - xc[i] * PG;
+      const unsigned pm = m0 + 8 * xg[i];
+      xoff[i] = kBufOOB;
+      if (pm < M) {
+        const int b = (int)fastdiv(pm, p.dv_hwo), hw = (int)pm - b * HWo;
+        xoff[i] = (unsigned)((b * (int)p.x.img + xc[i] * p.x.cs + hw) * 2);
+      }
     }
   }
   unsigned bsrc[B_IT];
@@ -116,9 +145,22 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
   };
 
   // register ring: stage d holds the pieces of step d (mod PF) between load and LDS store
-  h8 ra[PF][A_IT], rb[PF][B_IT];
+  h8 ra[PF][A_N], rb[PF][B_IT];
   int aci[PF];  // channel of the loaded A piece (for the ragged mask at store time)
   auto load = [&](int kt, int d) {
+    if constexpr (XT) {
+      // channels past Cin read zeros (their packed weights are zero too)
+#pragma unroll
+      for (int i = 0; i < X_IT; ++i) {
+        const bool ok = kt * BK + xc[i] < p.Cin && xoff[i] != kBufOOB;
+        const unsigned off = ok ? xoff[i] + (unsigned)(kt * BK * p.x.cs * 2) : kBufOOB;
+        ra[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+      }
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i)
+        rb[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
+      return;
+    }
     aci[d] = ci;
     const int ky = (int)(((unsigned)tap * kmul) >> 16), kx = tap - ky * p.K;
 #pragma unroll
@@ -134,6 +176,16 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
     advance();
   };
   auto store = [&](_Float16 * st, int d) {
+    if constexpr (XT) {
+#pragma unroll
+      for (int i = 0; i < X_IT; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st[(8 * xg[i] + j) * LDK + xc[i]] = ra[d][i][j];
+#pragma unroll
+      for (int i = 0; i < B_IT; ++i)
+        if (r0 + i * RPI < BN) *reinterpret_cast<h8 *>(st + (BM + r0 + i * RPI) * LDK + kc * 8) = rb[d][i];
+      return;
+    }
     u16x8 keep;
     if (RAG) {
 #pragma unroll
@@ -243,7 +295,8 @@ static void launch_t(const ConvParams & p, hipStream_t s)
   q.dv_hwo = fastdiv_make((unsigned)(p.Ho * p.Wo));
   q.dv_wo = fastdiv_make((unsigned)p.Wo);
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
-  if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, true>), grid, dim3(256), 0, s, q);
+  if (p.xt) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, 1, true>), grid, dim3(256), 0, s, q);
+  else if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, true>), grid, dim3(256), 0, s, q);
   else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, OCC>), grid, dim3(256), 0, s, q);
   if (p.ksplit > 1) {
     const long n = M * p.Cout;
@@ -273,7 +326,7 @@ static void launch_bk(const ConvParams & p, hipStream_t s)
     // fit four: the 128-VGPR build of the same tile (40x40 maps at batch 64, 800 tiles:
     // 22-34 -> 20-30 us).  3x3 convs lose more to the register cap than they gain (measured).
     if constexpr (BK == 32) {
-      if (p.K == 1 && !(p.Cin & 7) && p.ksplit == 1 && igemm_tiles(p) > 3 * 256 && igemm_tiles(p) <= 4 * 256) {
+      if (p.K == 1 && !(p.Cin & 7) && !p.xt && p.ksplit == 1 && igemm_tiles(p) > 3 * 256 && igemm_tiles(p) <= 4 * 256) {
         launch_t<2, 2, 2, 2, BK, PF128, 4>(p, s);
         break;
       }

@@ -53,7 +53,8 @@ ConvPacking conv_packing(const ConvSpec & s)
   const int cin_g = s.Cin / s.G;
   const bool dw = s.G > 1 && s.G == s.Cin && s.Cout == s.Cin && (s.K == 3 || s.K == 5);
   if (dw) pk.family = kFamDw;
-  else if (s.G == 1 && (s.x_nhwc || s.x_vec1)) pk.family = kFamIgemm;
+  else if (s.G == 1 && (s.x_nhwc || s.x_vec1 || (s.x_planes8 && s.K == 1 && s.S == 1 && s.P == 0)))
+    pk.family = kFamIgemm;
   else pk.family = kFamDirect;
   if (s.flags & IVH_FLAG_DIRECT_ONLY) pk.family = dw ? kFamDw : kFamDirect;
 
@@ -168,6 +169,13 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   if (ws) {
     p.ksplit = igemm_ksplit((long)batch * p.Ho * p.Wo, p.Cout, p.kpad);
     if (p.ksplit > 1) p.ws = ws;
+  }
+  if (!s.x_nhwc && !s.x_vec1) {  // 1x1 on NCHW planes (x_planes8): no other kernel applies
+    if (p.x.layout != kNCHW || p.x.cs != p.H * p.W || (p.x.cs % 8) || (p.x.img % 8) ||
+        (reinterpret_cast<uintptr_t>(p.x.ptr) % 16) || p.K != 1 || p.S != 1 || p.P != 0)
+      throw std::runtime_error("implicit-GEMM input view: NCHW planes of 8-pixel pieces expected");
+    p.xt = 1;
+    return kLaunchIgemm;
   }
   // 3x3 stride 1 with 16 < Cin <= 64: weights resident in LDS, persistent over pixel tiles.
   // Measured on MI355X at batch 64 against the LDS-patch kernel: faster for every such layer

@@ -24,6 +24,8 @@ struct ConvSpec {
   bool has_bias = false;
   bool x_nhwc = false;  // input channels-last with 16-byte aligned pixels (MFMA families)
   bool x_vec1 = false;  // single-pixel NCHW input (an FC / GEMV): the MFMA family reads it too
+  bool x_planes8 = false;  // 1x1 conv on NCHW input whose planes hold a multiple of 8 pixels:
+                           // the MFMA family reads it, transposing pixel pieces in LDS
   uint32_t flags = 0;   // IVH_FLAG_DIRECT_ONLY / IVH_FLAG_NO_HALO
   int Ho() const { return (H + 2 * P - K) / S + 1; }
   int Wo() const { return (W + 2 * P - K) / S + 1; }

@@ -1089,6 +1089,10 @@ void Model::uploadWeights()
     const Root & xr = *roots_[x.root < 0 ? 0 : x.root];
     cs.x_nhwc = x.kind == Tensor::kAct && xr.layout == kNHWC && (x.coff % 8) == 0;
     cs.x_vec1 = is1 && (long)cs.H * cs.W == 1 && x.kind != Tensor::kInit && (x.eoff % 8) == 0 && xr.layout == kNCHW;
+    // a 1x1 conv on NCHW channel planes (e.g. the graph input): the implicit GEMM reads
+    // 8-pixel pieces of each plane and transposes them in LDS
+    cs.x_planes8 = is1 && !cs.x_vec1 && x.kind != Tensor::kInit && xr.layout == kNCHW && ((long)cs.H * cs.W) % 8 == 0 &&
+                   (x.eoff % 8) == 0 && (xr.per_image % 8) == 0;
     cs.flags = flags_;
     Packed pk;
     pk.spec = cs;
@@ -1616,8 +1620,15 @@ void Model::validate(const Launch & l) const
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
     if (p.bias) check(p.bias, 0, (l.kind == Launch::kIgemm ? (p.Cout + 127) / 128 * 128 : p.Cout) - 1, 4, "conv bias");
     if (l.kind == Launch::kIgemm) {
-      if (p.x.layout != kNHWC) throw std::runtime_error("igemm needs channels-last input");
-      check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
+      if (p.xt) {
+        if (p.x.layout != kNCHW || p.K != 1 || p.S != 1 || p.P != 0 || p.halo || p.res || p.s2 || p.x.cs != HW ||
+            HW % 8 || p.x.img % 8)
+          throw std::runtime_error("igemm planar input geometry");
+        check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "igemm planar x");
+      } else {
+        if (p.x.layout != kNHWC) throw std::runtime_error("igemm needs channels-last input");
+        check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
+      }
       const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
       if (p.halo) {

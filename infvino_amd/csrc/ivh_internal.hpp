@@ -85,6 +85,10 @@ struct ConvParams {
   // 3x3 stride-2 small-channel kernel (conv_s2.hip): config + 1 (0: not used); th x tw is
   // then the output tile of one image and w the implicit-GEMM packing
   int s2 = 0;
+  // implicit GEMM of a 1x1 conv reading NCHW channel planes (x.cs = pixels per plane, a
+  // multiple of 8): each thread loads 8 consecutive pixels of one channel and writes them
+  // transposed into the tile's pixel rows in LDS (0: channels-last input)
+  int xt = 0;
   // divisions by Ho * Wo and by Wo (set by the implicit-GEMM launcher)
   FastDiv dv_hwo, dv_wo;
 };

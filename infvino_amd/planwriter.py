@@ -572,6 +572,20 @@ def single_conv(out_dir, cin, cout, H, W, k=1, s=1, groups=1, act=ACT_SILU, seed
     return pb.write(), pb.flops
 
 
+def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0):
+    """The C2PSA attention block alone: input [1, C, H, H] -> ReLU -> qkv 1x1, per-head q^T k * scale
+    over H*H tokens, softmax, v attn^T, + depthwise 3x3 positional conv of v, 1x1 projection
+    (ultralytics Attention, attn_ratio 0.5: head_dim C / heads, key_dim head_dim / 2).
+    Returns (plan path, FLOPs/image of the attention core: q^T k and v attn^T)."""
+    pb = PlanBuilder(out_dir, seed=seed)
+    # a ReLU first, so that the block reads an internal (channels-last) tensor as in the model
+    x = pb.unary(pb.input("images", [1, C, H, H]), UN_RELU)
+    pb.output(_attention(pb, x, heads))
+    N, hd = H * H, C // heads
+    core = 2.0 * heads * N * N * (hd // 2) + 2.0 * heads * hd * N * N
+    return pb.write(), core
+
+
 def conv1x1_config(out_dir, seed=0):
     """Single pointwise conv via the plan's conv1x1 op: Cin=64, Cout=128, 80x80, SiLU;
     X ~ U[0,1), W ~ N(0, sqrt(2/Cin)), bias ~ N(0, 0.01)."""

@@ -351,3 +351,21 @@ def test_pool_chain_without_concat(tmp_path):
     path = pool_chain_plan(str(tmp_path))
     assert _kernels(path, 2).count("maxpool_sppf") == 1
     _check_f32(path, 2, lo=-1.0, ref_mode=False)
+
+
+@pytest.mark.parametrize("cin,cout,hw,batch", [
+    (64, 128, 80, 3),     # config 1 on three images
+    (20, 40, 24, 2),      # Cin % 8 != 0: channels past Cin read zeros
+    (384, 64, 16, 1),     # long K at batch 1 (split-K); 384 planes reach past (HW - 1) * HW
+    (256, 136, 12, 5),    # Cout > 128, 8-pixel pieces crossing tiles and images
+    (64, 128, 10, 2),     # 100-pixel planes: not a multiple of 8 -> direct kernel
+])
+def test_conv1x1_planar_input(tmp_path, cin, cout, hw, batch):
+    """1x1 convs reading the plan's NCHW graph input (BASELINE config 1's shape class): the
+    implicit GEMM loads 8-pixel pieces of each channel plane and transposes them in LDS."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=1, act=pw.ACT_SILU)
+    kern = _conv_kernel(path, batch)
+    assert kern == "conv_direct" if (hw * hw) % 8 else kern in ("conv_igemm", "conv_igemm_sk")
+    _check_f32(path, batch, lo=-1.0)
+    if kern == "conv_igemm_sk":
+        _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
