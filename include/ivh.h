@@ -93,6 +93,15 @@ int ivh_max_batch(const ivh_model * m, int * max_batch);
 /* host buffers hold `batch` images back to back (batch * per-image numel elements) */
 int ivh_set_input_f16(ivh_model * m, const uint16_t * host, int batch);
 int ivh_set_input_f32(ivh_model * m, const float * host, int batch);
+/* ivh_set_input_f32 without any device allocation (no counterpart in the reference): for
+   callers that cannot allocate -- code around HIP graph capture, serving loops that forbid
+   hipMalloc.  ivh_set_input_f32 stages the f32 input in a device buffer it allocates on its
+   first call; this one streams it through a fixed 8 MiB array that every GPU the library
+   runs on holds until the process ends, 2^21 floats at a time, so no batch is too large for
+   it (batch is checked against the model's maximum, as for ivh_set_input_f32).  Results are
+   bit-identical to ivh_set_input_f32's.  Calls that overlap on one GPU (two models, or two
+   threads) share the array and race: serialise them per device. */
+int ivh_set_input_f32_noalloc(ivh_model * m, const float * host, int batch);
 int ivh_run(ivh_model * m, int batch);
 int ivh_sync(ivh_model * m);
 int ivh_read_output_f16(ivh_model * m, int i, uint16_t * host, int batch);

@@ -62,6 +62,7 @@ SIGNATURES = {
     "ivh_max_batch": (_i, [_vp, _ip]),
     "ivh_set_input_f16": (_i, [_vp, _vp, _i]),
     "ivh_set_input_f32": (_i, [_vp, _vp, _i]),
+    "ivh_set_input_f32_noalloc": (_i, [_vp, _vp, _i]),
     "ivh_run": (_i, [_vp, _i]),
     "ivh_sync": (_i, [_vp]),
     "ivh_read_output_f16": (_i, [_vp, _i, _vp, _i]),

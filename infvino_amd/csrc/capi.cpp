@@ -275,6 +275,14 @@ int ivh_set_input_f32(ivh_model * m, const float * host, int batch)
     M(m).setInputF32Trunc(host, batch);
   });
 }
+int ivh_set_input_f32_noalloc(ivh_model * m, const float * host, int batch)
+{
+  return guard([&] {
+    if (!host) throw std::invalid_argument("null input");
+    M(m).setInputF32TruncNoAlloc(host, batch);
+  });
+}
+
 int ivh_run(ivh_model * m, int batch)
 {
   return guard([&] { M(m).run(batch); });

@@ -1833,6 +1833,29 @@ void Model::setInputF32Trunc(const float * host, int batch)
   HIPCHECK(hipStreamSynchronize(stream_));
 }
 
+// The f32 input passes through the GPU's fixed 8 MiB scratch array in chunks: each chunk is
+// copied in and converted before the next copy overwrites the array (one stream orders the
+// copy after the previous chunk's kernel), so any batch fits and nothing is allocated.  Two
+// models converting on the same GPU at the same time share the array and race: callers on
+// one device serialise these calls.
+void Model::setInputF32TruncNoAlloc(const float * host, int batch)
+{
+  check_batch(batch, max_batch_);
+  if (dry_) throw std::runtime_error("dry-run model has no device");
+  HIPCHECK(hipSetDevice(device_));
+  float * sc = boundary_scratch(device_);
+  const long n = (long)inputNumel();
+  const long img = roots_[T_[input_name_]->root]->per_image;
+  for (int b = 0; b < batch; ++b)
+    for (long off = 0; off < n; off += kBoundaryScratchFloats) {
+      const long len = std::min(n - off, kBoundaryScratchFloats);
+      HIPCHECK(hipMemcpyAsync(sc, host + (long)b * n + off, (size_t)len * 4, hipMemcpyHostToDevice, stream_));
+      launch_f32_to_f16_trunc(sc, static_cast<__half *>(input_buf_) + (long)b * img + off, len, stream_);
+    }
+  HIPCHECK(hipGetLastError());
+  HIPCHECK(hipStreamSynchronize(stream_));
+}
+
 void Model::run(int batch)
 {
   check_batch(batch, max_batch_);

@@ -56,6 +56,8 @@ class Model {
 
   void setInputF16(const uint16_t * host, int batch);
   void setInputF32Trunc(const float * host, int batch);
+  // the same conversion staged through the GPU's fixed scratch array: allocates nothing
+  void setInputF32TruncNoAlloc(const float * host, int batch);
   void setInputDeviceF16(const void * dev, int batch);
   void run(int batch);
   void sync();

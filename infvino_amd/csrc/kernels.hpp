@@ -86,6 +86,10 @@ void launch_bmm_mfma(const SmallParams & q, hipStream_t s);  // bmm_mfma.hip
 
 // boundary conversions (include/infvino/Half.hpp semantics for the truncating one)
 void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t s);
+// Device address of the current GPU's fixed staging array (kBoundaryScratchFloats floats,
+// 8 MiB) for ivh_set_input_f32_noalloc; `device` must be the current device.
+constexpr long kBoundaryScratchFloats = 1L << 21;
+float * boundary_scratch(int device);
 void launch_f16_to_f32(const __half * in, float * out, long n, hipStream_t s);
 
 }  // namespace ivh

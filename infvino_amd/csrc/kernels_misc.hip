@@ -6,6 +6,10 @@
 #include "kernels.hpp"
 
 #include <initializer_list>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
 
 namespace ivh {
 
@@ -1450,6 +1454,31 @@ void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t
 {
   hipLaunchKernelGGL(f32_to_f16_trunc_kernel, dim3(nblk(n, 256)), dim3(256), 0, s, in,
                      reinterpret_cast<uint16_t *>(out), n);
+}
+
+// Staging area of the allocation-free f32 input conversion (ivh_set_input_f32_noalloc): a
+// fixed array in every GPU's memory, so that path needs no hipMalloc.  Host code must not use
+// the array's name as an address (it names a host-side shadow); boundary_scratch() returns
+// the device address of the current GPU's copy, resolved once per device.
+static __device__ __align__(256) float scratch[kBoundaryScratchFloats];
+
+float * boundary_scratch(int device)
+{
+  static std::mutex mu;
+  static std::map<int, float *> ptr_of;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto it = ptr_of.find(device);
+  if (it != ptr_of.end()) return it->second;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != device)
+    throw std::runtime_error("HIP error: boundary scratch asked for device " + std::to_string(device) +
+                             " while another is current");
+  void * ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    throw std::runtime_error(std::string("HIP error: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  ptr_of[device] = static_cast<float *>(ptr);
+  return static_cast<float *>(ptr);
 }
 
 void launch_f16_to_f32(const __half * in, float * out, long n, hipStream_t s)
