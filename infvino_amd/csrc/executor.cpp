@@ -297,8 +297,9 @@ void Model::fuseResidual()
       if (c.ins.size() < 4) c.ins.resize(4, "-");
       c.ins[3] = rname;
       c.outs[0] = e.outs[0];
+      const int cidx = pit->second;  // (pit dies with the erase)
       producer.erase(pname);
-      producer[e.outs[0]] = pit->second;
+      producer[e.outs[0]] = cidx;
       remove[i] = 1;
       break;
     }

@@ -320,3 +320,52 @@ int main(int argc, char **)
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
+
+
+MALFORMED = [c[:2] for c in [
+    ("tensor y 1 4\nnode ew_unary x y op=1 n=4\noutput y\n", ()),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary x y op=1 n=4\n", ()),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary x y op=1 n=4\noutput z\n", ()),
+    ("input x 1 4\ntensor y 1 4\nnode frobnicate x y\noutput y\n", ()),
+    ("input x 1 4\ninit w w.bin 4 4\ntensor y 1 4\nnode conv1x1 w,x,-,- y\noutput y\n", ()),
+    ("input x 1 4\ninit w w.bin 4 4\ntensor y 1 4\nnode conv1x1 w,x,-,- y\noutput y\n", [("w.bin", 7)]),
+    ("input x 1 4\ntensor y 1 4\nnode ew_unary q y op=1 n=4\noutput y\n", ()),
+    ("input x 1 8 4 4\ninit w w.bin 8 8 3 3\ntensor y 1 8 4 4\nnode conv3x3 x,w,-,- y stride=1 pad=1 Hout=5 Wout=4\n"
+     "output y\n", [("w.bin", 576)]),
+    ("input x 1 4\ntensor y 1 4\nnode slice_axis x y outer=1 axdim=4 inner=1 start=3 len=4\noutput y\n", ()),
+    ("input x 1 4 4\ntensor y 1 4 4\nnode maxpool x y C=4 H=4 W=4 Hout=4 Wout=4 K=99 S=1 P=2\noutput y\n", ()),
+    ("", ()),
+]]
+
+
+def test_host_sanitizers(plans, tmp_path):
+    """The planner's host code built with AddressSanitizer and UndefinedBehaviorSanitizer
+    (make -C infvino_amd/csrc asan; device code unchanged) runs every model as a dry run at
+    batch 1 / 5 / 64 / 3 / 1 under seven flag sets -- planning, packing, the memory plan's
+    overlap check and every launch's host bounds check -- and rejects malformed plans with an
+    error; any invalid access or undefined behaviour aborts the run."""
+    import shutil
+    import subprocess
+    clang = "/opt/rocm/llvm/bin/clang++"
+    if not os.path.exists(clang) or not shutil.which("make"):
+        pytest.skip("no clang++ / make")
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "infvino_amd", "csrc"), "asan", "-j8"], check=True,
+                   capture_output=True)
+    out = os.path.join(ROOT, "tests", "cpp", "_build", "asan")
+    exe = os.path.join(out, "dry_run_checks")
+    r = subprocess.run([clang, "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+                        "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "cpp", "dry_run_checks.cpp"),
+                        "-o", exe, "-L", out, "-linfvino_hip", "-Wl,-rpath," + out], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    good = [plans(n)[0] for n in ("yolov8n-pose", "mobilenetv3-small", "yolo11n-pose")]
+    good += [pw.c2psa_attention(str(tmp_path / "attn"))[0], pool_chain_plan(str(tmp_path / "pool"))]
+    bad = []
+    for i, (text, bins) in enumerate(MALFORMED):
+        d = tmp_path / f"bad{i}"
+        d.mkdir()
+        bad.append(_write(d, text, bins))
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    r = subprocess.run([exe] + good + ["--"] + bad, capture_output=True, text=True, env=env, timeout=600)
+    print(r.stdout[-2000:], r.stderr[-4000:])
+    assert r.returncode == 0 and "0 failures" in r.stdout
