@@ -159,34 +159,41 @@ def config1(ia, pw, iters):
 
 def attention(ia, pw, iters):
     """The C2PSA attention block (256 channels, 4 heads, head_dim 64, 20x20 = 400 tokens) at
-    batch 64 and 1: time of the attention core (the two batched matmuls, the scale and the
-    softmax) and of the whole block, each node timed with HIP events."""
+    batch 64 and 1: time of the attention core -- q^T k, scale, softmax, v P^T, as one fused
+    kernel (the default) and node by node (IVH_FLAG_NO_FUSE_ATTN) -- and of the whole block,
+    each node timed with HIP events."""
     out = {}
     for b in (64, 1):
-        with tempfile.TemporaryDirectory() as d:
-            path, core_flops = pw.c2psa_attention(d)
-            m = ia.PlanModel(path, 0, b, ia.IVH_FLAG_NO_GRAPH)
-            x0 = np.random.default_rng(0).random(m.inputNumel() * b, dtype=np.float32)
-            m.setInput(x0.astype(np.float16).view(np.uint16), b)
-            m.run(b)
-            prof = m.profileNodes(b, iters)
-            infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
-            m.close()
-        first = next(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
-        last = max(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
-        core = range(first, last + 1)
-        t_core = float(sum(prof[i] for i in core)) * 1e-3
-        by_core = sum(infos[i]["bytes"] for i in core) * b
-        t_block = float(sum(prof[i] for i, inf in enumerate(infos) if inf["op"] != "ew_unary" or i > 0)) * 1e-3
-        row = {"batch": b, "core_us": round(t_core * 1e6, 2), "block_us": round(t_block * 1e6, 2),
-               "core_gflop": round(core_flops * b / 1e9, 3), "core_mbytes": round(by_core / 1e6, 2),
-               "core_tflops": round(core_flops * b / t_core / 1e12, 2),
-               "roofline": roof_of(core_flops * b, by_core, t_core),
-               "nodes": {infos[i]["desc"]: round(float(prof[i]) * 1e3, 2) for i in core}}
+        row = {"batch": b}
+        for label, flags in (("fused", 0), ("node_by_node", ia.IVH_FLAG_NO_FUSE_ATTN)):
+            with tempfile.TemporaryDirectory() as d:
+                path, core_flops = pw.c2psa_attention(d)
+                m = ia.PlanModel(path, 0, b, ia.IVH_FLAG_NO_GRAPH | flags)
+                x0 = np.random.default_rng(0).random(m.inputNumel() * b, dtype=np.float32)
+                m.setInput(x0.astype(np.float16).view(np.uint16), b)
+                m.run(b)
+                prof = m.profileNodes(b, iters)
+                infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
+                m.close()
+            core = [i for i, inf in enumerate(infos) if inf["op"] == "attention"]
+            if not core:
+                first = next(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
+                last = max(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
+                core = list(range(first, last + 1))
+            t_core = float(sum(prof[i] for i in core)) * 1e-3
+            by_core = sum(infos[i]["bytes"] for i in core) * b
+            t_block = float(sum(prof[i] for i in range(1, len(infos)))) * 1e-3  # all but the leading ReLU
+            row[label] = {"core_us": round(t_core * 1e6, 2), "block_us": round(t_block * 1e6, 2),
+                          "core_mbytes": round(by_core / 1e6, 2),
+                          "core_tflops": round(core_flops * b / t_core / 1e12, 2),
+                          "roofline": roof_of(core_flops * b, by_core, t_core),
+                          "nodes": {infos[i]["desc"]: round(float(prof[i]) * 1e3, 2) for i in core}}
+        row["core_gflop"] = round(core_flops * b / 1e9, 3)
         out[f"b{b}"] = row
-        log(f"[attention] C2PSA 256ch 4 heads 400 tokens batch {b}: core {row['core_us']} us "
-            f"({row['core_tflops']} TFLOP/s, {row['roofline']['bound']} {row['roofline']['frac'] * 100:.1f}%), "
-            f"block {row['block_us']} us")
+        f, n = row["fused"], row["node_by_node"]
+        log(f"[attention] C2PSA 256ch 4 heads 400 tokens batch {b}: core fused {f['core_us']} us "
+            f"({f['core_tflops']} TFLOP/s, {f['roofline']['bound']} {f['roofline']['frac'] * 100:.1f}%) vs node by node "
+            f"{n['core_us']} us; block {f['block_us']} vs {n['block_us']} us")
     return out
 
 

@@ -64,6 +64,8 @@ extern "C" {
                                           one fused kernel */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
+#define IVH_FLAG_NO_FUSE_ATTN 0x1000u /* keep an attention core (q^T k, scale, softmax, v P^T)
+                                         node by node instead of one fused kernel */
 #define IVH_FLAG_PROFILE 0x800u   /* PlanModel's profiling=true: every run launches node by node
                                      with a HIP event between nodes, waits, and adds each node's
                                      time to the totals ivh_node_times reports (no graph) */

@@ -154,6 +154,7 @@ Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t 
     fuseResidual();
     fuseActivation();
     fusePermuteMatmul();
+    fuseAttention();
   }
   plan();
   if (!dry_) HIPCHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
@@ -307,6 +308,93 @@ void Model::fuseResidual()
   std::vector<PlanNode> kept;
   for (size_t i = 0; i < nodes_.size(); ++i)
     if (!remove[i]) kept.push_back(std::move(nodes_[i]));
+  nodes_ = std::move(kept);
+}
+
+// Attention core -> one fused node.  After fusePermuteMatmul, ultralytics' Attention reads
+//   S = bmm(q, k; ta)  [h][kd][N]^T x [h][kd][N] -> [h][N][N]
+//   T = ew_binary mul (S, scalar init)
+//   P = softmax_axis (T) over the last axis
+//   O = bmm(v, P; tb)  [h][hd][N] x [h][N][N]^T -> [h][hd][N]
+// each intermediate with that single reader; the four become node "attention" (q, k, v ->
+// O) with the scale's fp16 bits, run by attn_kernel (attention.hip), which keeps every
+// node's fp16 rounding.  kd 32, hd 64, N a multiple of 8 up to kAttnMaxN; anything else
+// stays node by node (as does everything with IVH_FLAG_NO_FUSE_ATTN).
+void Model::fuseAttention()
+{
+  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_ATTN)) return;
+  std::map<std::string, int> producer, uses;
+  std::map<std::string, std::vector<int>> readers;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & o : nodes_[i].outs) producer[o] = (int)i;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & in : nodes_[i].ins)
+      if (in != "-") {
+        ++uses[in];
+        readers[in].push_back((int)i);
+      }
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  auto sole_reader = [&](const std::string & t) -> int {
+    if (uses[t] != 1 || outs.count(t) || readers[t].size() != 1) return -1;
+    return readers[t][0];
+  };
+  auto dims3 = [&](const std::string & t, int64_t & a, int64_t & b, int64_t & c) {
+    const auto & d = T_.at(t)->dims;
+    if (d.size() < 2) return false;
+    b = d[d.size() - 2];
+    c = d.back();
+    a = T_.at(t)->numel / std::max<int64_t>(b * c, 1);
+    return a * b * c == T_.at(t)->numel;
+  };
+  std::vector<char> remove(nodes_.size(), 0);
+  std::map<int, PlanNode> replace;
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    const PlanNode & m1 = nodes_[i];
+    if (m1.op != "bmm" || m1.ins.size() < 2 || m1.i("ta") != 1 || m1.i("tb") == 1 || remove[i]) continue;
+    const int ie = sole_reader(m1.outs[0]);
+    if (ie < 0) continue;
+    const PlanNode & e = nodes_[ie];
+    if (e.op != "ew_binary" || e.i("op") != 2 || e.ins.size() < 2) continue;
+    const std::string sc = e.ins[0] == m1.outs[0] ? e.ins[1] : e.ins[0];
+    if (T_.count(sc) == 0 || T_.at(sc)->kind != Tensor::kInit || T_.at(sc)->numel != 1) continue;
+    const int is = sole_reader(e.outs[0]);
+    if (is < 0) continue;
+    const PlanNode & sm = nodes_[is];
+    if (sm.op != "softmax_axis" || sm.i("inner", 1) != 1) continue;
+    const int i2 = sole_reader(sm.outs[0]);
+    if (i2 < 0) continue;
+    const PlanNode & m2 = nodes_[i2];
+    if (m2.op != "bmm" || m2.ins.size() < 2 || m2.i("tb") != 1 || m2.i("ta") == 1 || m2.ins[1] != sm.outs[0]) continue;
+    int64_t hq, kd, n, hk, kd2, nk, hv, hd, nv, ho, hd2, no, hs, ns1, ns2;
+    if (!dims3(m1.ins[0], hq, kd, n) || !dims3(m1.ins[1], hk, kd2, nk) || !dims3(m2.ins[0], hv, hd, nv) ||
+        !dims3(m2.outs[0], ho, hd2, no) || !dims3(sm.outs[0], hs, ns1, ns2))
+      continue;
+    if (kd != kAttnKD || kd2 != kd || hd != kAttnHD || hd2 != hd || nk != n || nv != n || no != n || ns1 != n ||
+        ns2 != n || hk != hq || hv != hq || ho != hq || hs != hq || sm.i("axdim") != n || n % 8 || n > kAttnMaxN ||
+        attn_key_blocks((int)n) == 0)
+      continue;
+    // the scale: the init's one fp16 value
+    uint16_t bits = 0;
+    {
+      std::ifstream f(T_.at(sc)->file, std::ios::binary);
+      if (!f || !f.read(reinterpret_cast<char *>(&bits), 2)) continue;
+    }
+    PlanNode fz;
+    fz.op = "attention";
+    fz.ins = {m1.ins[0], m1.ins[1], m2.ins[0]};
+    fz.outs = {m2.outs[0]};
+    fz.attr["heads"] = std::to_string(hq);
+    fz.attr["n"] = std::to_string(n);
+    fz.attr["scale_bits"] = std::to_string(bits);
+    remove[i] = remove[ie] = remove[is] = 1;
+    replace[i2] = fz;
+  }
+  std::vector<PlanNode> kept;
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    if (remove[i]) continue;
+    auto it = replace.find((int)i);
+    kept.push_back(it != replace.end() ? std::move(it->second) : std::move(nodes_[i]));
+  }
   nodes_ = std::move(kept);
 }
 
@@ -1166,6 +1254,31 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
   const Tensor & yt = *T_[n.outs[0]];
   auto has = [&](size_t i) { return i < n.ins.size() && n.ins[i] != "-"; };
   auto fail = [&](const std::string & m) { throw std::runtime_error("node " + n.op + " -> " + yt.name + ": " + m); };
+  if (n.op == "attention") {
+    Launch L;
+    L.kind = Launch::kAttn;
+    AttnParams & a = L.ap;
+    a.batch = batch;
+    a.heads = n.i("heads");
+    a.n = n.i("n");
+    a.scale = h2f((uint16_t)n.i("scale_bits"));
+    a.q = view(n.ins.at(0), batch);
+    a.k = view(n.ins.at(1), batch);
+    a.v = view(n.ins.at(2), batch);
+    a.y = view(yt.name, batch);
+    // per-head blocks of dense NCHW tensors: the view's channel stride is one head's block
+    const long nn = a.n;
+    for (View * v : {&a.q, &a.k, &a.v, &a.y}) {
+      if (v->layout != kNCHW) fail("attention operands must be NCHW");
+      const long blk = (v == &a.q || v == &a.k) ? kAttnKD * nn : kAttnHD * nn;
+      const Tensor & t = *T_[v == &a.q ? n.ins[0] : v == &a.k ? n.ins[1] : v == &a.v ? n.ins[2] : yt.name];
+      if (t.numel != blk * a.heads) fail("attention operand size");
+      v->cs = (int)blk;  // head stride
+      if ((reinterpret_cast<uintptr_t>(v->ptr) & 15) || (v->img & 7)) fail("attention operand alignment");
+    }
+    out.push_back(L);
+    return;
+  }
   if (n.op == "pose_decode") {
     Launch L;
     L.kind = Launch::kDecode;
@@ -1588,6 +1701,20 @@ void Model::validate(const Launch & l) const
     if (C <= 0 || HW <= 0 || B <= 0) return -1;
     return (long)(B - 1) * v.img + (v.layout == kNHWC ? (HW - 1) * v.cs + (C - 1) : (C - 1) * v.cs + (HW - 1));
   };
+  if (l.kind == Launch::kAttn) {
+    const AttnParams & a = l.ap;
+    if (a.batch < 1 || a.batch > 65535 || a.heads < 1 || a.heads > 65535 || a.n < 8 || a.n % 8 || a.n > kAttnMaxN ||
+        attn_key_blocks(a.n) == 0)
+      throw std::runtime_error("attention geometry");
+    if (a.q.cs != kAttnKD * a.n || a.k.cs != kAttnKD * a.n || a.v.cs != kAttnHD * a.n || a.y.cs != kAttnHD * a.n)
+      throw std::runtime_error("attention head strides");
+    const long qk = (long)a.heads * kAttnKD * a.n, vy = (long)a.heads * kAttnHD * a.n;
+    check(a.q.ptr, 0, (long)(a.batch - 1) * a.q.img + qk - 1, 2, "attention q");
+    check(a.k.ptr, 0, (long)(a.batch - 1) * a.k.img + qk - 1, 2, "attention k");
+    check(a.v.ptr, 0, (long)(a.batch - 1) * a.v.img + vy - 1, 2, "attention v");
+    check(a.y.ptr, 0, (long)(a.batch - 1) * a.y.img + vy - 1, 2, "attention y");
+    return;
+  }
   if (l.kind == Launch::kDecode) {
     const DecodeParams & d = l.dp;
     if (d.batch < 1 || d.batch > 65535 || d.nscale < 1 || d.nscale > 4) throw std::runtime_error("decode grid");
@@ -1787,6 +1914,7 @@ void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
     case Launch::kDirect: launch_conv_direct(l.cp, stream_); break;
     case Launch::kDw: launch_dwconv(l.cp, stream_); break;
     case Launch::kDecode: launch_pose_decode(l.dp, stream_); break;
+    case Launch::kAttn: launch_attention(l.ap, stream_); break;
     default: launch_small(l.small, l.sp, stream_); break;
     }
   }
@@ -2045,6 +2173,7 @@ std::string Model::nodeKernel(int i)
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";
+  case Launch::kAttn: return "attention";
   case Launch::kSmall:
     if (l.small == kMaxPoolSppf) return "maxpool_sppf";
     return s.kernel;
@@ -2089,6 +2218,10 @@ void Model::buildStats()
         const Tensor & at = *T_[n.ins[0]];
         const Tensor & bt = *T_[n.ins[1]];
         s.flops = 2.0 * at.numel * (double)bt.dims.back();
+      }
+      if (n.op == "attention") {
+        const double N = n.i("n"), h = n.i("heads");
+        s.flops = h * (2.0 * N * N * kAttnKD + 2.0 * kAttnHD * N * N);
       }
       if (n.op == "pose_decode")
         std::snprintf(buf, sizeof(buf), "pose_decode %d scales, %d anchors, R %d, %d classes, %d keypoints -> %s",

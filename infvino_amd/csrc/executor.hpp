@@ -26,11 +26,12 @@ struct PlanNode {
 
 // One kernel launch with everything resolved for a given batch size.
 struct Launch {
-  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode } kind = kSmall;
+  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode, kAttn } kind = kSmall;
   int small = 0;
   ConvParams cp;
   SmallParams sp;
   DecodeParams dp;
+  AttnParams ap;
 };
 
 struct NodeStat {
@@ -93,6 +94,7 @@ class Model {
   void fuseResidual();
   void fuseActivation();
   void fusePermuteMatmul();
+  void fuseAttention();
   void plan();
   int chanBroadcast(const PlanNode & n) const;
   void assignViews();

@@ -108,6 +108,16 @@ struct SmallParams {
   int dims[18] = {0};          // ew_binary broadcast spec (rank <= 6)
 };
 
+// Fused attention core (q^T k, * scale, softmax, v P^T) of one node per head batch: q, k
+// [heads][kAttnKD][n], v, y [heads][kAttnHD][n] per image, NCHW views with cs = one head's
+// block; scale is the plan's fp16 scalar as fp32.
+constexpr int kAttnKD = 32, kAttnHD = 64, kAttnMaxN = 512;
+struct AttnParams {
+  View q, k, v, y;
+  int batch = 1, heads = 1, n = 0;
+  float scale = 1.0f;
+};
+
 // Fused Detect / Pose head decode: per-scale head tensors in, [4 + nc + 3 nk][A] out per image
 // (the plan's decode tail, matched by the executor).  Anchor a of scale s is pixel a - off[s]
 // of that scale's tensors.

@@ -82,6 +82,8 @@ enum SmallOp : int {
 };
 void launch_small(int kind, const SmallParams & p, hipStream_t s);
 void launch_pose_decode(const DecodeParams & p, hipStream_t s);  // fused head decode
+void launch_attention(const AttnParams & a, hipStream_t s);      // fused attention core
+int attn_key_blocks(int n);  // key blocks of 32 the fused attention kernel holds (0: n too large)
 void launch_bmm_mfma(const SmallParams & q, hipStream_t s);  // bmm_mfma.hip
 
 // boundary conversions (include/infvino/Half.hpp semantics for the truncating one)

@@ -369,3 +369,20 @@ def test_conv1x1_planar_input(tmp_path, cin, cout, hw, batch):
     _check_f32(path, batch, lo=-1.0)
     if kern == "conv_igemm_sk":
         _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
+
+
+@pytest.mark.parametrize("C,H,heads,batch", [(256, 20, 4, 3), (128, 20, 2, 2), (256, 16, 4, 2), (128, 12, 2, 3),
+                                             (128, 8, 2, 5)])
+def test_attention_fused(tmp_path, C, H, heads, batch):
+    """The C2PSA attention block (ultralytics Attention: qkv 1x1, q^T k * scale, softmax,
+    v P^T, + depthwise positional conv, 1x1 projection) with the core as one fused kernel,
+    against the oracle and against the same plan run node by node (IVH_FLAG_NO_FUSE_ATTN);
+    400 / 256 / 144 / 64 tokens (13 / 8 / 5 / 2 key blocks of 32)."""
+    path, _ = pw.c2psa_attention(str(tmp_path), C=C, H=H, heads=heads)
+    assert "attention" in _kernels(path, batch)
+    assert "attention" not in _kernels(path, batch, ia.IVH_FLAG_NO_FUSE_ATTN)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, nodes = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_FUSE_ATTN)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(nodes[0]))
+    print(f"fused vs node by node: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < 1e-3 and max_rel < 5e-3
