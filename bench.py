@@ -15,7 +15,9 @@ table goes to stderr.
   config1        the single pointwise conv (64->128 at 80x80, SiLU) at batch 1 and 64, with
                  its roofline (HBM bound)
   conv_sweep     the conv operator sweep (stem, strided / stride-1 3x3, depthwise) at batch
-                 64 and batch 1: per layer time, TFLOP/s, GB/s and fraction of its binding roof
+                 64 and batch 1, and the depthwise layers at batch 256: per layer time,
+                 TFLOP/s, GB/s and fraction of its binding roof (MFMA, HBM, or for depthwise
+                 the fp32 VALU)
   attention      the C2PSA attention block at 256 channels, 4 heads, head_dim 64, 400 tokens
                  (q^T k, softmax, v attn^T) at batch 64 and 1, with its roofline
   other_models   YOLOv8n-pose 640 (batch 16 / 64), MobileNetV3-small 224 (batch 1 / 32 / 256)
@@ -40,6 +42,10 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# Vector fp32 FMA without packed fp32 (which this build does not use): one FMA per lane per
+# cycle, 256 CUs x 64 lanes x 2 FLOPs x 2.4 GHz.  The roof of the depthwise convs, which run
+# on the VALU (v_fma_mix_f32) rather than on MFMA.
+PEAK_VALU_FP32_TFLOPS = 78.6
 
 
 def log(*a):
@@ -87,16 +93,20 @@ def layer_runs(ia, pw, name, batch, iters, flags=0):
     log(f"[bench] layer {name} batch {batch}: {iters} passes")
 
 
-def conv_sweep(ia, pw, batch, iters):
+def conv_sweep(ia, pw, batch, iters, only=None):
     """The conv operator sweep (stem, strided and stride-1 3x3, depthwise) at `batch`, each
     conv measured in the layout it has inside a model: the stem reads the NCHW graph input,
     every other conv sits between two ReLUs so its input and output are internal
     (channels-last) tensors.  Per layer: HIP-event time of the conv node, algorithmic
-    TFLOP/s and GB/s, and the fraction of the roof that binds it (MFMA when its arithmetic
-    intensity is above the ridge, HBM otherwise)."""
+    TFLOP/s and GB/s, and the fraction of the roof that binds it: for the MFMA convs MFMA
+    when the arithmetic intensity is above the ridge, HBM otherwise; for the depthwise convs
+    (vector FMAs) the larger of the HBM time and the fp32 VALU time.  `only`: a prefix of the
+    layer names to keep."""
     ridge = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     rows = []
     for name, cin, cout, H, W, k, s, g, act in pw.CONV_SWEEP:
+        if only and not name.startswith(only):
+            continue
         with tempfile.TemporaryDirectory() as d:
             m = ia.PlanModel(sweep_plan(pw, d, name), 0, batch, ia.IVH_FLAG_NO_GRAPH)
             x0 = np.random.default_rng(0).random(m.inputNumel() * batch, dtype=np.float32)
@@ -108,13 +118,17 @@ def conv_sweep(ia, pw, batch, iters):
             m.close()
         fl, by = inf["flops"] * batch, inf["bytes"] * batch
         tf, gbs = fl / t / 1e12, by / t / 1e9
-        mfma = fl / by >= ridge
+        if inf["kernel"] == "dwconv":
+            t_valu, t_hbm = fl / (PEAK_VALU_FP32_TFLOPS * 1e12), by / (PEAK_HBM_GBS * 1e9)
+            bound = "valu" if t_valu > t_hbm else "hbm"
+            frac = max(t_valu, t_hbm) / t
+        else:
+            bound = "mfma" if fl / by >= ridge else "hbm"
+            frac = tf / PEAK_FP16_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
         rows.append({"layer": name, "kernel": inf["kernel"], "us": round(t * 1e6, 2),
-                     "tflops": round(tf, 1), "gbs": round(gbs, 1),
-                     "bound": "mfma" if mfma else "hbm",
-                     "frac": round(tf / PEAK_FP16_TFLOPS if mfma else gbs / PEAK_HBM_GBS, 4)})
+                     "tflops": round(tf, 1), "gbs": round(gbs, 1), "bound": bound, "frac": round(frac, 4)})
         log(f"[sweep] {name:24s} b{batch} {inf['kernel']:12s} {t * 1e6:8.2f} us {tf:7.1f} TFLOP/s "
-            f"{gbs:7.1f} GB/s -> {rows[-1]['bound']} {rows[-1]['frac'] * 100:.1f}%")
+            f"{gbs:7.1f} GB/s -> {bound} {frac * 100:.1f}%")
     return rows
 
 
@@ -417,7 +431,10 @@ def main():
     m1.close()
 
     c1 = None if args.no_sweep else config1(ia, pw, max(args.profile_iters, 10))
-    sweep = None if args.no_sweep else {f"b{b}": conv_sweep(ia, pw, b, max(args.profile_iters, 10)) for b in (B, 1)}
+    sweep = None
+    if not args.no_sweep:
+        sweep = {f"b{b}": conv_sweep(ia, pw, b, max(args.profile_iters, 10)) for b in (B, 1)}
+        sweep["dw_b256"] = conv_sweep(ia, pw, 256, max(args.profile_iters, 10), only="dw")
     attn = None if args.no_sweep else attention(ia, pw, max(args.profile_iters, 10))
     others = None if args.no_models else model_lines(
         ia, pw, [("yolov8n-pose", 640, (16, 64)), ("mobilenetv3-small", 224, (1, 32, 256)),

@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
   __shared__ __attribute__((aligned(16))) _Float16 Qt[QW * KTP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z, N = a.n, n8 = N / 8;
+  const int h = blockIdx.y, b = blockIdx.z, N = a.n;
   const int q0 = blockIdx.x * QW;
   const _Float16 * qp = reinterpret_cast<const _Float16 *>(a.q.ptr) + (long)b * a.q.img + (long)h * a.q.cs;
   const _Float16 * kp = reinterpret_cast<const _Float16 *>(a.k.ptr) + (long)b * a.k.img + (long)h * a.k.cs;

@@ -22,7 +22,7 @@ constexpr unsigned kBufOOB = 0x80000000u;
 __device__ __forceinline__ int idiv_small(int n, int d, float inv)
 {
   int q = (int)((float)n * inv);
-  const int r = n - q * d;
+  const int r = n - (int)__umul24((unsigned)q, (unsigned)d);  // q, d < 2^24: a full-rate multiply
   q += (r >= d) - (r < 0);
   return q;
 }

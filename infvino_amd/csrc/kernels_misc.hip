@@ -5,6 +5,10 @@
 #include "conv_common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <type_traits>
 #include <initializer_list>
 #include <map>
 #include <mutex>
@@ -424,11 +428,194 @@ void launch_conv_direct(const ConvParams & p, hipStream_t s)
 // ------------------------------------------------------------------- depthwise
 // Restates depthwise_f16 / depthwise_v / depthwise_blk (kernels/conv_general.cl:85-187,
 // depthwise_blk.cl:118-228): y[c] = act(sum_k x[c]*w[c] + b[c]), K in {3,5}, S in {1,2}.
-// NHWC vector path: one lane = a strip of output pixels x 8 channels, 16-byte loads/stores,
-// fp32 accumulation.  Weights [K][K][C] as fp16 (the plan's values; one 16-byte load per tap
-// for 8 channels) for this kernel, as fp32 for the any-layout one.
+//
+// Channels-last tiled kernel.  A tile is TOH x TOW output pixels x 8G channels of one
+// image; its input window with the halo, ((TOH-1)S+K) x ((TOW-1)S+K) pixels x 8G channels,
+// is loaded into LDS with 16-byte buffer loads (consecutive lanes read consecutive 16-byte
+// pieces of the NHWC rows; pixels outside the image are loads past the buffer's range,
+// which return zeros, so the taps need no bound checks), together with the tile's
+// [K][K][8G] fp16 weights.  Each lane computes a PY x PX block of output pixels for 8
+// channels: its K*K weights stay in registers, each input row of its block is read from LDS
+// once and applied to every output row and column that uses it (sliding window), with fp32
+// accumulation (fp16 operands into v_fma_mix_f32) in (ky, kx) order.
+//
+// One work-group per tile.  Measured on MI355X, this beats a persistent grid that double-
+// buffers the window (two work-groups per CU, the next tile's loads in flight during the
+// FMAs): the FMAs and LDS reads need more waves per SIMD than that leaves to hide their
+// latencies, and several single-tile work-groups per CU overlap one's loads with another's
+// FMAs anyway.
+struct DwTile {
+  int G, BX, BY;      // 8-channel groups per tile; lane blocks along x and y
+  int ntx, nty, nct;  // tiles along x, along y, channel tiles
+  int IW, IH;         // input window of a tile, pixels
+};
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// acc + a.h * b.h in fp32 with one rounding, a and b fp16 halves (h = 0: low, 1: high) of
+// one dword each: v_fma_mix_f32 converts its fp16 operands exactly, so this equals
+// fmaf((float)a.h, (float)b.h, acc).  Written out because the compiler otherwise converts
+// every register-resident weight to fp32 once (8 more VGPRs per tap) and uses v_fmac_f32.
+template <int H>
+__device__ __forceinline__ void fma_mix(float & acc, unsigned a, unsigned b)
+{
+  if (H == 0) asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,1,0]" : "+v"(acc) : "v"(a), "v"(b));
+  else asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+// LDS pieces (16 bytes) of the depthwise window and weights: at most kDwMaxIt per lane, all
+// loaded into registers before the first LDS store (64 KiB)
+constexpr int kDwMaxIt = 16;
+constexpr int kDwBufPieces = kDwMaxIt * 256;
+constexpr int kDwMaxW = 4;  // weight pieces per lane: K*K*G <= 1024
+
+template <int K, int S, int PX, int PY, int ACT>
+__global__ void __launch_bounds__(256) dw_tile_kernel(const ConvParams p, const DwTile t)
+{
+  extern __shared__ __align__(16) unsigned char dw_lds[];
+  constexpr int NX = (PX - 1) * S + K;  // input columns of a lane's block
+  constexpr int NR = (PY - 1) * S + K;  // input rows of a lane's block
+  const int tid = threadIdx.x, G = t.G;
+  const int npix = t.IH * t.IW * G;  // window pieces
+  int w = blockIdx.x;
+  const int tx = w % t.ntx;
+  w /= t.ntx;
+  const int ty = w % t.nty;
+  w /= t.nty;
+  const int tc = w % t.nct, b = w / t.nct;
+  const int ox0 = tx * t.BX * PX, oy0 = ty * t.BY * PY;
+  const int ix0 = ox0 * S - p.P, iy0 = oy0 * S - p.P, c0 = tc * G * 8;
+
+  // this image's input view from channel c0 on, up to its last element
+  const __half * xb = p.x.ptr + (long)b * p.x.img + c0;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(xb), (short)0, (int)((((long)p.H * p.W - 1) * p.x.cs + p.Cin - c0) * 2), kBufDword3);
+  const h8 * wg = reinterpret_cast<const h8 *>(p.w2) + tc * G;
+  h8 * const xs = reinterpret_cast<h8 *>(dw_lds);  // [IH][IW][G] window pieces, then [K*K][G] weights
+  // window piece i = tid + 256 u: row i / RP of the window, piece rem = i % RP of that row
+  // (column rem / G, group rem % G); pieces outside the image load from past the buffer
+  const int RP = t.IW * G, nit = (npix + 255) >> 8;
+  const float inv_rp = __builtin_amdgcn_rcpf((float)RP), inv_g = __builtin_amdgcn_rcpf((float)G);
+  const int jlo = max(0, -ix0) * G, jhi = (p.W - ix0) * G;  // a row's pieces inside the image
+  // byte offsets: window origin (may be negative; only in-image pieces use it), one image row,
+  // one pixel; 24-bit multiplies (full rate) suffice, the host keeps an image below 2^31 bytes
+  // and its pixel count below 2^24
+  const int base0 = (iy0 * p.W + ix0) * p.x.cs * 2, rowb = p.W * p.x.cs * 2, pixb = p.x.cs * 2;
+  h8 v[kDwMaxIt];
+  auto load_window = [&](auto contig) {
+#pragma unroll
+    for (int u = 0; u < kDwMaxIt; ++u) {
+      if (u < nit) {
+        const int i = tid + u * 256;
+        const int row = idiv_small(i, RP, inv_rp), rem = i - (int)__umul24(row, RP), iy = iy0 + row;
+        int off = base0 + (int)__umul24(row, rowb);
+        if (decltype(contig)::value) {
+          off += rem * 16;  // whole pixels: the window row is one run of RP pieces
+        } else {
+          const int col = idiv_small(rem, G, inv_g);
+          off += (int)__umul24(col, pixb) + (rem - (int)__umul24(col, G)) * 16;
+        }
+        const bool in = i < npix && (unsigned)iy < (unsigned)p.H && rem >= jlo && rem < jhi;
+        v[u] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, in ? (unsigned)off : kBufOOB, 0, 0));
+      }
+    }
+  };
+  if (p.x.cs == 8 * G) load_window(std::true_type{});
+  else load_window(std::false_type{});
+  // weights: K*K*G pieces (at most kDwMaxW per lane)
+  const int nw = K * K * G;
+  h8 wv[kDwMaxW];
+#pragma unroll
+  for (int u = 0; u < kDwMaxW; ++u) {
+    const int i = tid + u * 256;
+    if (i < nw) {
+      const int tap = idiv_small(i, G, inv_g);
+      wv[u] = wg[(int)__umul24(tap, p.Cin >> 3) + i - (int)__umul24(tap, G)];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kDwMaxIt; ++u) {
+    const int i = tid + u * 256;
+    if (u < nit && (u < nit - 1 || i < npix)) xs[i] = v[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kDwMaxW; ++u)
+    if (tid + u * 256 < nw) xs[npix + tid + u * 256] = wv[u];
+  __syncthreads();
+  if (tid >= G * t.BX * t.BY) return;
+
+  const int q = tid / G, g = tid - q * G;
+  const int by = q / t.BX, bx = q - by * t.BX;
+  u32x4 wr[K * K];
+#pragma unroll
+  for (int k = 0; k < K * K; ++k) wr[k] = __builtin_bit_cast(u32x4, xs[npix + k * G + g]);
+  float acc[PY][PX][8];
+#pragma unroll
+  for (int i = 0; i < PY; ++i)
+#pragma unroll
+    for (int j = 0; j < PX; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[i][j][e] = 0.0f;
+  const h8 * base = xs + ((by * PY * S) * t.IW + bx * PX * S) * G + g;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    u32x4 xv[NX];
+#pragma unroll
+    for (int c = 0; c < NX; ++c) xv[c] = __builtin_bit_cast(u32x4, base[(r * t.IW + c) * G]);
+#pragma unroll
+    for (int i = 0; i < PY; ++i) {
+      const int ky = r - i * S;
+      if (ky < 0 || ky >= K) continue;
+#pragma unroll
+      for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+        for (int j = 0; j < PX; ++j)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            fma_mix<0>(acc[i][j][2 * d], xv[j * S + kx][d], wr[ky * K + kx][d]);
+            fma_mix<1>(acc[i][j][2 * d + 1], xv[j * S + kx][d], wr[ky * K + kx][d]);
+          }
+    }
+  }
+
+  const int c = c0 + g * 8;
+  float bv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (p.bias) {
+    const float4 b0 = *reinterpret_cast<const float4 *>(p.bias + c), b1 = *reinterpret_cast<const float4 *>(p.bias + c + 4);
+    bv[0] = b0.x; bv[1] = b0.y; bv[2] = b0.z; bv[3] = b0.w;
+    bv[4] = b1.x; bv[5] = b1.y; bv[6] = b1.z; bv[7] = b1.w;
+  }
+  _Float16 * yb = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + c;
+  const _Float16 * rb = p.r.ptr ? reinterpret_cast<const _Float16 *>(p.r.ptr) + (long)b * p.r.img + c : nullptr;
+#pragma unroll
+  for (int i = 0; i < PY; ++i) {
+    const int oy = oy0 + by * PY + i;
+#pragma unroll
+    for (int j = 0; j < PX; ++j) {
+      const int ox = ox0 + bx * PX + j;
+      if (oy >= p.Ho || ox >= p.Wo) continue;
+      const long hw = (long)oy * p.Wo + ox;
+      h8 out;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (_Float16)act_fast<ACT>(acc[i][j][e] + bv[e]);
+      if (rb) {  // act, one rounding, then the residual (the reference order)
+        const h8 rv = *reinterpret_cast<const h8 *>(rb + hw * p.r.cs);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = (_Float16)((float)out[e] + (float)rv[e]);
+      }
+      *reinterpret_cast<h8 *>(yb + hw * p.y.cs) = out;
+    }
+  }
+}
+
+// Strip kernel for the 5x5 stride-2 layers at large batch: one lane = 8 channels x a strip
+// of PX = 4 output pixels of one row, straight from global memory (L1/L2) into registers,
+// each loaded input column reused by the strip's taps, no LDS.  With stride 2 the tiled
+// kernel's window is about 4x its output tile and every tap is an LDS read; measured on
+// MI355X (72 channels, 28x28 -> 14x14, batch 256) this kernel takes 11.7 us against the
+// tiled kernel's 15.5, while at batch 64 the tiled kernel wins (6.7 against 7.5 us).
 template <int K, int S, int PX, int ACT>
-__global__ void __launch_bounds__(256) dw_nhwc_kernel(const ConvParams p, FastDiv d_c8, FastDiv d_strip, FastDiv d_ho)
+__global__ void __launch_bounds__(256) dw_strip_kernel(const ConvParams p, FastDiv d_c8, FastDiv d_strip, FastDiv d_ho)
 {
   // lane = (8-channel group, strip of PX output pixels of one row), channel groups fastest so
   // that neighbouring lanes read and write neighbouring 16-byte pieces
@@ -526,50 +713,169 @@ bool dwconv_vectorizable(const ConvParams & p)
   };
   return p.w2 && (reinterpret_cast<uintptr_t>(p.w2) & 15) == 0 && (p.Cin % 8) == 0 && (p.K == 3 || p.K == 5) &&
          (p.S == 1 || p.S == 2) && al(p.x) && al(p.y) &&
-         (!p.r.ptr || al(p.r)) && (long)p.batch * p.Ho * p.Wo * (p.Cin / 8) < (1L << 31);
+         (!p.r.ptr || al(p.r)) && (long)p.batch * p.Ho * p.Wo * (p.Cin / 8) < (1L << 31) &&
+         (((long)p.H * p.W - 1) * p.x.cs + p.Cin) * 2 < (1L << 31) &&  // one image's buffer range
+         (long)p.H * p.W < (1L << 24);
 }
 
-// Output pixels per lane of the channels-last depthwise kernel (a strip of one row;
-// measured on MI355X: one pixel per lane 70 us, four 32 us for 64 channels at 80x80, batch
-// 64 -- neighbouring taps are reused from registers; eight is slower on the 5x5 layers).
-constexpr int kDwPx = 4;
+// Tile choice for dw_tile_kernel.  Candidates: per-lane blocks PX x PY of at most two
+// pixels (larger blocks measured slower on MI355X: fewer waves, longer dependent FMA
+// chains), channel groups G = Cin/8 (whole pixels: a window row is one contiguous run) or a
+// divisor of it of at least 8 (runs of 128 bytes or more), lane blocks BX x BY (at most 256
+// lanes, window and weights within kDwBufPieces).  Cost: the largest of the VALU cycles per
+// SIMD (4 cycles per wave64 instruction, FMAs plus staging), the LDS cycles per CU (128
+// bytes per cycle, window stores plus block and weight reads) and the HBM bytes at 2500 per
+// shader cycle (about 5 TB/s), halo re-reads at four times that.  Launches with at least
+// 2.5 waves per SIMD hide their load latency; below that the candidate with the most waves
+// is taken (small batches); among those with enough, work-groups of two or more waves, then
+// the cheapest.
+struct DwPick {
+  int PX = 0, PY = 0;
+  DwTile t{};
+  size_t lds = 0;
+};
 
-template <int K, int S, int ACT>
-static void launch_dw_t(const ConvParams & p, hipStream_t s)
+static DwPick dw_pick_search(const ConvParams & p)
 {
-  constexpr int PX = kDwPx;
-  const int nstrip = (p.Wo + PX - 1) / PX;
-  const long n = (long)p.batch * p.Ho * nstrip * (p.Cin / 8);
-  hipLaunchKernelGGL((dw_nhwc_kernel<K, S, PX, ACT>), dim3(nblk(n, 256)), dim3(256), 0, s, p,
-                     fastdiv_make((unsigned)(p.Cin / 8)), fastdiv_make((unsigned)nstrip), fastdiv_make((unsigned)p.Ho));
+  const int C8 = p.Cin / 8, K = p.K, S = p.S;
+  const double hbm = (double)p.batch * ((double)p.H * p.W + (double)p.Ho * p.Wo) * p.Cin * 2.0;
+  constexpr double kEnoughWaves = 2.5 * 1024;
+  DwPick best;
+  double best_cost = 1e300, best_wk = 0.0;
+  bool best_big = false;
+  for (const int PX : {1, 2}) {
+    for (const int PY : {1, 2}) {
+      if (PX * PY > 2) continue;
+      const int nbx = (p.Wo + PX - 1) / PX, nby = (p.Ho + PY - 1) / PY;
+      const int NR = (PY - 1) * S + K, NX = (PX - 1) * S + K;
+      for (int G = 1; G <= C8; ++G) {
+        if (C8 % G || (G < C8 && G < 8)) continue;
+        for (int sx = 1, last_bx = 0; sx <= nbx && sx <= 16; ++sx) {
+          const int BX = (nbx + sx - 1) / sx;
+          if (BX == last_bx) continue;
+          last_bx = BX;
+          for (int sy = 1, last_by = 0; sy <= nby && sy <= 64; ++sy) {
+            const int BY = (nby + sy - 1) / sy;
+            if (BY == last_by) continue;
+            last_by = BY;
+            const int lanes = G * BX * BY;
+            if (lanes > 256) continue;
+            const int IW = (BX * PX - 1) * S + K, IH = (BY * PY - 1) * S + K;
+            const int nbuf = (IH * IW + K * K) * G;
+            if (nbuf > kDwBufPieces || K * K * G > kDwMaxW * 256) continue;
+            const int ntx = (p.Wo + BX * PX - 1) / (BX * PX), nty = (p.Ho + BY * PY - 1) / (BY * PY);
+            const double nwg = (double)ntx * nty * (C8 / G) * p.batch;
+            if (nwg >= 2147483648.0) continue;
+            const double waves = nwg * ((lanes + 63) / 64);
+            const double valu = waves * (PX * PY * K * K * 8 + ((nbuf + 255) / 256) * 25 + 150) * 4.0 / 1024.0;
+            const double lds = nwg * (nbuf + (double)lanes * (NR * NX + K * K)) * 16.0 / (256.0 * 128.0);
+            const double mem = hbm / 2500.0 + nwg * IH * IW * G * 16.0 / 10000.0;
+            const double cost = std::max(valu, std::max(lds, mem));
+            // rank: waves up to enough; then work-groups of at least two waves (one-wave
+            // groups pay the staging latency for a quarter of the lanes); then cost
+            const double wk = std::min(waves, kEnoughWaves);
+            const bool big = lanes >= 128;
+            const bool better = best.PX == 0 || wk > best_wk || (wk == best_wk && big > best_big) ||
+                                (wk == best_wk && big == best_big && cost < best_cost);
+            if (better) {
+              best_cost = cost;
+              best_wk = wk;
+              best_big = big;
+              best.PX = PX;
+              best.PY = PY;
+              best.t = DwTile{G, BX, BY, ntx, nty, C8 / G, IW, IH};
+              best.lds = (size_t)nbuf * 16;
+            }
+          }
+        }
+      }
+    }
+  }
+  return best;
+}
+
+// The search costs a few microseconds per call; eager runs call it every launch, so the
+// picks are kept per shape.
+static DwPick dw_pick(const ConvParams & p)
+{
+  static std::mutex mu;
+  static std::map<std::array<int, 7>, DwPick> cache;
+  const std::array<int, 7> key{p.Cin, p.H, p.W, p.K, p.S, p.P, p.batch};
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  const DwPick d = dw_pick_search(p);
+  cache.emplace(key, d);
+  return d;
+}
+
+template <int K, int S, int PX, int PY>
+static void launch_dw_tile(const ConvParams & p, const DwPick & d, hipStream_t s)
+{
+  const unsigned nwg = (unsigned)((long)d.t.ntx * d.t.nty * d.t.nct * p.batch);
+  switch (p.act) {
+#define IVH_DW_CASE(A)                                                                                     \
+  case A: hipLaunchKernelGGL((dw_tile_kernel<K, S, PX, PY, A>), dim3(nwg), dim3(256), d.lds, s, p, d.t); break;
+  IVH_DW_CASE(kActSiLU)
+  IVH_DW_CASE(kActReLU)
+  IVH_DW_CASE(kActHSwish)
+  IVH_DW_CASE(kActHSigmoid)
+  IVH_DW_CASE(kActSigmoid)
+  default: hipLaunchKernelGGL((dw_tile_kernel<K, S, PX, PY, kActNone>), dim3(nwg), dim3(256), d.lds, s, p, d.t); break;
+#undef IVH_DW_CASE
+  }
 }
 
 template <int K, int S>
-static void launch_dw_act(const ConvParams & p, hipStream_t s)
+static void launch_dw_ks(const ConvParams & p, const DwPick & d, hipStream_t s)
 {
-  switch (p.act) {
-  case kActSiLU: launch_dw_t<K, S, kActSiLU>(p, s); break;
-  case kActReLU: launch_dw_t<K, S, kActReLU>(p, s); break;
-  case kActHSwish: launch_dw_t<K, S, kActHSwish>(p, s); break;
-  case kActHSigmoid: launch_dw_t<K, S, kActHSigmoid>(p, s); break;
-  case kActSigmoid: launch_dw_t<K, S, kActSigmoid>(p, s); break;
-  default: launch_dw_t<K, S, kActNone>(p, s); break;
-  }
+  if (d.PX == 2) launch_dw_tile<K, S, 2, 1>(p, d, s);
+  else if (d.PY == 2) launch_dw_tile<K, S, 1, 2>(p, d, s);
+  else launch_dw_tile<K, S, 1, 1>(p, d, s);
+}
+
+template <int ACT>
+static void launch_dw_strip(const ConvParams & p, hipStream_t s)
+{
+  constexpr int PX = 4;
+  const int nstrip = (p.Wo + PX - 1) / PX;
+  const long n = (long)p.batch * p.Ho * nstrip * (p.Cin / 8);
+  hipLaunchKernelGGL((dw_strip_kernel<5, 2, PX, ACT>), dim3(nblk(n, 256)), dim3(256), 0, s, p,
+                     fastdiv_make((unsigned)(p.Cin / 8)), fastdiv_make((unsigned)nstrip), fastdiv_make((unsigned)p.Ho));
+}
+
+// The strip kernel is taken for 5x5 stride 2 once it has at least 1.5 waves per SIMD.
+static bool dw_use_strip(const ConvParams & p)
+{
+  return p.K == 5 && p.S == 2 && (long)p.batch * p.Ho * ((p.Wo + 3) / 4) * (p.Cin / 8) >= 1536L * 64;
 }
 
 void launch_dwconv(const ConvParams & p, hipStream_t s)
 {
   const long M = (long)p.batch * p.Ho * p.Wo;
-  if (dwconv_vectorizable(p)) {
-    if (p.K == 3) {
-      if (p.S == 1) launch_dw_act<3, 1>(p, s);
-      else launch_dw_act<3, 2>(p, s);
-    } else {
-      if (p.S == 1) launch_dw_act<5, 1>(p, s);
-      else launch_dw_act<5, 2>(p, s);
-    }
-  } else {
+  if (!dwconv_vectorizable(p)) {
     hipLaunchKernelGGL(dw_generic_kernel, dim3(nblk(M * p.Cin, 256)), dim3(256), 0, s, p);
+    return;
+  }
+  if (dw_use_strip(p)) {
+    switch (p.act) {
+    case kActSiLU: launch_dw_strip<kActSiLU>(p, s); break;
+    case kActReLU: launch_dw_strip<kActReLU>(p, s); break;
+    case kActHSwish: launch_dw_strip<kActHSwish>(p, s); break;
+    case kActHSigmoid: launch_dw_strip<kActHSigmoid>(p, s); break;
+    case kActSigmoid: launch_dw_strip<kActSigmoid>(p, s); break;
+    default: launch_dw_strip<kActNone>(p, s); break;
+    }
+    return;
+  }
+  const DwPick d = dw_pick(p);
+  if (d.PX == 0) throw std::runtime_error("depthwise: no tile fits");
+  if (p.K == 3) {
+    if (p.S == 1) launch_dw_ks<3, 1>(p, d, s);
+    else launch_dw_ks<3, 2>(p, d, s);
+  } else {
+    if (p.S == 1) launch_dw_ks<5, 1>(p, d, s);
+    else launch_dw_ks<5, 2>(p, d, s);
   }
 }
 

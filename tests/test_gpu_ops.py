@@ -243,6 +243,25 @@ def test_depthwise(tmp_path, c, hw, k, s, act, internal):
     _check_f32(path, 2, lo=-1.0)
 
 
+@pytest.mark.parametrize("c,hw,k,s,batches", [
+    (16, 112, 3, 2, (1, 6)), (64, 80, 3, 1, (1, 3)), (240, 14, 5, 1, (1, 9)), (576, 7, 5, 1, (1, 5)),
+    (88, 28, 3, 1, (2, 4)), (120, 33, 5, 2, (1, 3)), (8, 61, 5, 1, (1, 2)), (40, 45, 3, 2, (3, 1)),
+    (96, 56, 5, 2, (48, 1))])  # batch 48: the 5x5 stride-2 strip kernel; batch 1: tiled
+def test_depthwise_tiles(tmp_path, c, hw, k, s, batches):
+    """Channels-last depthwise over tile grids with ragged right and bottom edges, several
+    channel tiles and sizes whose tile choice (or kernel) changes with the batch: every batch
+    size agrees with the oracle, and image 0 is bit-identical across batch sizes (the
+    per-pixel sum order does not depend on the tile or kernel)."""
+    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=pw.ACT_HSWISH, pre_relu=True)
+    outs = []
+    for b in batches:
+        assert _conv_kernel(path, b) == "dwconv"
+        outs.append(_check_f32(path, b, lo=-1.0, ref_mode=False)[0])
+    n0 = outs[0].size // batches[0]
+    for o, b in zip(outs[1:], batches[1:]):
+        assert np.array_equal(o[:n0], outs[0][:n0])
+
+
 def _small_plan(d, build):
     pb = pw.PlanBuilder(str(d), seed=3)
     out = build(pb)
