@@ -101,6 +101,7 @@ public:
   {
     int index = 0;
     std::string op, kernel, tag;
+    std::string launch;  // kernel label and launch detail (ivh_node_tag)
     double ms = 0.0, flops = 0.0, bytes = 0.0;
     int calls = 0;
   };
@@ -162,6 +163,9 @@ private:
       rows[i].op = op;
       rows[i].kernel = kern;
       rows[i].tag = desc;
+      char lt[256];
+      check(ivh_node_tag(m_, i, lt, sizeof lt));
+      rows[i].launch = lt;
     }
     return rows;
   }

@@ -24,6 +24,7 @@
  *   ivh_last_run_ms       PlanModel::lastRunMs / ClBackend::lastInferMs, PlanModel.hpp:176, ClBackend.hpp:47
  *   ivh_profile_nodes     PlanModel::profile() per-node GPU time, PlanModel.hpp:201-224
  *   ivh_node_info         PlanModel::PlanProfile::NodeRow (op, tag, signature), PlanModel.hpp:203-211
+ *   ivh_node_tag          PlanModel::PlanProfile::NodeRow::tag (shape and data path), PlanModel.hpp:208
  *   ivh_device_info       ClBackend::device() / describeDevice, ClBackend.hpp:46, include/infvino/Device.hpp
  *   ivh_runtime_version   DeviceInfo::opencl_version, include/infvino/Device.hpp:23
  *   ivh_node_times        PlanModel::profile() / opProfile() accumulated under profiling=true,
@@ -125,6 +126,10 @@ int ivh_clear_profile(ivh_model * m);  /* PlanModel::clearProfile, PlanModel.hpp
 /* node i: op, kernel family and shape text; algorithmic FLOPs and fp16 bytes per image */
 int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel, size_t kernel_len,
                   char * desc, size_t desc_len, double * flops, double * bytes);
+/* Runtime tag of node i: the kernel label of ivh_node_info followed by its launch detail
+ * (tile config, channel chunk, K step, split, build), as PlanProfile::NodeRow::tag carries the
+ * data path (include/infvino/PlanModel.hpp:208). */
+int ivh_node_tag(ivh_model * m, int i, char * tag, size_t tag_len);
 int ivh_memory_info(const ivh_model * m, int batch, size_t * arena_bytes, size_t * weight_bytes);
 
 /* ---------------------------------------------------------------- single-op entry points

@@ -76,6 +76,7 @@ SIGNATURES = {
     "ivh_node_times": (_i, [_vp, _dp, _ip, _i]),
     "ivh_clear_profile": (_i, [_vp]),
     "ivh_node_info": (_i, [_vp, _i, C.c_char_p, _sz, C.c_char_p, _sz, C.c_char_p, _sz, _dp, _dp]),
+    "ivh_node_tag": (_i, [_vp, _i, C.c_char_p, _sz]),
     "ivh_memory_info": (_i, [_vp, _i, _szp, _szp]),
     # single-op entry points (device pointers as integers, stream None = null stream)
     "ivh_conv_out_dims": (_i, [_cdp, _ip, _ip]),
@@ -255,6 +256,12 @@ class PlanModel:
         _check(lib().ivh_node_info(self._h, i, op, 64, kern, 64, desc, 256, C.byref(fl), C.byref(by)))
         return {"op": op.value.decode(), "kernel": kern.value.decode(), "desc": desc.value.decode(),
                 "flops": fl.value, "bytes": by.value}
+
+    def nodeTag(self, i: int) -> str:
+        """Kernel label plus launch detail (tile config, K step, split, build) of node i."""
+        t = C.create_string_buffer(256)
+        _check(lib().ivh_node_tag(self._h, i, t, 256))
+        return t.value.decode()
 
     def memoryInfo(self, batch: int = 1):
         a, w = C.c_size_t(), C.c_size_t()

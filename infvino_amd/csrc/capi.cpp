@@ -371,6 +371,16 @@ int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel,
     if (bytes) *bytes = s.bytes;
   });
 }
+int ivh_node_tag(ivh_model * m, int i, char * tag, size_t tag_len)
+{
+  return guard([&] {
+    M(m).nodeStat(i);  // range check
+    const std::string t = M(m).nodeTag(i);
+    if (!tag || tag_len == 0) return;
+    std::strncpy(tag, t.c_str(), tag_len - 1);
+    tag[tag_len - 1] = 0;
+  });
+}
 int ivh_memory_info(const ivh_model * m, int batch, size_t * arena_bytes, size_t * weight_bytes)
 {
   return guard([&] {

@@ -21,6 +21,9 @@
 #include "conv_common.hpp"
 #include "kernels.hpp"
 
+#include <cstdio>
+#include <string>
+
 namespace ivh {
 
 // ------------------------------------------------------------ im2col kernel
@@ -312,6 +315,14 @@ static long igemm_tiles(const ConvParams & p)
   return ((long)p.batch * p.Ho * p.Wo + 127) / 128 * ((p.Cout + bn - 1) / bn);
 }
 
+// The 128-VGPR build (four resident work-groups per CU) of the 128-wide tile: 1x1 convs with
+// K step 32 whose 769..1024 tiles overflow three work-groups per CU
+static bool igemm_occ4(const ConvParams & p)
+{
+  return p.K == 1 && p.bk == 32 && igemm_bn(p.Cout) == 128 && !(p.Cin & 7) && !p.xt && p.ksplit == 1 &&
+         igemm_tiles(p) > 3 * 256 && igemm_tiles(p) <= 4 * 256;
+}
+
 // Register prefetch depth (K steps in flight) per tile width (measured on MI355X over
 // depths 1..6: deeper rings cost occupancy on the wide tiles and gain little elsewhere).
 constexpr int PF32 = 2, PF64 = 2, PF128 = 2;
@@ -326,7 +337,7 @@ static void launch_bk(const ConvParams & p, hipStream_t s)
     // fit four: the 128-VGPR build of the same tile (40x40 maps at batch 64, 800 tiles:
     // 22-34 -> 20-30 us).  3x3 convs lose more to the register cap than they gain (measured).
     if constexpr (BK == 32) {
-      if (p.K == 1 && !(p.Cin & 7) && !p.xt && p.ksplit == 1 && igemm_tiles(p) > 3 * 256 && igemm_tiles(p) <= 4 * 256) {
+      if (igemm_occ4(p)) {
         launch_t<2, 2, 2, 2, BK, PF128, 4>(p, s);
         break;
       }
@@ -382,6 +393,21 @@ ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb)
   q.y.ptr += (long)b0 * p.y.img;
   if (q.r.ptr) q.r.ptr += (long)b0 * p.r.img;
   return q;
+}
+
+std::string igemm_launch_tag(const ConvParams & p)
+{
+  char b[160];
+  if (p.res)
+    snprintf(b, sizeof b, "cfg=%d th=%d tw=%d ck=%d store=%d", p.res - 1, p.th, p.tw, p.ck, res_store_width(p));
+  else if (p.halo)
+    snprintf(b, sizeof b, "cfg=%d th=%d tw=%d ck=%d", p.halo - 1, p.th, p.tw, p.ck);
+  else if (p.s2)
+    snprintf(b, sizeof b, "cfg=%d th=%d tw=%d", p.s2 - 1, p.th, p.tw);
+  else
+    snprintf(b, sizeof b, "bn=%d bk=%d ksplit=%d%s%s%s", igemm_bn(p.Cout), p.bk, p.ksplit,
+             igemm_occ4(p) ? " vgpr128" : "", p.xt ? " planar" : "", (p.Cin & 7) ? " cin-ragged" : "");
+  return b;
 }
 
 void launch_conv_igemm(const ConvParams & p, hipStream_t s)

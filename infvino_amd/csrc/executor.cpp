@@ -2161,6 +2161,17 @@ std::vector<double> Model::profileNodes(int batch, int iters)
   return ms;
 }
 
+std::string Model::nodeTag(int i)
+{
+  std::string k = nodeKernel(i);
+  const LaunchPlan & P = launches(max_batch_);
+  if (P.begin.at(i) == P.end.at(i)) return k;
+  const Launch & l = P.L[P.begin[i]];
+  if (l.kind == Launch::kIgemm) return k + " " + igemm_launch_tag(l.cp);
+  if (l.kind == Launch::kDw) return k + " " + dw_launch_tag(l.cp);
+  return k;
+}
+
 std::string Model::nodeKernel(int i)
 {
   const NodeStat & s = stats_.at(i);

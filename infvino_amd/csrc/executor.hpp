@@ -82,6 +82,8 @@ class Model {
   const NodeStat & nodeStat(int i) const { return stats_.at(i); }
   // kernel family node i launches at the largest batch (conv_halo / conv_igemm / conv_stem ...)
   std::string nodeKernel(int i);
+  // nodeKernel plus the launch detail (tile config, K step, split, build) at the largest batch
+  std::string nodeTag(int i);
   size_t arenaBytes(int batch) const { return (size_t)arena_elems1_ * batch * 2; }
   size_t weightBytes() const { return weight_bytes_; }
 

@@ -4,6 +4,8 @@
 
 #include "ivh_internal.hpp"
 
+#include <string>
+
 namespace ivh {
 
 // conv_mfma.hip
@@ -13,6 +15,9 @@ int igemm_kpad(int cout, int kk);          // packed K: kk rounded up to that st
 constexpr int kIgemmBK = 32;               // packed K is always a multiple of this
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple
 void launch_conv_igemm(const ConvParams & p, hipStream_t s);
+// launch detail of an implicit-GEMM-family conv (resident-weight / LDS-patch / stride-2 tile
+// config, or the im2col tile, K step, split and build) for node tags
+std::string igemm_launch_tag(const ConvParams & p);
 int conv_batch_chunk(const ConvParams & p);                      // images per launch (< 2^31 B input)
 ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb);  // images [b0, b0 + nb)
 int igemm_ksplit(long M, int cout, int kpad);  // 1 = no split
@@ -58,6 +63,7 @@ void launch_conv_s2(const ConvParams & p, hipStream_t s);
 // kernels_misc.hip
 void launch_conv_direct(const ConvParams & p, hipStream_t s);   // any K/S/P/G, any layout
 void launch_dwconv(const ConvParams & p, hipStream_t s);        // depthwise, any layout
+std::string dw_launch_tag(const ConvParams & p);                 // kernel and tile of a depthwise launch
 bool dwconv_vectorizable(const ConvParams & p);
 bool stem_rows_supported(const ConvParams & p);  // the row-tiled stem kernel applies
 

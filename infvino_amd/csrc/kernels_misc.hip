@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstdio>
 #include <type_traits>
 #include <initializer_list>
 #include <map>
@@ -848,6 +849,16 @@ static void launch_dw_strip(const ConvParams & p, hipStream_t s)
 static bool dw_use_strip(const ConvParams & p)
 {
   return p.K == 5 && p.S == 2 && (long)p.batch * p.Ho * ((p.Wo + 3) / 4) * (p.Cin / 8) >= 1536L * 64;
+}
+
+std::string dw_launch_tag(const ConvParams & p)
+{
+  if (!dwconv_vectorizable(p)) return "generic";
+  if (dw_use_strip(p)) return "strip px=4";
+  const DwPick d = dw_pick(p);
+  char b[128];
+  snprintf(b, sizeof b, "tile px=%d py=%d g=%d bx=%d by=%d", d.PX, d.PY, d.t.G, d.t.BX, d.t.BY);
+  return b;
 }
 
 void launch_dwconv(const ConvParams & p, hipStream_t s)

@@ -213,6 +213,24 @@ def test_halo_residual_chain(tmp_path):
     _check_f32(path, 2, lo=-1.0, flags=nr)
 
 
+@pytest.mark.parametrize("cin,cout,hw,k,batch,want", [
+    (128, 128, 160, 3, 2, "cfg=7"), (96, 136, 96, 3, 2, "cfg=7"), (128, 128, 224, 3, 2, "cfg=3"),
+    (128, 128, 160, 1, 4, "vgpr128")])
+def test_tile_configs(tmp_path, cin, cout, hw, k, batch, want):
+    """The LDS-patch configs that batch 64 uses for the wide 3x3 layers (3: 32-channel chunks,
+    7: 64-channel chunks, 96 -> 136 leaving a ragged last chunk and a partial output tile)
+    and the 128-VGPR build of the 128-wide im2col tile, reached at small batch, against the
+    oracle."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, act=pw.ACT_SILU, pre_relu=True)
+    m = ia.PlanModel(path, 0, batch, ia.IVH_FLAG_DRY_RUN)
+    m.run(batch)
+    tag = next(m.nodeTag(i) for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
+    m.close()
+    print(tag)
+    assert want in tag.split()
+    _check_f32(path, batch, lo=-1.0, ref_mode=False)
+
+
 @pytest.mark.parametrize("cin,cout,hw,k,s,batch", [
     (256, 256, 20, 3, 1, 1),   # batch 1: 8 output tiles, 72 K tiles -> split-K
     (128, 51, 40, 3, 1, 1),

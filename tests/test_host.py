@@ -85,6 +85,32 @@ def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     assert kern == next(v for key, v in want.items() if name.startswith(key))
 
 
+# (cin, cout, hw, k, batch) -> launch detail the planner must pick.  Batch 64 runs the wide
+# 3x3 layers on LDS-patch configs 3 (32-channel chunks) and 7 (64-channel chunks); these
+# small-batch shapes reach the same configs, and the 1x1 shape reaches 769..1024 output tiles
+# of the 128-wide im2col tile, the case of its 128-VGPR build.
+TAGGED = [
+    ((128, 128, 160, 3, 2), "conv_halo cfg=7", "ck=64"),
+    ((96, 136, 96, 3, 2), "conv_halo cfg=7", "ck=64"),
+    ((128, 128, 224, 3, 2), "conv_halo cfg=3", "ck=32"),
+    ((128, 128, 40, 3, 64), "conv_halo cfg=3", "ck=32"),
+    ((256, 256, 20, 3, 64), "conv_halo cfg=7", "ck=64"),
+    ((128, 128, 160, 1, 4), "conv_igemm bn=128 bk=32 ksplit=1", "vgpr128"),
+]
+
+
+@pytest.mark.parametrize("shape,head,detail", TAGGED, ids=[f"{a}to{b}_{c}_k{d}_b{e}" for (a, b, c, d, e), _, _ in TAGGED])
+def test_launch_tags(tmp_path, shape, head, detail):
+    """ivh_node_tag names the tile config the planner picked (host-only dry run)."""
+    cin, cout, hw, k, b = shape
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, act=pw.ACT_SILU, pre_relu=True)
+    m = ia.PlanModel(path, 0, b, DRY)
+    m.run(b)
+    tag = next(m.nodeTag(i) for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
+    m.close()
+    assert tag.startswith(head) and detail in tag.split(), tag
+
+
 def test_zero_copy_views_in_c2f(plans):
     """C2f: cv1 output is split by views, the bottleneck outputs and both halves land in the
     concat buffer in place, so no copy_c/concat node launches anything."""
