@@ -681,16 +681,17 @@ __global__ void __launch_bounds__(256) dw_strip_kernel(const ConvParams p, FastD
   }
 }
 
-// Any-layout depthwise: one lane = one output element.
-__global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p)
+// Any-layout depthwise: one lane = one output pixel of one channel plane, grid (pixel
+// blocks, channel, image) so that the channel's weights are wave-uniform (scalar loads) and,
+// on NCHW tensors, neighbouring lanes read neighbouring pixels.  Same tap order and roundings
+// as the channels-last kernels: act(sum + b), one fp16 rounding, then the residual.
+__global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p, FastDiv d_wo)
 {
   const int HWo = p.Ho * p.Wo;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)p.batch * HWo * p.Cin) return;
-  const int hw = (int)(idx % HWo);
-  const long t = idx / HWo;
-  const int c = (int)(t % p.Cin), b = (int)(t / p.Cin);
-  const int oy = hw / p.Wo, ox = hw % p.Wo;
+  const int hw = blockIdx.x * 256 + threadIdx.x;
+  if (hw >= HWo) return;
+  const int c = blockIdx.y, b = blockIdx.z;
+  const int oy = (int)fastdiv((unsigned)hw, d_wo), ox = hw - oy * p.Wo;
   const float * W = reinterpret_cast<const float *>(p.w);
   float acc = 0.0f;
   for (int ky = 0; ky < p.K; ++ky) {
@@ -702,9 +703,60 @@ __global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p)
       acc += vld(p.x, b, c, (long)iy * p.W + ix) * W[(ky * p.K + kx) * p.Cin + c];
     }
   }
-  float v = act_f(acc + (p.bias ? p.bias[c] : 0.0f), p.act);
+  float v = (float)(_Float16)act_f(acc + (p.bias ? p.bias[c] : 0.0f), p.act);
   if (p.r.ptr) v += vld(p.r, b, c, hw);
   vst(p.y, b, c, hw, v);
+}
+
+// Channel-planar (NCHW in and out) depthwise with K in {3, 5}: one lane = PX consecutive
+// output pixels of one row of one channel plane (strips of a plane on neighbouring lanes,
+// then the next channel), grid (strips of all planes, image); each input row segment of the
+// strip is loaded once for its PX outputs.  Same tap order and roundings as the other
+// kernels.
+template <int K, int S, int PX>
+__global__ void __launch_bounds__(256) dw_nchw_kernel(const ConvParams p, FastDiv d_strips, FastDiv d_plane)
+{
+  constexpr int NX = (PX - 1) * S + K;
+  const int strips = (p.Wo + PX - 1) / PX, plane = p.Ho * strips;
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  if (q >= p.Cin * plane) return;
+  const int c = (int)fastdiv((unsigned)q, d_plane), r = q - c * plane, b = blockIdx.y;
+  const int oy = (int)fastdiv((unsigned)r, d_strips), ox0 = (r - oy * strips) * PX;
+  const _Float16 * xp = reinterpret_cast<const _Float16 *>(p.x.ptr) + (long)b * p.x.img + (long)c * p.x.cs;
+  const float * W = reinterpret_cast<const float *>(p.w) + c;
+  float w[K * K];
+#pragma unroll
+  for (int k = 0; k < K * K; ++k) w[k] = W[k * p.Cin];
+  const int iy0 = oy * S - p.P, ix0 = ox0 * S - p.P;
+  float acc[PX];
+#pragma unroll
+  for (int j = 0; j < PX; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int ky = 0; ky < K; ++ky) {
+    const int iy = iy0 + ky;
+    if ((unsigned)iy >= (unsigned)p.H) continue;
+    float xr[NX];
+#pragma unroll
+    for (int t = 0; t < NX; ++t) {
+      const int ix = ix0 + t;
+      xr[t] = (unsigned)ix < (unsigned)p.W ? (float)xp[iy * p.W + ix] : 0.0f;
+    }
+#pragma unroll
+    for (int kx = 0; kx < K; ++kx)
+#pragma unroll
+      for (int j = 0; j < PX; ++j) acc[j] += xr[j * S + kx] * w[ky * K + kx];
+  }
+  const float bias = p.bias ? p.bias[c] : 0.0f;
+  _Float16 * yp = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + (long)c * p.y.cs;
+#pragma unroll
+  for (int j = 0; j < PX; ++j) {
+    const int ox = ox0 + j;
+    if (ox >= p.Wo) continue;
+    const int hw = oy * p.Wo + ox;
+    float v = (float)(_Float16)act_f(acc[j] + bias, p.act);
+    if (p.r.ptr) v += vld(p.r, b, c, hw);
+    yp[hw] = (_Float16)v;
+  }
 }
 
 bool dwconv_vectorizable(const ConvParams & p)
@@ -853,7 +905,9 @@ static bool dw_use_strip(const ConvParams & p)
 
 std::string dw_launch_tag(const ConvParams & p)
 {
-  if (!dwconv_vectorizable(p)) return "generic";
+  if (!dwconv_vectorizable(p))
+    return p.x.layout == kNCHW && p.y.layout == kNCHW && (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2)
+               ? "planar px=4" : "generic";
   if (dw_use_strip(p)) return "strip px=4";
   const DwPick d = dw_pick(p);
   char b[128];
@@ -863,9 +917,25 @@ std::string dw_launch_tag(const ConvParams & p)
 
 void launch_dwconv(const ConvParams & p, hipStream_t s)
 {
-  const long M = (long)p.batch * p.Ho * p.Wo;
   if (!dwconv_vectorizable(p)) {
-    hipLaunchKernelGGL(dw_generic_kernel, dim3(nblk(M * p.Cin, 256)), dim3(256), 0, s, p);
+    if (p.Cin > 65535 || p.batch > 65535) throw std::runtime_error("depthwise: grid");
+    const dim3 grid(nblk((long)p.Ho * p.Wo, 256), (unsigned)p.Cin, (unsigned)p.batch);
+    const bool planar = p.x.layout == kNCHW && p.y.layout == kNCHW && (long)p.H * p.W < (1L << 31) &&
+                        (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2);
+    if (planar) {
+      constexpr int PX = 4;
+      const int strips = (p.Wo + PX - 1) / PX;
+      const long n = (long)p.Cin * p.Ho * strips;
+      if (n >= (1L << 31)) throw std::runtime_error("depthwise: grid");
+      const dim3 g(nblk(n, 256), (unsigned)p.batch);
+      const FastDiv f = fastdiv_make((unsigned)strips), fp = fastdiv_make((unsigned)(p.Ho * strips));
+      if (p.K == 3 && p.S == 1) hipLaunchKernelGGL((dw_nchw_kernel<3, 1, PX>), g, dim3(256), 0, s, p, f, fp);
+      else if (p.K == 3) hipLaunchKernelGGL((dw_nchw_kernel<3, 2, PX>), g, dim3(256), 0, s, p, f, fp);
+      else if (p.S == 1) hipLaunchKernelGGL((dw_nchw_kernel<5, 1, PX>), g, dim3(256), 0, s, p, f, fp);
+      else hipLaunchKernelGGL((dw_nchw_kernel<5, 2, PX>), g, dim3(256), 0, s, p, f, fp);
+    } else {
+      hipLaunchKernelGGL(dw_generic_kernel, grid, dim3(256), 0, s, p, fastdiv_make((unsigned)p.Wo));
+    }
     return;
   }
   if (dw_use_strip(p)) {
@@ -1282,12 +1352,16 @@ __global__ void __launch_bounds__(256) maxpool_s1_cols_kernel(const SmallParams 
 // over the union of their windows, and clipping composes the same way).  One work-group per
 // (image, 8 channels): the plane into LDS, row maxima of widths 5 / 9 / 13, then column
 // maxima.  Maxima of fp16 values are fp16 values: packed fp16 max (IEEE maxNum, as fmaxf)
-// gives every output bit for bit as the chained pools compute it.
+// gives every output bit for bit as the chained pools compute it.  The work-groups of one
+// image's neighbouring channel groups, which read and write the same 128-byte lines of the
+// channels-last tensors, run on one XCD (xcd_tile), so those lines meet in one L2 instead of
+// leaving eight partially written copies to be merged behind the L2s.
 __global__ void __launch_bounds__(256) maxpool_sppf3_kernel(const SmallParams q)
 {
   extern __shared__ h8 pl[];  // 4 planes of H * W pixels: input, row maxima 5 / 9 / 13
-  const int HW = q.H * q.W;
-  const int b = blockIdx.y, c = blockIdx.x * 8;
+  const int HW = q.H * q.W, C8 = q.C / 8;
+  const int t = xcd_tile(blockIdx.x, (int)gridDim.x);
+  const int b = t / C8, c = (t - b * C8) * 8;
   const h8 ninf = (h8)(_Float16)(-__builtin_inff());
   for (int p = threadIdx.x; p < HW; p += 256) pl[p] = ld8(q.a.ptr, (long)b * q.a.img + (long)p * q.a.cs + c);
   __syncthreads();
@@ -1577,7 +1651,7 @@ bool launch_small_vec(int kind, const SmallParams & q, hipStream_t s)
 void launch_small(int kind, const SmallParams & q, hipStream_t s)
 {
   if (kind == kMaxPoolSppf) {
-    hipLaunchKernelGGL(maxpool_sppf3_kernel, dim3((unsigned)(q.C / 8), (unsigned)q.batch), dim3(256),
+    hipLaunchKernelGGL(maxpool_sppf3_kernel, dim3((unsigned)(q.C / 8 * q.batch)), dim3(256),
                        (size_t)4 * q.H * q.W * 16, s, q);
     return;
   }
