@@ -65,6 +65,10 @@ extern "C" {
                                           one fused kernel */
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
+#define IVH_FLAG_NO_PIPE 0x2000u  /* 3x3 stride-1 convs never use the DMA-pipelined kernel */
+#define IVH_FLAG_PIPE_ANY 0x4000u /* 3x3 stride-1 convs use the DMA-pipelined kernel wherever it
+                                     applies (Cin >= 32, any grid size), not only where it is
+                                     measured fastest */
 #define IVH_FLAG_NO_FUSE_ATTN 0x1000u /* keep an attention core (q^T k, scale, softmax, v P^T)
                                          node by node instead of one fused kernel */
 #define IVH_FLAG_PROFILE 0x800u   /* PlanModel's profiling=true: every run launches node by node

@@ -177,11 +177,39 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
     p.xt = 1;
     return kLaunchIgemm;
   }
+  // 3x3 stride 1 with Cin % 8 == 0, 64 < Cin, Cout <= 256: the DMA-pipelined persistent
+  // kernel on the 32-channel-chunk packing, when its items fill the persistent grid.
+  // Measured on MI355X at batch 64 against the LDS-patch kernel: 128->128 at 40x40 46.5 ->
+  // 43.0 us, 128->51 / 128->64 at 40x40 28.2 / 27.6 -> 26.1 / 27.1 us; with Cin <= 64 the
+  // resident-weight kernel below stays faster (64->64 at 80x80: 44 vs 51 us).
+  int hc, th, tw;
+  const bool pipe_any = (s.flags & IVH_FLAG_PIPE_ANY) != 0;
+  if (p.K == 3 && p.S == 1 && p.P == 1 && !(s.flags & IVH_FLAG_NO_PIPE) && (p.Cin > 64 || pipe_any) && p.Cout <= 256 &&
+      pipe_views_ok(p) &&
+      pipe_plan(p.Cin, p.Cout, p.H, p.W, batch, p.act, &hc, &th, &tw)) {
+    const int hi = halo_index(32);
+    if (pk.halo[hi] != kNoSeg && pk.kpad_halo[hi] == (p.Cin + 31) / 32 * 9 * 32) {
+      ConvParams q = p;
+      q.th = th;
+      q.tw = tw;
+      q.pipe = hc + 1;
+      if (pipe_any || pipe_items(q) >= kPipeMinItems) {
+        p.pipe = hc + 1;
+        p.th = th;
+        p.tw = tw;
+        p.ck = 32;
+        p.ksplit = 1;
+        p.ws = nullptr;
+        p.w = reinterpret_cast<const __half *>(base + pk.halo[hi]);
+        p.kpad = pk.kpad_halo[hi];
+        return kLaunchIgemm;
+      }
+    }
+  }
   // 3x3 stride 1 with 16 < Cin <= 64: weights resident in LDS, persistent over pixel tiles.
   // Measured on MI355X at batch 64 against the LDS-patch kernel: faster for every such layer
   // of the YOLO models except a fused residual with Cin <= 32 (32->32 at 80x80 + residual:
   // 35 vs 30 us); with Cin <= 16 the two are even (16->16 at 160x160: 49 vs 51 us).
-  int hc, th, tw;
   if (p.K == 3 && p.S == 1 && p.P == 1 && !(s.flags & IVH_FLAG_NO_RESIDENT) && p.Cin > 16 &&
       !(p.r.ptr && p.Cin <= 32) && res_views_ok(p) &&
       res_plan(p.Cin, p.Cout, p.H, p.W, batch, p.act, &hc, &th, &tw)) {

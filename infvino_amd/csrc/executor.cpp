@@ -1742,14 +1742,14 @@ void Model::validate(const Launch & l) const
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
     // the resident-weight kernel writes 4-channel groups into the view's padding channels
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
           "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
     if (p.bias) check(p.bias, 0, (l.kind == Launch::kIgemm ? (p.Cout + 127) / 128 * 128 : p.Cout) - 1, 4, "conv bias");
     if (l.kind == Launch::kIgemm) {
       if (p.xt) {
-        if (p.x.layout != kNCHW || p.K != 1 || p.S != 1 || p.P != 0 || p.halo || p.res || p.s2 || p.x.cs != HW ||
+        if (p.x.layout != kNCHW || p.K != 1 || p.S != 1 || p.P != 0 || p.halo || p.res || p.s2 || p.pipe || p.x.cs != HW ||
             HW % 8 || p.x.img % 8)
           throw std::runtime_error("igemm planar input geometry");
         check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "igemm planar x");
@@ -1783,6 +1783,17 @@ void Model::validate(const Launch & l) const
         check(p.w, 0, nrows * p.kpad - 1, 2, "resident-weight w");
         if (res_grid_x(p, cfg) < 1 || res_grid_x(p, cfg) > 65535) throw std::runtime_error("resident-weight grid");
       }
+      if (p.pipe) {
+        const int cfg = p.pipe - 1;
+        if (cfg < 0 || cfg > 1 || p.halo || p.res || p.s2 || p.ck != 32 || p.K != 3 || p.S != 1 || p.P != 1 ||
+            p.ksplit != 1 || p.th < 1 || p.tw < 1 || p.Ho != p.H || p.Wo != p.W || p.th * p.tw > 256 ||
+            p.th + 2 > p.H + 1 || p.Cout > 256 || (cfg == 0) != (p.Cout > 64) || !pipe_views_ok(p) ||
+            (long)(p.th + 2) * (5 * p.tw + 16) > (cfg == 0 ? 1728 : 2112))
+          throw std::runtime_error("pipelined conv geometry");
+        if (p.kpad != (p.Cin + 31) / 32 * 9 * 32) throw std::runtime_error("pipelined conv packing");
+        if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 14)) throw std::runtime_error("pipelined conv geometry too large");
+        check(p.w, 0, (long)(p.Cout + 127) / 128 * 128 * p.kpad - 1, 2, "pipelined conv w");
+      }
       if (p.s2) {
         const int cfg = p.s2 - 1;
         if (cfg < 0 || cfg > 1 || p.halo || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
@@ -1797,8 +1808,8 @@ void Model::validate(const Launch & l) const
         check(p.ws, 0, (long)p.ksplit * rows * M - 1, 4, "igemm split-K workspace");
       }
       if (p.kpad % kIgemmBK && !p.res) throw std::runtime_error("kpad not a multiple of the K tile");
-      if (!p.halo && !p.res && (p.bk != 32 && p.bk != 64)) throw std::runtime_error("kpad not a multiple of the K tile");
-      if (!p.halo && !p.res && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
+      if (!p.halo && !p.res && !p.pipe && (p.bk != 32 && p.bk != 64)) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (!p.halo && !p.res && !p.pipe && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
     } else if (l.kind == Launch::kDirect && p.stem_mfma) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
       check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");
@@ -2180,7 +2191,7 @@ std::string Model::nodeKernel(int i)
   const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
   case Launch::kIgemm:
-    return l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
+    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";

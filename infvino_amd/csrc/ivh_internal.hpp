@@ -79,6 +79,9 @@ struct ConvParams {
   // 3x3 stride-1 pad-1 resident-weight kernel (conv_res.hip, Cin <= ck): config + 1 (0: not
   // used); th x tw and ck as for the halo kernel, w the single-chunk halo packing
   int res = 0;
+  // 3x3 stride-1 pad-1 DMA-pipelined kernel (conv_pipe.hip, Cin % 8 == 0, Cin >= 32): config
+  // + 1 (0: not used); th x tw as for the halo kernel, w the 32-channel-chunk halo packing
+  int pipe = 0;
   // channels after the output view's last one that belong to no tensor (the padding of a
   // channels-last root whose last channel range this view is); a kernel may write there
   int ypad = 0;

@@ -50,6 +50,18 @@ constexpr int kResMaxRows = 34;  // patch rows (TH + 2) of the resident-weight k
 constexpr int kHaloMaxRows = 34;  // patch rows (TH + 2) of the LDS-patch kernel's tiles
 void launch_conv_res(const ConvParams & p, hipStream_t s);
 
+// conv_pipe.hip: 3x3 stride-1 pad-1 convs with Cin % 8 == 0, Cin >= 32, fed through LDS by
+// DMA (buffer loads into LDS), persistent over (tile, channel block) items
+// config and output tile th x tw for a layer at a batch size; false: not eligible
+bool pipe_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw);
+int pipe_bn(int cfg);
+long pipe_items(const ConvParams & p);
+// the input, output and residual views suit the kernel (16-byte channels-last input pieces,
+// 8-channel output stores, 4-channel residual loads)
+bool pipe_views_ok(const ConvParams & p);
+constexpr int kPipeMinItems = 256;  // fewer items: the other 3x3 kernels
+void launch_conv_pipe(const ConvParams & p, hipStream_t s);
+
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
 bool s2_plan(int cin, int cout, int Ho, int Wo, int * cfg, int * th, int * tw);
 int s2_patch(int th, int tw);  // patch pixels of a th x tw output tile

@@ -79,7 +79,7 @@ def test_conv1x1_config(tmp_path):
 
 SWEEP_KERNEL = {"stem": ("conv_stem",), "dw": ("dwconv",),
                 "conv3x3s2": ("conv_igemm", "conv_igemm_sk", "conv_s2"),
-                "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res")}
+                "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res", "conv_pipe")}
 
 
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
@@ -117,7 +117,7 @@ def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
     (the graph input)."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act, pre_relu=cin > 3)
     kern = _conv_kernel(path, 3)
-    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res")
+    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res", "conv_pipe")
     _check_f32(path, 3, lo=-1.0)
 
 
@@ -185,6 +185,47 @@ def test_res_residual_chain(tmp_path):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (128, 128, 40, 40, 2, pw.ACT_SILU),    # BN 128 (config 0), four 32-channel chunks
+    (72, 64, 33, 35, 2, pw.ACT_SILU),      # BN 64, a last chunk of 8 channels, odd H and W
+    (96, 136, 24, 40, 2, pw.ACT_SILU),     # two channel blocks, the second 8 channels wide
+    (64, 51, 48, 48, 1, pw.ACT_HSWISH),    # Cout 51: 8-channel stores reach the view's padding
+    (256, 256, 20, 20, 2, pw.ACT_RELU),    # eight chunks, two blocks of 128 channels
+    (32, 64, 80, 80, 32, pw.ACT_SILU),     # one chunk per item, 810 items: several per work-group
+    (40, 24, 20, 20, 6, pw.ACT_RELU),      # two chunks (8 real channels in the second), BN 64
+])
+def test_pipe_conv3x3(tmp_path, cin, cout, H, W, batch, act):
+    """3x3 stride-1 convs through the DMA-pipelined kernel (forced with IVH_FLAG_PIPE_ANY at
+    these small sizes) vs the oracle and vs the other 3x3 kernels."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=act, pre_relu=True, post_relu=True)
+    print(f"pipe conv {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_PIPE_ANY) == "conv_pipe"
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_PIPE) != "conv_pipe"
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_PIPE_ANY)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PIPE)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def test_pipe_residual_chain(tmp_path):
+    """Bottleneck chain of 64 channels at batch 8 (3x3 SiLU, 3x3 + residual, 3x3 without
+    activation + residual) through the DMA-pipelined kernel with the fused residual add."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, 64, 40, 40]), pw.UN_RELU)
+        t = pb.conv(x, 64, 3)
+        t = pb.conv(t, 64, 3)
+        y = pb.binary(x, t, 0)
+        u = pb.conv(y, 64, 3, act=pw.ACT_NONE)
+        z = pb.binary(y, u, 0)
+        return pb.unary(z, pw.UN_RELU)
+    path = _small_plan(tmp_path, build)
+    assert _kernels(path, 8, ia.IVH_FLAG_PIPE_ANY).count("conv_pipe") == 3
+    got = _check_f32(path, 8, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_PIPE_ANY)
+    _, _, other = _run(path, 8, lo=-1.0, flags=ia.IVH_FLAG_NO_PIPE)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
 @pytest.mark.parametrize("cin,cout,H,W,batch", [
     (16, 32, 64, 64, 3),       # the YOLO 16->32 downsample shape class: 128-pixel tiles
     (16, 64, 40, 40, 2),       # 16 in, 64 out: 64-pixel tiles, two channel blocks
@@ -222,13 +263,13 @@ def test_tile_configs(tmp_path, cin, cout, hw, k, batch, want):
     and the 128-VGPR build of the 128-wide im2col tile, reached at small batch, against the
     oracle."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, act=pw.ACT_SILU, pre_relu=True)
-    m = ia.PlanModel(path, 0, batch, ia.IVH_FLAG_DRY_RUN)
+    m = ia.PlanModel(path, 0, batch, ia.IVH_FLAG_DRY_RUN | ia.IVH_FLAG_NO_PIPE)
     m.run(batch)
     tag = next(m.nodeTag(i) for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
     m.close()
     print(tag)
     assert want in tag.split()
-    _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_PIPE)
 
 
 @pytest.mark.parametrize("cin,cout,hw,k,s,batch", [

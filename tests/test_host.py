@@ -55,7 +55,9 @@ def test_kernel_choice_yolov8(plans):
     """Planner choices at batch 64: the stem kernel for the Cin = 3 conv, the stride-2
     LDS-patch kernel for the 16->32 downsample, the implicit GEMM for the 32->64 one, the
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
-    Cin <= 32 ones with a fused residual) and the stride-1 LDS-patch kernel for the rest."""
+    Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
+    40x40 maps (enough items for its persistent grid) and the stride-1 LDS-patch kernel for
+    the rest."""
     m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
@@ -63,11 +65,16 @@ def test_kernel_choice_yolov8(plans):
     assert by["conv3x3 3x640x640->16x320x320 k3 s2 g1 act1"] == "conv_stem"
     assert by["conv3x3 16x320x320->32x160x160 k3 s2 g1 act1"] == "conv_s2"
     assert by["conv3x3 32x160x160->64x80x80 k3 s2 g1 act1"] == "conv_igemm"
-    s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), "+res" in i["desc"]) for i in info
-          if i["op"] == "conv3x3" and " s1 " in i["desc"]]
-    want = lambda cin, res: "conv_res" if 16 < cin <= 64 and not (res and cin <= 32) else "conv_halo"
-    assert s1 and all(k == want(cin, res) for k, cin, res in s1)
-    assert sum(k == "conv_res" for k, _, _ in s1) >= 20
+    s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), int(i["desc"].split()[1].split("x")[1]),
+           "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
+
+    def want(cin, hw, res):
+        if 16 < cin <= 64 and not (res and cin <= 32):
+            return "conv_res"
+        return "conv_pipe" if cin > 64 and hw >= 40 else "conv_halo"
+    assert s1 and all(k == want(cin, hw, res) for k, cin, hw, res in s1)
+    assert sum(k == "conv_res" for k, _, _, _ in s1) >= 20
+    assert sum(k == "conv_pipe" for k, _, _, _ in s1) >= 3
     m.close()
 
 
@@ -75,7 +82,7 @@ def test_kernel_choice_yolov8(plans):
 def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     """Each conv sweep layer at batch 64, as it runs inside a model, gets its kernel family."""
     want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2", "conv3x3s2": "conv_igemm",
-            "conv3x3s1_64": "conv_res", "conv3x3s1": "conv_halo", "dw": "dwconv"}
+            "conv3x3s1_64": "conv_res", "conv3x3s1_128": "conv_pipe", "conv3x3s1": "conv_halo", "dw": "dwconv"}
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act,
                              pre_relu=not name.startswith("stem"), post_relu=True)
     m = ia.PlanModel(path, 0, 64, DRY)
@@ -90,21 +97,25 @@ def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
 # small-batch shapes reach the same configs, and the 1x1 shape reaches 769..1024 output tiles
 # of the 128-wide im2col tile, the case of its 128-VGPR build.
 TAGGED = [
-    ((128, 128, 160, 3, 2), "conv_halo cfg=7", "ck=64"),
-    ((96, 136, 96, 3, 2), "conv_halo cfg=7", "ck=64"),
-    ((128, 128, 224, 3, 2), "conv_halo cfg=3", "ck=32"),
-    ((128, 128, 40, 3, 64), "conv_halo cfg=3", "ck=32"),
-    ((256, 256, 20, 3, 64), "conv_halo cfg=7", "ck=64"),
-    ((128, 128, 160, 1, 4), "conv_igemm bn=128 bk=32 ksplit=1", "vgpr128"),
+    ((128, 128, 160, 3, 2), "conv_halo cfg=7", "ck=64", 0),
+    ((96, 136, 96, 3, 2), "conv_halo cfg=7", "ck=64", 0),
+    ((128, 128, 224, 3, 2), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE),
+    ((128, 128, 40, 3, 64), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE),
+    ((256, 256, 20, 3, 64), "conv_halo cfg=7", "ck=64", 0),
+    ((128, 128, 160, 1, 4), "conv_igemm bn=128 bk=32 ksplit=1", "vgpr128", 0),
+    ((128, 128, 40, 3, 64), "conv_pipe cfg=0", "items=438", 0),
+    ((128, 64, 40, 3, 64), "conv_pipe cfg=1", "items=410", 0),
+    ((64, 64, 80, 3, 2), "conv_pipe cfg=1", "items=54", ia.IVH_FLAG_PIPE_ANY),
 ]
 
 
-@pytest.mark.parametrize("shape,head,detail", TAGGED, ids=[f"{a}to{b}_{c}_k{d}_b{e}" for (a, b, c, d, e), _, _ in TAGGED])
-def test_launch_tags(tmp_path, shape, head, detail):
+@pytest.mark.parametrize("shape,head,detail,flags", TAGGED,
+                         ids=[f"{a}to{b}_{c}_k{d}_b{e}_f{f:x}" for (a, b, c, d, e), _, _, f in TAGGED])
+def test_launch_tags(tmp_path, shape, head, detail, flags):
     """ivh_node_tag names the tile config the planner picked (host-only dry run)."""
     cin, cout, hw, k, b = shape
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, act=pw.ACT_SILU, pre_relu=True)
-    m = ia.PlanModel(path, 0, b, DRY)
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, act=pw.ACT_SILU, pre_relu=True, post_relu=True)
+    m = ia.PlanModel(path, 0, b, DRY | flags)
     m.run(b)
     tag = next(m.nodeTag(i) for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
     m.close()
