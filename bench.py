@@ -23,6 +23,11 @@ table goes to stderr.
   other_models   YOLOv8n-pose 640 (batch 16 / 64), MobileNetV3-small 224 (batch 1 / 32 / 256)
                  and YOLO11n-pose 640 (batch 1 / 64): images/s of graph replays and batch-1
                  latency
+  mfma_roof_probe  the fp16 MFMA rate of the conv kernels' inner-loop shape with no global
+                 traffic (infvino_amd/tools/mfma_roof), for zero and for random operands: the
+                 matrix cores draw more power on random data and the clock drops, so the
+                 random-operand rate is the practical MFMA roof; conv_sweep rows of MFMA-bound
+                 layers carry frac_practical against it
   cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
                  workload on this host's cores -- a reported baseline, not a target; it
                  records the probe for a CPU OpenCL runtime that could run the reference's own
@@ -240,6 +245,24 @@ def opencl_probe():
     return res
 
 
+def mfma_roof_probe():
+    """Runs infvino_amd/tools/mfma_roof (a child process) and returns its JSON line, or a
+    note when the probe binary is absent or fails."""
+    import subprocess
+    exe = os.path.join(ROOT, "infvino_amd", "tools", "mfma_roof")
+    if not os.path.exists(exe):
+        return {"note": "probe not built (make -C infvino_amd/csrc tools)"}
+    try:
+        r = subprocess.run([exe, "2000"], capture_output=True, text=True, timeout=120)
+    except subprocess.TimeoutExpired:
+        return {"note": "probe timed out"}
+    if r.returncode != 0:
+        return {"note": f"probe failed: {r.stderr.strip()[-200:]}"}
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"[bench] MFMA roof probe: zeros {res['zeros_tflops']} TFLOP/s, random {res['random_tflops']} TFLOP/s")
+    return res
+
+
 def model_lines(ia, pw, specs, steps, warmup):
     """The other model configurations: images/s of graph replays at each batch (inputs
     resident in HBM) and the synchronous batch-1 latency."""
@@ -431,10 +454,16 @@ def main():
     m1.close()
 
     c1 = None if args.no_sweep else config1(ia, pw, max(args.profile_iters, 10))
+    probe = mfma_roof_probe()
     sweep = None
     if not args.no_sweep:
         sweep = {f"b{b}": conv_sweep(ia, pw, b, max(args.profile_iters, 10)) for b in (B, 1)}
         sweep["dw_b256"] = conv_sweep(ia, pw, 256, max(args.profile_iters, 10), only="dw")
+        if probe.get("random_tflops"):
+            for rows in sweep.values():
+                for r in rows:
+                    if r["bound"] == "mfma":
+                        r["frac_practical"] = round(r["tflops"] / probe["random_tflops"], 4)
     attn = None if args.no_sweep else attention(ia, pw, max(args.profile_iters, 10))
     others = None if args.no_models else model_lines(
         ia, pw, [("yolov8n-pose", 640, (16, 64)), ("mobilenetv3-small", 224, (1, 32, 256)),
@@ -453,14 +482,14 @@ def main():
         t = time.perf_counter()
         O.run_plan(p, x[:n_in * k], k)
         el = time.perf_counter() - t
-        probe = opencl_probe()
+        ocl = opencl_probe()
         cpu = {"value": round(k / el, 3), "unit": "images/s", "cores": cores, "kind": "port",
                "sample": f"{k} images of {args.model} 3x{args.imgsz}x{args.imgsz} through the C oracle "
                          f"(fp32 accumulate, OpenMP over output channels), {el:.1f} s",
                "reference_kernels": ("unavailable: no OpenCL CPU device on this host (the reference's .cl "
-                                     "kernels need one; see opencl_probe)") if probe["cpu_devices"] == 0 else
+                                     "kernels need one; see opencl_probe)") if ocl["cpu_devices"] == 0 else
                                     "an OpenCL CPU device exists (opencl_probe); not used by this bench",
-               "opencl_probe": probe}
+               "opencl_probe": ocl}
         log(f"[bench] cpu oracle: {k / el:.3f} images/s on {cores} threads")
 
     out = {
@@ -484,6 +513,7 @@ def main():
         "tflops_effective": round(flops_img * ips / 1e12, 2),
         "roofline": roof,
         "roofline_step": roof_step,
+        "mfma_roof_probe": probe,
         "config1": c1,
         "conv_sweep": sweep,
         "attention": attn,
