@@ -156,6 +156,7 @@ Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t 
     fusePermuteMatmul();
     fuseAttention();
   }
+  findPairs();
   plan();
   if (!dry_) HIPCHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   allocate();
@@ -1047,6 +1048,17 @@ void Model::allocate()
       r.last = std::max(r.last, ni + 2);
     }
   }
+  // A bottleneck pair runs as one launch at its first conv ni: it reads x (the first conv's
+  // input, and the second's residual) and writes y (the second conv's output) together, so
+  // x stays live to the second conv and y is live from ni.
+  for (int ni = 0; ni < N; ++ni) {
+    const int nj = pair_next_[ni];
+    if (nj < 0) continue;
+    const Tensor & xt = *T_[nodes_[ni].ins[0]];
+    const Tensor & yt = *T_[nodes_[nj].outs[0]];
+    if (xt.root >= 0 && xt.kind != Tensor::kInit) roots_[xt.root]->last = std::max(roots_[xt.root]->last, nj);
+    if (yt.root >= 0) roots_[yt.root]->first = std::min(roots_[yt.root]->first, ni);
+  }
   // best-fit placement, largest first, on closed [first, last] intervals
   std::vector<int> order;
   for (size_t i = 0; i < roots_.size(); ++i) {
@@ -1248,6 +1260,153 @@ bool Model::sppfChain(size_t ni) const
   return true;
 }
 
+// Bottleneck pairs: node A = conv3x3 (stride 1, pad 1, 32 -> 32 channels, no residual) whose
+// output has one reader, node B = conv3x3 (stride 1, pad 1, 32 -> 32) on it, B's residual none
+// or A's input, both activations among those the kernel has.  Structural only: whether the
+// pair runs fused also depends on the views (pairLaunch); the liveness that allocate gives
+// a pair is harmless when it does not.
+void Model::findPairs()
+{
+  pair_next_.assign(nodes_.size(), -1);
+  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_PAIR | IVH_FLAG_DIRECT_ONLY | IVH_FLAG_NO_HALO)) return;
+  std::map<std::string, std::vector<int>> readers;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (const auto & in : nodes_[i].ins)
+      if (in != "-") readers[in].push_back((int)i);
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  auto act_ok = [](int a) { return a == kActNone || a == kActSiLU || a == kActReLU || a == kActHSwish; };
+  auto conv32 = [&](const PlanNode & n) {
+    if (n.op != "conv3x3" || n.ins.size() < 2 || n.outs.size() != 1 || n.i("stride", 1) != 1 || n.i("pad", 1) != 1)
+      return false;
+    const Tensor & w = *T_.at(n.ins[1]);
+    const Tensor & x = *T_.at(n.ins[0]);
+    return w.dims.size() == 4 && w.dims[0] == 32 && w.dims[1] == 32 && w.dims[2] == 3 && w.dims[3] == 3 &&
+           x.C == 32 && n.i("Hout") == x.H && n.i("Wout") == x.W && act_ok(n.i("act"));
+  };
+  std::vector<char> used(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    const PlanNode & a = nodes_[i];
+    if (used[i] || !conv32(a) || (a.ins.size() > 3 && a.ins[3] != "-")) continue;
+    const std::string & t = a.outs[0];
+    const auto it = readers.find(t);
+    if (it == readers.end() || it->second.size() != 1 || outs.count(t)) continue;
+    const int j = it->second[0];
+    const PlanNode & b = nodes_[j];
+    if (j <= (int)i || used[j] || !conv32(b) || b.ins[0] != t) continue;
+    if (b.ins.size() > 3 && b.ins[3] != "-" && b.ins[3] != a.ins[0]) continue;
+    if (T_.at(b.ins[0])->H != T_.at(a.ins[0])->H || T_.at(b.ins[0])->W != T_.at(a.ins[0])->W) continue;
+    pair_next_[i] = j;
+    used[i] = used[j] = 1;
+  }
+}
+
+bool Model::pairLaunch(size_t ni, int batch, Launch & L)
+{
+  const int nj = pair_next_[ni];
+  if (nj < 0) return false;
+  Launch A = convLaunch(ni, batch), B = convLaunch((size_t)nj, batch);
+  if (A.kind != Launch::kIgemm || B.kind != Launch::kIgemm) return false;
+  // both convs' 32-channel-chunk LDS-patch packing: [32 rows][9 taps][32 channels]
+  const std::pair<ConvParams *, size_t> convs[2] = {{&A.cp, ni}, {&B.cp, (size_t)nj}};
+  for (const auto & pr : convs) {
+    const Packed & pk = packed_[pr.second];
+    const int hi = 1;  // the ck = 32 segment
+    if (pk.pk.halo[hi] == kNoSeg || pk.pk.kpad_halo[hi] != 288 || !pk.dev) return false;
+    pr.first->w = reinterpret_cast<const __half *>(static_cast<const char *>(pk.dev) + pk.pk.halo[hi]);
+    pr.first->kpad = 288;
+  }
+  const ConvParams & a = A.cp;
+  ConvParams & b = B.cp;
+  auto nhwc16 = [&](const View & v) {
+    return v.layout == kNHWC && v.cs % 8 == 0 && v.img % 8 == 0 && (reinterpret_cast<uintptr_t>(v.ptr) % 16) == 0;
+  };
+  if (!nhwc16(a.x) || !nhwc16(b.y) || a.H != b.H || a.W != b.W) return false;
+  if (b.r.ptr && (b.r.ptr != a.x.ptr || b.r.img != a.x.img || b.r.cs != a.x.cs || b.r.layout != a.x.layout)) return false;
+  const long xl = (long)(batch - 1) * a.x.img + ((long)a.H * a.W - 1) * a.x.cs + 32;
+  const long yl = (long)(batch - 1) * b.y.img + ((long)b.H * b.W - 1) * b.y.cs + 32;
+  if (xl * 2 >= (1L << 31) || yl * 2 >= (1L << 31) || (long)a.W * a.x.cs >= (1L << 23)) return false;
+  int th, tw;
+  if (!pair_plan(b.H, b.W, batch, &th, &tw)) return false;
+  b.th = th;
+  b.tw = tw;
+  b.pipe = b.res = b.halo = b.s2 = 0;
+  b.ksplit = 1;
+  b.ws = nullptr;
+  L.kind = Launch::kPair;
+  L.cp = b;
+  L.cp2 = a;
+  return true;
+}
+
+Launch Model::convLaunch(size_t ni, int batch)
+{
+  const PlanNode & n = nodes_[ni];
+  const Tensor & yt = *T_[n.outs[0]];
+  auto has = [&](size_t i) { return i < n.ins.size() && n.ins[i] != "-"; };
+  auto fail = [&](const std::string & m) { throw std::runtime_error("node " + n.op + " -> " + yt.name + ": " + m); };
+  const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
+  {
+    const Packed & pk = packed_[ni];
+    const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
+    const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
+    Launch L;
+    ConvParams & p = L.cp;
+    p.batch = batch;
+    p.Cout = (int)wt.dims[0];
+    if (is1) {
+      p.Cin = (int)wt.dims[1];
+      const long N = xt.numel / std::max(p.Cin, 1);
+      if (xt.numel != N * p.Cin) fail("x numel not a multiple of Cin");
+      if (xt.dims.size() == 4 && (long)xt.H * xt.W == N && xt.C == p.Cin) { p.H = xt.H; p.W = xt.W; }
+      else { p.H = (int)N; p.W = 1; }
+      p.K = 1; p.S = 1; p.P = 0; p.G = 1;
+      p.Ho = p.H; p.Wo = p.W;
+    } else {
+      p.Cin = xt.C; p.H = xt.H; p.W = xt.W;
+      p.K = is3 ? 3 : n.i("K", 3);
+      p.S = is3 ? n.i("stride", 1) : n.i("S", 1);
+      p.P = is3 ? n.i("pad", 1) : n.i("P", 1);
+      p.G = isg ? n.i("G", 1) : 1;
+      p.Ho = n.i("Hout"); p.Wo = n.i("Wout");
+      if (p.Ho != (p.H + 2 * p.P - p.K) / p.S + 1 || p.Wo != (p.W + 2 * p.P - p.K) / p.S + 1)
+        fail("Hout/Wout inconsistent with input geometry");
+      if (wt.numel != (long)p.Cout * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
+    }
+    if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
+    if (yt.numel != (long)p.Cout * p.Ho * p.Wo) fail("output numel mismatch");
+    p.act = n.i("act");
+    p.x = view(xt.name, batch);
+    p.y = view(yt.name, batch);
+    if (p.y.layout == kNHWC && yt.kind != Tensor::kInit) {
+      const Root & yr = *roots_.at(yt.root);
+      if (yt.coff + p.Cout == yr.C) p.ypad = yr.cs - yr.C;
+    }
+    if (has(3)) {
+      const Tensor & rt = *T_[n.ins[3]];
+      if (rt.numel != yt.numel) fail("residual numel mismatch");
+      p.r = view(rt.name, batch);
+    }
+    // single-pixel tensors: NCHW and NHWC coincide; present them channels-last
+    auto pix1 = [](View & v, int C) { v.layout = kNHWC; v.cs = (int)round_up(C, 8); };
+    if (p.H * p.W == 1) pix1(p.x, p.Cin);
+    if (p.Ho * p.Wo == 1) { pix1(p.y, p.Cout); if (p.r.ptr) pix1(p.r, p.Cout); }
+    if (!pk.dev || pk.spec.Cin != p.Cin || pk.spec.Cout != p.Cout || pk.spec.H != p.H || pk.spec.W != p.W ||
+        pk.spec.K != p.K || pk.spec.G != p.G || pk.spec.Ho() != p.Ho || pk.spec.Wo() != p.Wo)
+      fail("packed conv geometry");
+    int k;
+    try {
+      k = conv_resolve(pk.spec, pk.pk, pk.dev, batch, (flags_ & IVH_FLAG_NO_SPLITK) ? nullptr : ws_, p);
+    } catch (const std::exception & e) {
+      fail(e.what());
+    }
+    L.kind = k == kLaunchIgemm ? Launch::kIgemm : (k == kLaunchDirect ? Launch::kDirect : Launch::kDw);
+    return L;
+  }
+
+  fail("not a conv node");
+  return Launch{};
+}
+
 void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vector<char> & covered)
 {
   const PlanNode & n = nodes_[ni];
@@ -1335,61 +1494,15 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
   }
   const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
   if (is1 || is3 || isg) {
-    const Packed & pk = packed_[ni];
-    const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
-    const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
-    Launch L;
-    ConvParams & p = L.cp;
-    p.batch = batch;
-    p.Cout = (int)wt.dims[0];
-    if (is1) {
-      p.Cin = (int)wt.dims[1];
-      const long N = xt.numel / std::max(p.Cin, 1);
-      if (xt.numel != N * p.Cin) fail("x numel not a multiple of Cin");
-      if (xt.dims.size() == 4 && (long)xt.H * xt.W == N && xt.C == p.Cin) { p.H = xt.H; p.W = xt.W; }
-      else { p.H = (int)N; p.W = 1; }
-      p.K = 1; p.S = 1; p.P = 0; p.G = 1;
-      p.Ho = p.H; p.Wo = p.W;
-    } else {
-      p.Cin = xt.C; p.H = xt.H; p.W = xt.W;
-      p.K = is3 ? 3 : n.i("K", 3);
-      p.S = is3 ? n.i("stride", 1) : n.i("S", 1);
-      p.P = is3 ? n.i("pad", 1) : n.i("P", 1);
-      p.G = isg ? n.i("G", 1) : 1;
-      p.Ho = n.i("Hout"); p.Wo = n.i("Wout");
-      if (p.Ho != (p.H + 2 * p.P - p.K) / p.S + 1 || p.Wo != (p.W + 2 * p.P - p.K) / p.S + 1)
-        fail("Hout/Wout inconsistent with input geometry");
-      if (wt.numel != (long)p.Cout * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
+    if (pair_next_[ni] >= 0) {
+      Launch P;
+      if (pairLaunch(ni, batch, P)) {
+        out.push_back(P);
+        covered[pair_next_[ni]] = 1;
+        return;
+      }
     }
-    if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
-    if (yt.numel != (long)p.Cout * p.Ho * p.Wo) fail("output numel mismatch");
-    p.act = n.i("act");
-    p.x = view(xt.name, batch);
-    p.y = view(yt.name, batch);
-    if (p.y.layout == kNHWC && yt.kind != Tensor::kInit) {
-      const Root & yr = *roots_.at(yt.root);
-      if (yt.coff + p.Cout == yr.C) p.ypad = yr.cs - yr.C;
-    }
-    if (has(3)) {
-      const Tensor & rt = *T_[n.ins[3]];
-      if (rt.numel != yt.numel) fail("residual numel mismatch");
-      p.r = view(rt.name, batch);
-    }
-    // single-pixel tensors: NCHW and NHWC coincide; present them channels-last
-    auto pix1 = [](View & v, int C) { v.layout = kNHWC; v.cs = (int)round_up(C, 8); };
-    if (p.H * p.W == 1) pix1(p.x, p.Cin);
-    if (p.Ho * p.Wo == 1) { pix1(p.y, p.Cout); if (p.r.ptr) pix1(p.r, p.Cout); }
-    if (!pk.dev || pk.spec.Cin != p.Cin || pk.spec.Cout != p.Cout || pk.spec.H != p.H || pk.spec.W != p.W ||
-        pk.spec.K != p.K || pk.spec.G != p.G || pk.spec.Ho() != p.Ho || pk.spec.Wo() != p.Wo)
-      fail("packed conv geometry");
-    int k;
-    try {
-      k = conv_resolve(pk.spec, pk.pk, pk.dev, batch, (flags_ & IVH_FLAG_NO_SPLITK) ? nullptr : ws_, p);
-    } catch (const std::exception & e) {
-      fail(e.what());
-    }
-    L.kind = k == kLaunchIgemm ? Launch::kIgemm : (k == kLaunchDirect ? Launch::kDirect : Launch::kDw);
-    out.push_back(L);
+    out.push_back(convLaunch(ni, batch));
     return;
   }
 
@@ -1737,6 +1850,29 @@ void Model::validate(const Launch & l) const
     check(d.y.ptr, 0, vlast(d.y, d.batch, ny, d.A), 2, "decode y");
     return;
   }
+  if (l.kind == Launch::kPair) {
+    const ConvParams & a = l.cp2;
+    const ConvParams & p = l.cp;
+    const long HW = (long)p.H * p.W;
+    if (p.batch < 1 || p.batch > 65535 || a.batch != p.batch) throw std::runtime_error("batch out of grid range");
+    if (a.Cin != 32 || a.Cout != 32 || p.Cin != 32 || p.Cout != 32 || a.K != 3 || p.K != 3 || a.S != 1 || p.S != 1 ||
+        a.P != 1 || p.P != 1 || a.H != p.H || a.W != p.W || p.Ho != p.H || p.Wo != p.W || a.kpad != 288 || p.kpad != 288)
+      throw std::runtime_error("conv pair geometry");
+    if (p.th < 1 || p.tw < 1 || (p.th + 2) * (p.tw + 2) > 512 || p.th * p.tw > 512 || (p.th + 4) * (p.tw + 4) > 640 || p.th + 4 > 36 ||
+        p.th + 4 > p.H + 1 || (long)p.batch * (p.H + 1) >= (1L << 22))
+      throw std::runtime_error("conv pair tile");
+    for (const View * v : {&a.x, &p.y})
+      if (v->layout != kNHWC || v->cs % 8 || v->img % 8 || (reinterpret_cast<uintptr_t>(v->ptr) % 16))
+        throw std::runtime_error("conv pair views");
+    if (p.r.ptr && p.r.ptr != a.x.ptr) throw std::runtime_error("conv pair residual is not the pair's input");
+    check(a.x.ptr, 0, vlast(a.x, p.batch, 32, HW), 2, "conv pair x");
+    check(p.y.ptr, 0, vlast(p.y, p.batch, 32, HW), 2, "conv pair y");
+    check(a.w, 0, 32L * 288 - 1, 2, "conv pair first weights");
+    check(p.w, 0, 32L * 288 - 1, 2, "conv pair second weights");
+    if (a.bias) check(a.bias, 0, 31, 4, "conv pair first bias");
+    if (p.bias) check(p.bias, 0, 31, 4, "conv pair second bias");
+    return;
+  }
   if (l.kind != Launch::kSmall) {
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
@@ -1926,6 +2062,7 @@ void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
     case Launch::kDw: launch_dwconv(l.cp, stream_); break;
     case Launch::kDecode: launch_pose_decode(l.dp, stream_); break;
     case Launch::kAttn: launch_attention(l.ap, stream_); break;
+    case Launch::kPair: launch_conv_pair(l.cp2, l.cp, stream_); break;
     default: launch_small(l.small, l.sp, stream_); break;
     }
   }
@@ -2180,6 +2317,9 @@ std::string Model::nodeTag(int i)
   const Launch & l = P.L[P.begin[i]];
   if (l.kind == Launch::kIgemm) return k + " " + igemm_launch_tag(l.cp);
   if (l.kind == Launch::kDw) return k + " " + dw_launch_tag(l.cp);
+  if (l.kind == Launch::kPair)
+    return k + " th=" + std::to_string(l.cp.th) + " tw=" + std::to_string(l.cp.tw) + " tiles=" +
+           std::to_string(pair_tiles(l.cp.H, l.cp.W, l.cp.batch, l.cp.th, l.cp.tw)) + (l.cp.r.ptr ? " +res" : "");
   return k;
 }
 
@@ -2196,6 +2336,7 @@ std::string Model::nodeKernel(int i)
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";
   case Launch::kAttn: return "attention";
+  case Launch::kPair: return "conv_pair";
   case Launch::kSmall:
     if (l.small == kMaxPoolSppf) return "maxpool_sppf";
     return s.kernel;

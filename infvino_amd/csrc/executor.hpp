@@ -26,9 +26,10 @@ struct PlanNode {
 
 // One kernel launch with everything resolved for a given batch size.
 struct Launch {
-  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode, kAttn } kind = kSmall;
+  enum Kind { kIgemm, kDirect, kDw, kSmall, kDecode, kAttn, kPair } kind = kSmall;
   int small = 0;
   ConvParams cp;
+  ConvParams cp2;  // kPair: the first conv of the pair (cp is the second)
   SmallParams sp;
   DecodeParams dp;
   AttnParams ap;
@@ -113,6 +114,14 @@ class Model {
   // `covered`: nodes whose work a launch of node ni already does (they emit nothing)
   void emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vector<char> & covered);
   bool sppfChain(size_t ni) const;
+  // C2f / C3k2 bottleneck pairs (conv_pair.hip): pair_next_[ni] = node of the second conv
+  // when node ni is the first conv of a pair, else -1 (decided at load, before allocate)
+  void findPairs();
+  std::vector<int> pair_next_;
+  // the launch of a conv node (conv1x1 / conv3x3 / conv_general) at a batch size
+  Launch convLaunch(size_t ni, int batch);
+  // node ni and its pair partner as one kPair launch; false when a view does not suit it
+  bool pairLaunch(size_t ni, int batch, Launch & L);
   void validate(const Launch & l) const;
   void * devAlloc(size_t bytes, bool zero);
   void devUpload(void * d, const void * src, size_t bytes);

@@ -62,6 +62,13 @@ bool pipe_views_ok(const ConvParams & p);
 constexpr int kPipeMinItems = 256;  // fewer items: the other 3x3 kernels
 void launch_conv_pipe(const ConvParams & p, hipStream_t s);
 
+// conv_pair.hip: two chained 3x3 stride-1 convs of 32 channels (a bottleneck) in one launch
+bool pair_plan(int H, int W, int batch, int * th, int * tw);  // output tile; false: not eligible
+long pair_tiles(int H, int W, int batch, int th, int tw);
+// a: the first conv (x, weights / bias / act of conv 1), b: the second (y, residual,
+// weights / bias / act of conv 2, th x tw); both weights in the 32-channel halo packing
+void launch_conv_pair(const ConvParams & a, const ConvParams & b, hipStream_t s);
+
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
 bool s2_plan(int cin, int cout, int Ho, int Wo, int * cfg, int * th, int * tw);
 int s2_patch(int th, int tw);  // patch pixels of a th x tw output tile

@@ -56,8 +56,9 @@ def test_kernel_choice_yolov8(plans):
     LDS-patch kernel for the 16->32 downsample, the implicit GEMM for the 32->64 one, the
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
     Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
-    40x40 maps (enough items for its persistent grid) and the stride-1 LDS-patch kernel for
-    the rest."""
+    40x40 maps (enough items for its persistent grid), the fused pair kernel for the three
+    32-channel bottlenecks at 80x80 (their second conv then launches nothing) and the
+    stride-1 LDS-patch kernel for the rest."""
     m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
@@ -68,13 +69,16 @@ def test_kernel_choice_yolov8(plans):
     s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), int(i["desc"].split()[1].split("x")[1]),
            "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
 
-    def want(cin, hw, res):
+    def want(k, cin, hw, res):
+        if cin == 32 and hw == 80 and k in ("conv_pair", "(fused)"):  # bottleneck pairs, one launch
+            return True
         if 16 < cin <= 64 and not (res and cin <= 32):
-            return "conv_res"
-        return "conv_pipe" if cin > 64 and hw >= 40 else "conv_halo"
-    assert s1 and all(k == want(cin, hw, res) for k, cin, hw, res in s1)
-    assert sum(k == "conv_res" for k, _, _, _ in s1) >= 20
+            return k == "conv_res"
+        return k == ("conv_pipe" if cin > 64 and hw >= 40 else "conv_halo")
+    assert s1 and all(want(k, cin, hw, res) for k, cin, hw, res in s1)
+    assert sum(k == "conv_res" for k, _, _, _ in s1) >= 16
     assert sum(k == "conv_pipe" for k, _, _, _ in s1) >= 3
+    assert sum(k == "conv_pair" for k, _, _, _ in s1) == 3 and sum(k == "(fused)" for k, _, _, _ in s1) == 3
     m.close()
 
 
