@@ -1260,9 +1260,9 @@ bool Model::sppfChain(size_t ni) const
   return true;
 }
 
-// Bottleneck pairs: node A = conv3x3 (stride 1, pad 1, 32 -> 32 channels, no residual) whose
-// output has one reader, node B = conv3x3 (stride 1, pad 1, 32 -> 32) on it, B's residual none
-// or A's input, both activations among those the kernel has.  Structural only: whether the
+// Bottleneck pairs: node A = conv3x3 (stride 1, pad 1, C -> C channels with C = 16 or 32, no
+// residual) whose output has one reader, node B = conv3x3 (stride 1, pad 1, C -> C) on it, B's
+// residual none or A's input, both activations among those the kernel has.  Structural only: whether the
 // pair runs fused also depends on the views (pairLaunch); the liveness that allocate gives
 // a pair is harmless when it does not.
 void Model::findPairs()
@@ -1275,24 +1275,28 @@ void Model::findPairs()
       if (in != "-") readers[in].push_back((int)i);
   std::set<std::string> outs(outputs_.begin(), outputs_.end());
   auto act_ok = [](int a) { return a == kActNone || a == kActSiLU || a == kActReLU || a == kActHSwish; };
-  auto conv32 = [&](const PlanNode & n) {
+  // channels of a conv that can be a pair member, else 0
+  auto pair_c = [&](const PlanNode & n) {
     if (n.op != "conv3x3" || n.ins.size() < 2 || n.outs.size() != 1 || n.i("stride", 1) != 1 || n.i("pad", 1) != 1)
-      return false;
+      return 0;
     const Tensor & w = *T_.at(n.ins[1]);
     const Tensor & x = *T_.at(n.ins[0]);
-    return w.dims.size() == 4 && w.dims[0] == 32 && w.dims[1] == 32 && w.dims[2] == 3 && w.dims[3] == 3 &&
-           x.C == 32 && n.i("Hout") == x.H && n.i("Wout") == x.W && act_ok(n.i("act"));
+    const int c = x.C;
+    const bool ok = (c == 16 || c == 32) && w.dims.size() == 4 && w.dims[0] == c && w.dims[1] == c &&
+                    w.dims[2] == 3 && w.dims[3] == 3 && n.i("Hout") == x.H && n.i("Wout") == x.W && act_ok(n.i("act"));
+    return ok ? c : 0;
   };
   std::vector<char> used(nodes_.size(), 0);
   for (size_t i = 0; i < nodes_.size(); ++i) {
     const PlanNode & a = nodes_[i];
-    if (used[i] || !conv32(a) || (a.ins.size() > 3 && a.ins[3] != "-")) continue;
+    const int c = used[i] ? 0 : pair_c(a);
+    if (!c || (a.ins.size() > 3 && a.ins[3] != "-")) continue;
     const std::string & t = a.outs[0];
     const auto it = readers.find(t);
     if (it == readers.end() || it->second.size() != 1 || outs.count(t)) continue;
     const int j = it->second[0];
     const PlanNode & b = nodes_[j];
-    if (j <= (int)i || used[j] || !conv32(b) || b.ins[0] != t) continue;
+    if (j <= (int)i || used[j] || pair_c(b) != c || b.ins[0] != t) continue;
     if (b.ins.size() > 3 && b.ins[3] != "-" && b.ins[3] != a.ins[0]) continue;
     if (T_.at(b.ins[0])->H != T_.at(a.ins[0])->H || T_.at(b.ins[0])->W != T_.at(a.ins[0])->W) continue;
     pair_next_[i] = j;
@@ -1306,14 +1310,16 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   if (nj < 0) return false;
   Launch A = convLaunch(ni, batch), B = convLaunch((size_t)nj, batch);
   if (A.kind != Launch::kIgemm || B.kind != Launch::kIgemm) return false;
-  // both convs' 32-channel-chunk LDS-patch packing: [32 rows][9 taps][32 channels]
+  // both convs' LDS-patch packing of one channel chunk: [C rows][taps][C channels], 9 taps
+  // with C = 32, 10 (a zero tenth) with C = 16
+  const int C = A.cp.Cin, hi = C == 16 ? 0 : 1, kpad = halo_taps(C) * C;  // halo segments 0: ck 16, 1: ck 32
+  if ((C != 16 && C != 32) || B.cp.Cin != C || A.cp.Cout != C || B.cp.Cout != C) return false;
   const std::pair<ConvParams *, size_t> convs[2] = {{&A.cp, ni}, {&B.cp, (size_t)nj}};
   for (const auto & pr : convs) {
     const Packed & pk = packed_[pr.second];
-    const int hi = 1;  // the ck = 32 segment
-    if (pk.pk.halo[hi] == kNoSeg || pk.pk.kpad_halo[hi] != 288 || !pk.dev) return false;
+    if (pk.pk.halo[hi] == kNoSeg || pk.pk.kpad_halo[hi] != kpad || !pk.dev) return false;
     pr.first->w = reinterpret_cast<const __half *>(static_cast<const char *>(pk.dev) + pk.pk.halo[hi]);
-    pr.first->kpad = 288;
+    pr.first->kpad = kpad;
   }
   const ConvParams & a = A.cp;
   ConvParams & b = B.cp;
@@ -1322,11 +1328,11 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   };
   if (!nhwc16(a.x) || !nhwc16(b.y) || a.H != b.H || a.W != b.W) return false;
   if (b.r.ptr && (b.r.ptr != a.x.ptr || b.r.img != a.x.img || b.r.cs != a.x.cs || b.r.layout != a.x.layout)) return false;
-  const long xl = (long)(batch - 1) * a.x.img + ((long)a.H * a.W - 1) * a.x.cs + 32;
-  const long yl = (long)(batch - 1) * b.y.img + ((long)b.H * b.W - 1) * b.y.cs + 32;
+  const long xl = (long)(batch - 1) * a.x.img + ((long)a.H * a.W - 1) * a.x.cs + C;
+  const long yl = (long)(batch - 1) * b.y.img + ((long)b.H * b.W - 1) * b.y.cs + C;
   if (xl * 2 >= (1L << 31) || yl * 2 >= (1L << 31) || (long)a.W * a.x.cs >= (1L << 23)) return false;
   int th, tw;
-  if (!pair_plan(b.H, b.W, batch, &th, &tw)) return false;
+  if (!pair_plan(C, b.H, b.W, batch, &th, &tw)) return false;
   b.th = th;
   b.tw = tw;
   b.pipe = b.res = b.halo = b.s2 = 0;
@@ -1855,22 +1861,23 @@ void Model::validate(const Launch & l) const
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W;
     if (p.batch < 1 || p.batch > 65535 || a.batch != p.batch) throw std::runtime_error("batch out of grid range");
-    if (a.Cin != 32 || a.Cout != 32 || p.Cin != 32 || p.Cout != 32 || a.K != 3 || p.K != 3 || a.S != 1 || p.S != 1 ||
-        a.P != 1 || p.P != 1 || a.H != p.H || a.W != p.W || p.Ho != p.H || p.Wo != p.W || a.kpad != 288 || p.kpad != 288)
+    const int C = a.Cin;
+    if ((C != 16 && C != 32) || a.Cout != C || p.Cin != C || p.Cout != C || a.K != 3 || p.K != 3 || a.S != 1 ||
+        p.S != 1 || a.P != 1 || p.P != 1 || a.H != p.H || a.W != p.W || p.Ho != p.H || p.Wo != p.W ||
+        a.kpad != halo_taps(C) * C || p.kpad != halo_taps(C) * C)
       throw std::runtime_error("conv pair geometry");
-    if (p.th < 1 || p.tw < 1 || (p.th + 2) * (p.tw + 2) > 512 || p.th * p.tw > 512 || (p.th + 4) * (p.tw + 4) > 640 || p.th + 4 > 36 ||
-        p.th + 4 > p.H + 1 || (long)p.batch * (p.H + 1) >= (1L << 22))
+    if (!pair_tile_ok(C, p.th, p.tw) || p.th + 4 > p.H + 1 || (long)p.batch * (p.H + 1) >= (1L << 22))
       throw std::runtime_error("conv pair tile");
     for (const View * v : {&a.x, &p.y})
       if (v->layout != kNHWC || v->cs % 8 || v->img % 8 || (reinterpret_cast<uintptr_t>(v->ptr) % 16))
         throw std::runtime_error("conv pair views");
     if (p.r.ptr && p.r.ptr != a.x.ptr) throw std::runtime_error("conv pair residual is not the pair's input");
-    check(a.x.ptr, 0, vlast(a.x, p.batch, 32, HW), 2, "conv pair x");
-    check(p.y.ptr, 0, vlast(p.y, p.batch, 32, HW), 2, "conv pair y");
-    check(a.w, 0, 32L * 288 - 1, 2, "conv pair first weights");
-    check(p.w, 0, 32L * 288 - 1, 2, "conv pair second weights");
-    if (a.bias) check(a.bias, 0, 31, 4, "conv pair first bias");
-    if (p.bias) check(p.bias, 0, 31, 4, "conv pair second bias");
+    check(a.x.ptr, 0, vlast(a.x, p.batch, C, HW), 2, "conv pair x");
+    check(p.y.ptr, 0, vlast(p.y, p.batch, C, HW), 2, "conv pair y");
+    check(a.w, 0, (long)C * a.kpad - 1, 2, "conv pair first weights");
+    check(p.w, 0, (long)C * p.kpad - 1, 2, "conv pair second weights");
+    if (a.bias) check(a.bias, 0, C - 1, 4, "conv pair first bias");
+    if (p.bias) check(p.bias, 0, C - 1, 4, "conv pair second bias");
     return;
   }
   if (l.kind != Launch::kSmall) {

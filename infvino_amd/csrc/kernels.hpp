@@ -62,8 +62,10 @@ bool pipe_views_ok(const ConvParams & p);
 constexpr int kPipeMinItems = 256;  // fewer items: the other 3x3 kernels
 void launch_conv_pipe(const ConvParams & p, hipStream_t s);
 
-// conv_pair.hip: two chained 3x3 stride-1 convs of 32 channels (a bottleneck) in one launch
-bool pair_plan(int H, int W, int batch, int * th, int * tw);  // output tile; false: not eligible
+// conv_pair.hip: two chained 3x3 stride-1 convs of C = 16 or 32 channels (a bottleneck) in
+// one launch
+bool pair_plan(int C, int H, int W, int batch, int * th, int * tw);  // output tile; false: not eligible
+bool pair_tile_ok(int C, int th, int tw);  // the tile fits the kernel's ring, patch and rows
 long pair_tiles(int H, int W, int batch, int th, int tw);
 // a: the first conv (x, weights / bias / act of conv 1), b: the second (y, residual,
 // weights / bias / act of conv 2, th x tw); both weights in the 32-channel halo packing

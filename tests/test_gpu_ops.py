@@ -207,26 +207,30 @@ def test_pipe_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
-@pytest.mark.parametrize("H,W,batch,res,act1,act2", [
-    (80, 80, 2, True, pw.ACT_SILU, pw.ACT_SILU),     # the YOLOv8 C2f bottleneck at 80x80
-    (80, 80, 3, False, pw.ACT_SILU, pw.ACT_SILU),    # no shortcut (the neck's C2f)
-    (33, 35, 2, True, pw.ACT_HSWISH, pw.ACT_RELU),   # odd map: ragged tiles on both axes
-    (20, 20, 6, True, pw.ACT_SILU, pw.ACT_NONE),     # small maps: tiles across image boundaries
-    (40, 40, 1, False, pw.ACT_RELU, pw.ACT_SILU),    # batch 1
-    (80, 80, 16, True, pw.ACT_SILU, pw.ACT_SILU),    # several tiles per work-group
+@pytest.mark.parametrize("C,H,W,batch,res,act1,act2", [
+    (32, 80, 80, 2, True, pw.ACT_SILU, pw.ACT_SILU),     # the YOLOv8 C2f bottleneck at 80x80
+    (32, 80, 80, 3, False, pw.ACT_SILU, pw.ACT_SILU),    # no shortcut (the neck's C2f)
+    (32, 33, 35, 2, True, pw.ACT_HSWISH, pw.ACT_RELU),   # odd map: ragged tiles on both axes
+    (32, 20, 20, 6, True, pw.ACT_SILU, pw.ACT_NONE),     # small maps: tiles across image boundaries
+    (32, 40, 40, 1, False, pw.ACT_RELU, pw.ACT_SILU),    # batch 1
+    (32, 80, 80, 16, True, pw.ACT_SILU, pw.ACT_SILU),    # several tiles per work-group
+    (16, 160, 160, 2, True, pw.ACT_SILU, pw.ACT_SILU),   # the YOLOv8 C2f bottleneck at 160x160
+    (16, 33, 35, 3, False, pw.ACT_HSWISH, pw.ACT_RELU),  # 16 channels: ragged tiles, no shortcut
+    (16, 20, 20, 6, True, pw.ACT_RELU, pw.ACT_NONE),     # 16 channels: tiles across image boundaries
+    (16, 160, 160, 9, True, pw.ACT_SILU, pw.ACT_SILU),   # 16 channels: several tiles per work-group
 ])
-def test_conv_pair(tmp_path, H, W, batch, res, act1, act2):
-    """A 32-channel bottleneck (3x3 -> 3x3, optionally + the block input) as one launch of the
-    fused pair kernel vs the oracle and vs the two convs run apart."""
+def test_conv_pair(tmp_path, C, H, W, batch, res, act1, act2):
+    """A bottleneck of C = 16 or 32 channels (3x3 -> 3x3, optionally + the block input) as one
+    launch of the fused pair kernel vs the oracle and vs the two convs run apart."""
     def build(pb):
-        x = pb.unary(pb.input("x", [1, 32, H, W]), pw.UN_RELU)
-        t = pb.conv(x, 32, 3, act=act1)
-        t = pb.conv(t, 32, 3, act=act2)
+        x = pb.unary(pb.input("x", [1, C, H, W]), pw.UN_RELU)
+        t = pb.conv(x, C, 3, act=act1)
+        t = pb.conv(t, C, 3, act=act2)
         if res:
             t = pb.binary(x, t, 0)
         return pb.unary(t, pw.UN_RELU)
     path = _small_plan(tmp_path, build)
-    print(f"conv pair {H}x{W} batch {batch} res {res} acts {act1} {act2}", flush=True)
+    print(f"conv pair C {C} {H}x{W} batch {batch} res {res} acts {act1} {act2}", flush=True)
     assert _kernels(path, batch).count("conv_pair") == 1
     assert "conv_pair" not in _kernels(path, batch, ia.IVH_FLAG_NO_FUSE_PAIR)
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)

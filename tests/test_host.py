@@ -57,8 +57,8 @@ def test_kernel_choice_yolov8(plans):
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
     Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
     40x40 maps (enough items for its persistent grid), the fused pair kernel for the three
-    32-channel bottlenecks at 80x80 (their second conv then launches nothing) and the
-    stride-1 LDS-patch kernel for the rest."""
+    32-channel bottlenecks at 80x80 and the 16-channel one at 160x160 (their second conv then
+    launches nothing) and the stride-1 LDS-patch kernel for the rest."""
     m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
@@ -70,7 +70,7 @@ def test_kernel_choice_yolov8(plans):
            "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
 
     def want(k, cin, hw, res):
-        if cin == 32 and hw == 80 and k in ("conv_pair", "(fused)"):  # bottleneck pairs, one launch
+        if (cin, hw) in ((32, 80), (16, 160)) and k in ("conv_pair", "(fused)"):  # bottleneck pairs, one launch
             return True
         if 16 < cin <= 64 and not (res and cin <= 32):
             return k == "conv_res"
@@ -78,7 +78,7 @@ def test_kernel_choice_yolov8(plans):
     assert s1 and all(want(k, cin, hw, res) for k, cin, hw, res in s1)
     assert sum(k == "conv_res" for k, _, _, _ in s1) >= 16
     assert sum(k == "conv_pipe" for k, _, _, _ in s1) >= 3
-    assert sum(k == "conv_pair" for k, _, _, _ in s1) == 3 and sum(k == "(fused)" for k, _, _, _ in s1) == 3
+    assert sum(k == "conv_pair" for k, _, _, _ in s1) == 4 and sum(k == "(fused)" for k, _, _, _ in s1) == 4
     m.close()
 
 
