@@ -66,8 +66,10 @@ extern "C" {
 #define IVH_FLAG_DRY_RUN 0x40u    /* no device: plan, pack and bounds-check launches only
                                      (ivh_run validates, data calls fail) */
 #define IVH_FLAG_NO_PIPE 0x2000u  /* 3x3 stride-1 convs never use the DMA-pipelined kernel */
-#define IVH_FLAG_NO_FUSE_PAIR 0x8000u /* run a C2f / C3k2 bottleneck's two 3x3 convs (32
-                                        channels) as two launches, not one */
+#define IVH_FLAG_NO_FUSE_PAIR 0x8000u /* run a C2f / C3k2 bottleneck's two 3x3 convs (16 or
+                                        32 channels) as two launches, not one */
+#define IVH_FLAG_NO_S2_PERSIST 0x10000u /* 3x3 stride-2 convs never use the persistent
+                                           resident-weight kernel */
 #define IVH_FLAG_PIPE_ANY 0x4000u /* 3x3 stride-1 convs use the DMA-pipelined kernel wherever it
                                      applies (Cin >= 32, any grid size), not only where it is
                                      measured fastest */

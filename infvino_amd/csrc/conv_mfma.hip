@@ -404,6 +404,8 @@ std::string igemm_launch_tag(const ConvParams & p)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d ck=%d store=%d", p.res - 1, p.th, p.tw, p.ck, res_store_width(p));
   else if (p.halo)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d ck=%d", p.halo - 1, p.th, p.tw, p.ck);
+  else if (p.s2 > 2)
+    snprintf(b, sizeof b, "cfg=%d th=%d tw=%d tiles=%ld", p.s2 - 1, p.th, p.tw, s2pk_tiles(p));
   else if (p.s2)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d", p.s2 - 1, p.th, p.tw);
   else

@@ -253,6 +253,27 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
       }
     }
   }
+  // 3x3 stride 2 with 16 or 32 (padded) input channels, Cout <= 64, no residual: the
+  // persistent resident-weight kernel of conv_s2.hip on the implicit-GEMM packing, when its
+  // tiles fill the persistent grid several times over.
+  const bool act_ok = p.act == kActNone || p.act == kActSiLU || p.act == kActReLU || p.act == kActHSwish;
+  if (!p.halo && p.K == 3 && p.S == 2 && p.P == 1 && !(s.flags & IVH_FLAG_NO_S2_PERSIST) && act_ok &&
+      (pk.cin8 == 16 || pk.cin8 == 32) && p.Cout <= 64 && pk.kpad >= 9 * pk.cin8 &&
+      p.Ho == (p.H - 1) / 2 + 1 && p.Wo == (p.W - 1) / 2 + 1 && s2pk_views_ok(p)) {
+    const int cfg = (pk.cin8 == 16 ? 2 : 4) + (p.Cout > 32 ? 1 : 0);
+    ConvParams q = p;
+    q.s2 = cfg + 1;
+    if (s2pk_tiles(q) >= kS2PkMinTiles) {
+      p.s2 = cfg + 1;
+      p.th = 8 / s2pk_cb(cfg);
+      p.tw = 16;
+      p.ksplit = 1;
+      p.ws = nullptr;
+      if (p.x.layout != kNHWC || (p.x.cs % 8) || (p.x.img % 8) || (reinterpret_cast<uintptr_t>(p.x.ptr) % 16))
+        throw std::runtime_error("implicit-GEMM input view not 16-byte aligned NHWC");
+      return kLaunchIgemm;
+    }
+  }
   // small-channel stride-2 convs: the LDS-patch kernel of conv_s2.hip on the same packing
   int sc;
   if (!p.halo && p.K == 3 && p.S == 2 && p.P == 1 && s2_plan(p.Cin, p.Cout, p.Ho, p.Wo, &sc, &th, &tw) &&

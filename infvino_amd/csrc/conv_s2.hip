@@ -15,10 +15,17 @@
 // the K loop has no stage and no barrier: the only barriers are "patch and weights in LDS"
 // and "patch consumed" (the epilogue then stages the output tile in the patch's LDS).
 // Weights use the implicit-GEMM packing fp16 [Cout_pad128][kpad], k = tap * CK + ci.
+#include <algorithm>
+
 #include "conv_common.hpp"
 #include "kernels.hpp"
 
 namespace ivh {
+
+namespace {
+typedef unsigned u2q __attribute__((ext_vector_type(2)));
+typedef unsigned u4q __attribute__((ext_vector_type(4)));
+}  // namespace
 
 template <int CK, int WGM, int WGN, int TN, int PMAX>
 __global__ void __launch_bounds__(256) conv3x3s2_kernel(const ConvParams p)
@@ -139,6 +146,228 @@ __global__ void __launch_bounds__(256) conv3x3s2_kernel(const ConvParams p)
   });
 }
 
+// ---------------------------------------------------------------- persistent kernel
+//
+// 3x3 stride-2 pad-1 convs of CK = 16 or 32 input channels (Cin <= CK), Cout <= 32 CB: the
+// work-group's weights [32 CB][9 CK] stay in LDS for the whole launch, and the grid is
+// persistent over TH x 16 output tiles (contiguous tile ranges, XCD-aware), the next
+// tile's input patch in flight in registers while the current one is computed.
+//
+// The (2TH+1) x 33 input patch sits in LDS de-interleaved by column parity: every patch row
+// holds its 17 even columns, then its 16 odd ones, so the three horizontal taps of a stride-2
+// output row read consecutive pixels (dx = 0: even column tx, 1: odd column tx, 2: even
+// column tx + 1).  gfx950 serves a ds_read_b128 in 16-lane groups (per half-wave, the quads
+// of even and of odd bit parity) over 64 four-byte banks: a fragment of 32 pixels = two
+// 16-wide output rows is conflict free when the pixel pitch is an odd number of 16-byte
+// slots (48 bytes with 16 channels, 80 with 32) and two patch rows span a multiple of 256
+// bytes (row pitch a multiple of 128 bytes), so that both output rows fall on one bank
+// pattern.
+//
+// Waves: 4, each one 32-pixel block (two output rows) x one 32-channel block, K = 9 CK in
+// slices of 16 on one accumulator (v_mfma_f32_32x32x16_f16).  With CB = 1 the tile is 8 x
+// 16 (four pixel blocks), with CB = 2 it is 4 x 16.  Epilogue in registers: bias + act in
+// fp32, one fp16 rounding, 8 consecutive channels per lane after a permlane32 swap, 16-byte
+// stores (NHWC output, Cout padded to 8 by the view).
+namespace {
+template <int CK> struct S2P {
+  static constexpr int CKP = CK + 8;                     // pixel pitch (halves): odd 16-byte slots
+  static constexpr int ODD = 17 * CKP;                   // odd-column plane of a patch row
+  static constexpr int RH = (33 * CKP + 63) / 64 * 64;   // row pitch (halves): multiple of 128 bytes
+  static constexpr int LDW = 9 * CK + 8;                 // weight row pitch (halves): odd slots
+};
+}  // namespace
+
+template <int CK, int CB, int ACT>
+__global__ void __launch_bounds__(256, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(const ConvParams p)
+{
+  using F = Mf<32>;
+  using L = S2P<CK>;
+  typedef F::acc_t acc_t;
+  constexpr int PB = 4 / CB;            // pixel blocks per tile
+  constexpr int TH = 2 * PB, TW = 16;   // output tile
+  constexpr int PR = 2 * TH + 1;        // patch rows
+  constexpr int CQ = CK / 8;            // 16-byte pieces per pixel
+  constexpr int NPC = PR * 33 * CQ;     // patch pieces
+  constexpr int P_IT = (NPC + 255) / 256;
+  constexpr int BN = 32 * CB;
+  constexpr int WQ = 9 * CK / 8;        // 16-byte pieces per weight row
+  constexpr int W_IT = (BN * WQ + 255) / 256;
+  constexpr int NSL = 9 * CK / 16;      // K slices
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[BN * L::LDW];
+  __shared__ __attribute__((aligned(16))) _Float16 Ps[PR * L::RH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pb = wave % PB, cb = wave / PB;
+  const int tiles_x = (p.Wo + TW - 1) / TW, tiles_y = (p.Ho + TH - 1) / TH;
+  const int tiles_img = tiles_x * tiles_y, ntiles = p.batch * tiles_img;
+  const int G = gridDim.x, r = xcd_tile(blockIdx.x, G);
+  const int t_lo = (int)((long)r * ntiles / G), t_hi = (int)((long)(r + 1) * ntiles / G);
+  const int ntl = t_hi - t_lo;
+  if (ntl <= 0) return;
+
+  const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
+  const long y_last = (long)(p.batch - 1) * p.y.img + ((long)p.Ho * p.Wo - 1) * p.y.cs + (p.Cout + 7) / 8 * 8;
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(p.y.ptr, (short)0, (int)(y_last * 2), kBufDword3);
+
+  // weights [BN][9 CK] (implicit-GEMM packing, k = tap * CK + ci), once per launch
+  {
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__half *>(p.w), (short)0, BN * p.kpad * 2, kBufDword3);
+    h8 rw[W_IT];
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i) {
+      const int e = tid + i * 256, row = e / WQ;
+      rw[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+          wr, row < BN ? (unsigned)((row * p.kpad + (e - row * WQ) * 8) * 2) : kBufOOB, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < W_IT; ++i) {
+      const int e = tid + i * 256, row = e / WQ;
+      if (row < BN) *reinterpret_cast<h8 *>(Ws + row * L::LDW + (e - row * WQ) * 8) = rw[i];
+    }
+  }
+  // bias of the lane's 16 channel rows in its block
+  float bv[16];
+#pragma unroll
+  for (int v4 = 0; v4 < 16; v4 += 4) {
+    float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + cb * 32 + F::row(lane, v4));
+    bv[v4] = b4.x;
+    bv[v4 + 1] = b4.y;
+    bv[v4 + 2] = b4.z;
+    bv[v4 + 3] = b4.w;
+  }
+
+  // patch pieces of this thread: e = tid + 256 i -> pixel e / CQ = (row py, column px) of
+  // the (2TH+1) x 33 patch, piece e % CQ; packed as py << 8 | px (0xffff: none)
+  const int q8 = (tid % CQ) * 8;
+  int pyx[P_IT];
+#pragma unroll
+  for (int i = 0; i < P_IT; ++i) {
+    const int pp = (tid + i * 256) / CQ, py = pp / 33;
+    pyx[i] = pp < PR * 33 ? (py << 8) | (pp - py * 33) : 0xffff;
+  }
+  // channels >= Cin of a ragged pixel are zeroed bitwise (their bits never reach the MFMAs)
+  u16x8 keep;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) keep[k] = q8 + k < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+  const bool ragged = p.Cin < CK;
+
+  auto origin = [&](int t, int & b, int & oy0, int & ox0) __attribute__((always_inline)) {
+    b = t / tiles_img;
+    const int tr = t - b * tiles_img, ty = tr / tiles_x;
+    oy0 = ty * TH;
+    ox0 = (tr - ty * tiles_x) * TW;
+  };
+  const int xrow = p.W * p.x.cs;
+  auto load_patch = [&](int t, h8 (&rp)[P_IT]) __attribute__((always_inline)) {
+    int b, oy0, ox0;
+    origin(t, b, oy0, ox0);
+    const int iy0 = 2 * oy0 - 1, ix0 = 2 * ox0 - 1;
+    const int base = b * (int)p.x.img + iy0 * xrow + ix0 * p.x.cs + q8;
+#pragma unroll
+    for (int i = 0; i < P_IT; ++i) {
+      const int py = pyx[i] >> 8, px = pyx[i] & 0xff;
+      const bool ok = pyx[i] != 0xffff && (unsigned)(iy0 + py) < (unsigned)p.H && (unsigned)(ix0 + px) < (unsigned)p.W;
+      const int off = base + py * xrow + px * p.x.cs;
+      rp[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (unsigned)off * 2u : kBufOOB, 0, 0));
+    }
+  };
+  auto store_patch = [&](const h8 (&rp)[P_IT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < P_IT; ++i)
+      if (pyx[i] != 0xffff) {
+        const int py = pyx[i] >> 8, px = pyx[i] & 0xff;
+        h8 v = rp[i];
+        if (ragged) v = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, v) & keep);
+        *reinterpret_cast<h8 *>(Ps + py * L::RH + ((px & 1) ? L::ODD : 0) + (px >> 1) * L::CKP + q8) = v;
+      }
+  };
+
+  // fragments: B = pixel (lane & 31) of block pb = output row 2 pb + (lane & 31) / 16, column
+  // (lane & 15); A = weight row cb * 32 + (lane & 31)
+  const int kq = F::kq(lane);
+  const int bl = (2 * (2 * pb + ((lane >> 4) & 1))) * L::RH + (lane & 15) * L::CKP + kq;
+  const int al = (cb * 32 + (lane & 31)) * L::LDW + kq;
+
+  h8 rp[P_IT];
+  load_patch(t_lo, rp);
+  __syncthreads();  // weights in LDS
+  store_patch(rp);
+  load_patch(t_lo + (ntl > 1 ? 1 : 0), rp);
+  __syncthreads();  // first patch in LDS
+
+  // fragments of K slice sl (tap sl / (CK / 16), channels 16 (sl % (CK / 16)) ..)
+  auto frag = [&](int sl, h8 & fa, h8 & fb) __attribute__((always_inline)) {
+    const int tap = sl / (CK / 16), j = sl % (CK / 16);
+    const int dy = tap / 3, dx = tap % 3;
+    const int boff = dy * L::RH + (dx == 1 ? L::ODD : (dx == 2 ? L::CKP : 0)) + 16 * j;
+    fa = *reinterpret_cast<const h8 *>(Ws + al + tap * CK + 16 * j);
+    fb = *reinterpret_cast<const h8 *>(Ps + bl + boff);
+  };
+  constexpr int D = CK == 16 ? 2 : 4;  // K slices whose fragments are in flight
+
+  for (int i = 0; i < ntl; ++i) {
+    // two accumulators (even and odd K slices): independent MFMA chains, summed at the end
+    acc_t acc[2];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][v] = acc[1][v] = 0.0f;
+    h8 fa[D], fb[D];
+#pragma unroll
+    for (int sl = 0; sl < D && sl < NSL; ++sl) frag(sl, fa[sl], fb[sl]);
+#pragma unroll
+    for (int sl = 0; sl < NSL; ++sl) {
+      const h8 a0 = fa[sl % D], b0 = fb[sl % D];
+      if (sl + D < NSL) frag(sl + D, fa[sl % D], fb[sl % D]);
+      acc[sl & 1] = F::mma(a0, b0, acc[sl & 1]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads D slices ahead of their MFMAs
+    }
+    acc_t acc_s;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc_s[v] = acc[0][v] + acc[1][v];
+    __syncthreads();  // every wave is done with the patch
+    if (i + 1 < ntl) {
+      store_patch(rp);  // tile i + 1
+      load_patch(t_lo + (i + 2 < ntl ? i + 2 : i + 1), rp);
+    }
+    // epilogue of tile i: output pixel of the lane, 8-channel stores after the swap
+    {
+      int b, oy0, ox0;
+      origin(t_lo + i, b, oy0, ox0);
+      const int oy = oy0 + 2 * pb + ((lane >> 4) & 1), ox = ox0 + (lane & 15);
+      const bool ok = oy < p.Ho && ox < p.Wo;
+      const unsigned yo = ok ? ((unsigned)b * (unsigned)p.y.img + (unsigned)(oy * p.Wo + ox) * (unsigned)p.y.cs) * 2u : kBufOOB;
+      auto vals = [&](int v4) __attribute__((always_inline)) {
+        float o4[4] = {act_fast<ACT>(acc_s[v4] + bv[v4]), act_fast<ACT>(acc_s[v4 + 1] + bv[v4 + 1]),
+                       act_fast<ACT>(acc_s[v4 + 2] + bv[v4 + 2]), act_fast<ACT>(acc_s[v4 + 3] + bv[v4 + 3])};
+        h4 hv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          __asm__("" : "+v"(o4[q]));  // fp32 result, then one fp16 rounding
+          hv[q] = (_Float16)o4[q];
+        }
+        return hv;
+      };
+#pragma unroll
+      for (int v4 = 0; v4 < 16; v4 += 8) {
+        // runs v4 (channels c..c+3 / c+4..c+7 on lanes < 32 / >= 32) and v4 + 4 (c+8..c+11 /
+        // c+12..c+15): swapped so every lane holds 8 consecutive channels
+        const u2q lo = __builtin_bit_cast(u2q, vals(v4));
+        const u2q hi = __builtin_bit_cast(u2q, vals(v4 + 4));
+        const auto s0 = __builtin_amdgcn_permlane32_swap(lo[0], hi[0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(lo[1], hi[1], false, false);
+        const u4q q = {s0[0], s1[0], s0[1], s1[1]};
+        const int c = cb * 32 + F::row(lane, v4) - 4 * (lane >> 5) + 8 * (lane >> 5);
+        if (c < p.Cout)
+          __builtin_amdgcn_raw_buffer_store_b128(q, yr, yo == kBufOOB ? kBufOOB : yo + (unsigned)c * 2u, 0, 0);
+      }
+    }
+    __syncthreads();  // patch of tile i + 1 in LDS
+  }
+}
+
 // ---------------------------------------------------------------- host side
 
 namespace {
@@ -186,11 +415,65 @@ long s2_grid(const ConvParams & p)
   return (long)p.batch * ((p.Ho + p.th - 1) / p.th) * ((p.Wo + p.tw - 1) / p.tw);
 }
 
+// ---------------------------------------------------------------- persistent kernel, host side
+
+namespace {
+constexpr int kS2PkCUs = 256;
+}  // namespace
+
+int s2pk_ck(int cfg) { return cfg == 2 || cfg == 3 ? 16 : 32; }
+int s2pk_cb(int cfg) { return cfg == 2 || cfg == 4 ? 1 : 2; }
+
+bool s2pk_views_ok(const ConvParams & p)
+{
+  const View & y = p.y;
+  if (y.layout != kNHWC || (y.cs % 8) || (y.img % 8) || (reinterpret_cast<uintptr_t>(y.ptr) % 16)) return false;
+  if (p.Cout % 8 && p.ypad < 8 - p.Cout % 8) return false;
+  const long ylast = (long)(p.batch - 1) * y.img + ((long)p.Ho * p.Wo - 1) * y.cs + (p.Cout + 7) / 8 * 8;
+  const long xlast = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  return !p.r.ptr && ylast * 2 < (1L << 31) && xlast * 2 < (1L << 31) && (long)p.W * p.x.cs < (1L << 23) &&
+         p.W < 65536 && p.H < 65536;
+}
+
+long s2pk_tiles(const ConvParams & p)
+{
+  const int cb = s2pk_cb(p.s2 - 1), th = 8 / cb;
+  return (long)p.batch * ((p.Ho + th - 1) / th) * ((p.Wo + 15) / 16);
+}
+
+template <int CK, int CB>
+static void launch_s2pk_act(const ConvParams & p, hipStream_t s)
+{
+  // work-groups per CU: 4 with 16 channels (38 KB of LDS, <= 128 VGPRs), 2 with 32 (64 KB)
+  const long per_cu = CK == 16 ? 4 : 2;
+  const dim3 grid((unsigned)std::min<long>(s2pk_tiles(p), per_cu * kS2PkCUs)), block(256);
+  switch (p.act) {
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActSiLU>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActReLU>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActHSwish>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActNone>), grid, block, 0, s, p); break;
+  }
+}
+
+static void launch_conv_s2pk(const ConvParams & p, hipStream_t s)
+{
+  switch (p.s2 - 1) {
+  case 2: launch_s2pk_act<16, 1>(p, s); break;
+  case 3: launch_s2pk_act<16, 2>(p, s); break;
+  case 4: launch_s2pk_act<32, 1>(p, s); break;
+  default: launch_s2pk_act<32, 2>(p, s); break;
+  }
+}
+
 void launch_conv_s2(const ConvParams & p, hipStream_t s)
 {
   const int bc = conv_batch_chunk(p);
   if (bc < p.batch) {
     for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_s2(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
+    return;
+  }
+  if (p.s2 > 2) {
+    launch_conv_s2pk(p, s);
     return;
   }
   const dim3 grid((unsigned)s2_grid(p));

@@ -1884,8 +1884,9 @@ void Model::validate(const Launch & l) const
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
-    // the resident-weight kernel writes 4-channel groups into the view's padding channels
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
+    // the resident-weight, pipelined and persistent stride-2 kernels write 4- or 8-channel
+    // groups into the view's padding channels
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.s2 > 2 ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
           "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
@@ -1937,7 +1938,15 @@ void Model::validate(const Launch & l) const
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 14)) throw std::runtime_error("pipelined conv geometry too large");
         check(p.w, 0, (long)(p.Cout + 127) / 128 * 128 * p.kpad - 1, 2, "pipelined conv w");
       }
-      if (p.s2) {
+      if (p.s2 > 2) {
+        const int cfg = p.s2 - 1, ck = s2pk_ck(cfg), cb = s2pk_cb(cfg);
+        if (cfg > 5 || p.halo || p.res || p.pipe || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
+            p.cin8 != ck || p.Cin > ck || p.Cout > 32 * cb || p.th != 8 / cb || p.tw != 16 || p.kpad < 9 * ck ||
+            p.Ho != (p.H - 1) / 2 + 1 || p.Wo != (p.W - 1) / 2 + 1 || !s2pk_views_ok(p) ||
+            (p.act != kActNone && p.act != kActSiLU && p.act != kActReLU && p.act != kActHSwish))
+          throw std::runtime_error("persistent stride-2 geometry");
+        check(p.w, 0, (long)32 * cb * p.kpad - 1, 2, "persistent stride-2 w");
+      } else if (p.s2) {
         const int cfg = p.s2 - 1;
         if (cfg < 0 || cfg > 1 || p.halo || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
             p.cin8 != s2_cfg_ck(cfg) || p.Cout > s2_cfg_bn(cfg) || p.th < 1 || p.tw < 1 ||
@@ -2338,7 +2347,7 @@ std::string Model::nodeKernel(int i)
   const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
   case Launch::kIgemm:
-    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? "conv_s2" : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
+    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.s2 ? (l.cp.s2 > 2 ? "conv_s2p" : "conv_s2") : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";

@@ -71,7 +71,14 @@ long pair_tiles(int H, int W, int batch, int th, int tw);
 // weights / bias / act of conv 2, th x tw); both weights in the 32-channel halo packing
 void launch_conv_pair(const ConvParams & a, const ConvParams & b, hipStream_t s);
 
-// conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64
+// conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64 (configs 0, 1: one
+// tile per work-group), and the persistent resident-weight kernel (configs 2-5: 16 or 32
+// input channels, Cout <= 32 or <= 64)
+int s2pk_ck(int cfg);                       // input-channel chunk of a persistent config
+int s2pk_cb(int cfg);                       // 32-channel output blocks of a persistent config
+bool s2pk_views_ok(const ConvParams & p);   // output NHWC 16-byte stores, no residual, 32-bit offsets
+long s2pk_tiles(const ConvParams & p);      // output tiles (p.s2 set)
+constexpr long kS2PkMinTiles = 512;
 bool s2_plan(int cin, int cout, int Ho, int Wo, int * cfg, int * th, int * tw);
 int s2_patch(int th, int tw);  // patch pixels of a th x tw output tile
 int s2_cfg_bm(int cfg);

@@ -78,7 +78,7 @@ def test_conv1x1_config(tmp_path):
 
 
 SWEEP_KERNEL = {"stem": ("conv_stem",), "dw": ("dwconv",),
-                "conv3x3s2": ("conv_igemm", "conv_igemm_sk", "conv_s2"),
+                "conv3x3s2": ("conv_igemm", "conv_igemm_sk", "conv_s2", "conv_s2p"),
                 "conv3x3s1": ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res", "conv_pipe")}
 
 
@@ -272,6 +272,42 @@ def test_conv3x3_s2(tmp_path, cin, cout, H, W, batch):
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=2, act=pw.ACT_SILU, pre_relu=True)
     assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_SPLITK) == "conv_s2"
     _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=ia.IVH_FLAG_NO_SPLITK)
+
+
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (32, 64, 160, 160, 8, pw.ACT_SILU),    # the YOLOv8 32->64 downsample at 160x160
+    (16, 32, 320, 320, 3, pw.ACT_SILU),    # the YOLOv8 16->32 downsample at 320x320
+    (28, 40, 97, 131, 8, pw.ACT_RELU),     # Cin 28 (ragged 32-channel chunk), odd map: ragged tiles
+    (12, 24, 130, 70, 20, pw.ACT_HSWISH),  # Cin 12 (ragged 16-channel chunk), 8 x 16 tiles
+    (32, 32, 64, 96, 48, pw.ACT_SILU),     # 32 -> 32 (one 32-channel block)
+])
+def test_conv3x3_s2_persistent(tmp_path, cin, cout, H, W, batch, act):
+    """3x3 stride-2 convs through the persistent resident-weight kernel of conv_s2.hip vs the
+    oracle and vs the same conv with that kernel switched off."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=2, act=act, pre_relu=True, post_relu=True)
+    print(f"persistent s2 conv {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    assert _conv_kernel(path, batch) == "conv_s2p"
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_S2_PERSIST) != "conv_s2p"
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_S2_PERSIST)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def test_conv3x3_s2_persistent_no_act(tmp_path):
+    """The persistent stride-2 kernel without an activation (its output read by a 1x1 conv,
+    so no later activation folds into it), at batch 40 (960 tiles of 4 x 16)."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, 32, 64, 96]), pw.UN_RELU)
+        t = pb.conv(x, 64, 3, s=2, act=pw.ACT_NONE)
+        return pb.conv(t, 32, 1)
+    path = _small_plan(tmp_path, build)
+    kinds = _kernels(path, 40)
+    assert kinds.count("conv_s2p") == 1
+    got = _check_f32(path, 40, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, 40, lo=-1.0, flags=ia.IVH_FLAG_NO_S2_PERSIST)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
 def test_halo_residual_chain(tmp_path):

@@ -52,8 +52,9 @@ def test_dry_run_plans_and_bounds(plans, name):
 
 
 def test_kernel_choice_yolov8(plans):
-    """Planner choices at batch 64: the stem kernel for the Cin = 3 conv, the stride-2
-    LDS-patch kernel for the 16->32 downsample, the implicit GEMM for the 32->64 one, the
+    """Planner choices at batch 64: the stem kernel for the Cin = 3 conv, the persistent
+    stride-2 kernel for the 16->32 and 32->64 downsamples, the implicit GEMM for the wider
+    ones (64->128 and up), the
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
     Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
     40x40 maps (enough items for its persistent grid), the fused pair kernel for the three
@@ -64,8 +65,9 @@ def test_kernel_choice_yolov8(plans):
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
     by = {i["desc"]: i["kernel"] for i in info}
     assert by["conv3x3 3x640x640->16x320x320 k3 s2 g1 act1"] == "conv_stem"
-    assert by["conv3x3 16x320x320->32x160x160 k3 s2 g1 act1"] == "conv_s2"
-    assert by["conv3x3 32x160x160->64x80x80 k3 s2 g1 act1"] == "conv_igemm"
+    assert by["conv3x3 16x320x320->32x160x160 k3 s2 g1 act1"] == "conv_s2p"
+    assert by["conv3x3 32x160x160->64x80x80 k3 s2 g1 act1"] == "conv_s2p"
+    assert by["conv3x3 64x80x80->128x40x40 k3 s2 g1 act1"] == "conv_igemm"
     s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), int(i["desc"].split()[1].split("x")[1]),
            "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
 
@@ -85,7 +87,7 @@ def test_kernel_choice_yolov8(plans):
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
 def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     """Each conv sweep layer at batch 64, as it runs inside a model, gets its kernel family."""
-    want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2", "conv3x3s2": "conv_igemm",
+    want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2p", "conv3x3s2_32": "conv_s2p", "conv3x3s2": "conv_igemm",
             "conv3x3s1_64": "conv_res", "conv3x3s1_128": "conv_pipe", "conv3x3s1": "conv_halo", "dw": "dwconv"}
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act,
                              pre_relu=not name.startswith("stem"), post_relu=True)
