@@ -398,7 +398,9 @@ ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb)
 std::string igemm_launch_tag(const ConvParams & p)
 {
   char b[160];
-  if (p.pipe)
+  if (p.pw)
+    snprintf(b, sizeof b, "blocks=%ld lds=%zu", pw_blocks(p), pw_lds_bytes(p));
+  else if (p.pipe)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d items=%ld", p.pipe - 1, p.th, p.tw, pipe_items(p));
   else if (p.res)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d ck=%d store=%d", p.res - 1, p.th, p.tw, p.ck, res_store_width(p));
@@ -419,6 +421,10 @@ void launch_conv_igemm(const ConvParams & p, hipStream_t s)
   const int bc = conv_batch_chunk(p);
   if (bc < p.batch) {
     for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_igemm(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);
+    return;
+  }
+  if (p.pw) {
+    launch_conv_pw(p, s);
     return;
   }
   if (p.pipe) {

@@ -88,6 +88,9 @@ struct ConvParams {
   // 3x3 stride-2 small-channel kernel (conv_s2.hip): config + 1 (0: not used); th x tw is
   // then the output tile of one image and w the implicit-GEMM packing
   int s2 = 0;
+  // 1x1 stride-1 streaming kernel (conv_pw.hip, Cout <= 64, channels-last views): 1 when
+  // used; w is then the implicit-GEMM packing
+  int pw = 0;
   // implicit GEMM of a 1x1 conv reading NCHW channel planes (x.cs = pixels per plane, a
   // multiple of 8): each thread loads 8 consecutive pixels of one channel and writes them
   // transposed into the tile's pixel rows in LDS (0: channels-last input)

@@ -71,6 +71,14 @@ long pair_tiles(int H, int W, int batch, int th, int tw);
 // weights / bias / act of conv 2, th x tw); both weights in the 32-channel halo packing
 void launch_conv_pair(const ConvParams & a, const ConvParams & b, hipStream_t s);
 
+// conv_pw.hip: 1x1 stride-1 convs with Cout <= 64 on channels-last views (streaming)
+bool pw_views_ok(const ConvParams & p);
+bool pw_plan(const ConvParams & p);         // eligible (shape, activation, views, LDS)
+long pw_blocks(const ConvParams & p);       // 32-pixel blocks of the batch
+size_t pw_lds_bytes(const ConvParams & p);  // weights and bias in LDS
+constexpr long kPwMinBlocks = 1024;
+void launch_conv_pw(const ConvParams & p, hipStream_t s);
+
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64 (configs 0, 1: one
 // tile per work-group), and the persistent resident-weight kernel (configs 2-5: 16 or 32
 // input channels, Cout <= 32 or <= 64)

@@ -1738,7 +1738,6 @@ __device__ __forceinline__ void decode_anchor(const DecodeParams & p, int b, int
   if (nk > 0) {
     const float ck = hv(p.ckpt, 0), mx = hv(p.ancm, a), my = hv(p.ancm, (long)p.A + a);
     _Float16 * yk = y + (4 + nc) * ys;
-#pragma unroll
     for (int k = 0; k < nk; ++k) {
       yk[(3 * k) * ys] = (_Float16)(rh(rh(fk(3 * k) * ck) + mx) * st);
       yk[(3 * k + 1) * ys] = (_Float16)(rh(rh(fk(3 * k + 1) * ck) + my) * st);

@@ -310,6 +310,32 @@ def test_conv3x3_s2_persistent_no_act(tmp_path):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (32, 32, 160, 160, 2, pw.ACT_SILU),    # the YOLOv8 C2f 1x1 at 160x160
+    (96, 64, 80, 80, 6, pw.ACT_SILU),      # 96 -> 64: two 64-channel K chunks (one half empty), two 32-channel blocks
+    (48, 40, 97, 61, 8, pw.ACT_HSWISH),    # K 48 (a partly empty chunk), Cout 40, odd pixel count
+    (512, 24, 20, 30, 64, pw.ACT_RELU),    # K 512 (eight chunks), Cout 24 (ragged 32-channel block)
+    (64, 56, 80, 80, 6, pw.ACT_SILU),      # Cout 56 (ragged second 32-channel block)
+    (64, 64, 40, 40, 24, pw.ACT_NONE),     # no activation
+])
+def test_conv1x1_streaming(tmp_path, cin, cout, H, W, batch, act):
+    """1x1 convs through the streaming pointwise kernel of conv_pw.hip vs the oracle and vs
+    the implicit GEMM."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, cin, H, W]), pw.UN_RELU)
+        t = pb.conv(x, cout, 1, act=act)
+        return pb.conv(t, 16, 1)  # read channels-last, so no activation folds into the first
+    path = _small_plan(tmp_path, build)
+    print(f"streaming 1x1 {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    kinds = _kernels(path, batch)
+    assert kinds.count("conv_pw") >= 1, kinds
+    assert "conv_pw" not in _kernels(path, batch, ia.IVH_FLAG_NO_PW)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PW)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
 def test_halo_residual_chain(tmp_path):
     """Bottleneck chain (3x3, 3x3 + residual) on 48x48: halo kernel with the fused residual."""
     def build(pb):
