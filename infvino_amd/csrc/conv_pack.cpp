@@ -267,19 +267,20 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
       }
     }
   }
-  // 3x3 stride 2 with 16 or 32 (padded) input channels, Cout <= 64, no residual: the
-  // persistent resident-weight kernel of conv_s2.hip on the implicit-GEMM packing, when its
-  // tiles fill the persistent grid several times over.
+  // 3x3 stride 2 with 16 or 32 (padded) input channels and Cout <= 64, or 64 input channels
+  // and Cout <= 128 (64-channel blocks on the grid's y), no residual: the persistent
+  // resident-weight kernel of conv_s2.hip on the implicit-GEMM packing, when its tiles fill
+  // the persistent grid several times over.
   const bool act_ok = p.act == kActNone || p.act == kActSiLU || p.act == kActReLU || p.act == kActHSwish;
   if (!p.halo && p.K == 3 && p.S == 2 && p.P == 1 && !(s.flags & IVH_FLAG_NO_S2_PERSIST) && act_ok &&
-      (pk.cin8 == 16 || pk.cin8 == 32) && p.Cout <= 64 && pk.kpad >= 9 * pk.cin8 &&
-      p.Ho == (p.H - 1) / 2 + 1 && p.Wo == (p.W - 1) / 2 + 1 && s2pk_views_ok(p)) {
-    const int cfg = (pk.cin8 == 16 ? 2 : 4) + (p.Cout > 32 ? 1 : 0);
+      (((pk.cin8 == 16 || pk.cin8 == 32) && p.Cout <= 64) || (pk.cin8 == 64 && p.Cout <= 128)) &&
+      pk.kpad >= 9 * pk.cin8 && p.Ho == (p.H - 1) / 2 + 1 && p.Wo == (p.W - 1) / 2 + 1 && s2pk_views_ok(p)) {
+    const int cfg = pk.cin8 == 64 ? 6 : (pk.cin8 == 16 ? 2 : 4) + (p.Cout > 32 ? 1 : 0);
     ConvParams q = p;
     q.s2 = cfg + 1;
     if (s2pk_tiles(q) >= kS2PkMinTiles) {
       p.s2 = cfg + 1;
-      p.th = 8 / s2pk_cb(cfg);
+      p.th = s2pk_th(cfg);
       p.tw = 16;
       p.ksplit = 1;
       p.ws = nullptr;

@@ -177,27 +177,28 @@ template <int CK> struct S2P {
 };
 }  // namespace
 
-template <int CK, int CB, int ACT>
-__global__ void __launch_bounds__(256, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(const ConvParams p)
+template <int CK, int CB, int PB, int ACT>
+__global__ void __launch_bounds__(64 * PB * CB, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(const ConvParams p)
 {
   using F = Mf<32>;
   using L = S2P<CK>;
   typedef F::acc_t acc_t;
-  constexpr int PB = 4 / CB;            // pixel blocks per tile
+  constexpr int NT = 64 * PB * CB;      // threads: a wave per (pixel block, channel block)
   constexpr int TH = 2 * PB, TW = 16;   // output tile
   constexpr int PR = 2 * TH + 1;        // patch rows
   constexpr int CQ = CK / 8;            // 16-byte pieces per pixel
   constexpr int NPC = PR * 33 * CQ;     // patch pieces
-  constexpr int P_IT = (NPC + 255) / 256;
+  constexpr int P_IT = (NPC + NT - 1) / NT;
   constexpr int BN = 32 * CB;
   constexpr int WQ = 9 * CK / 8;        // 16-byte pieces per weight row
-  constexpr int W_IT = (BN * WQ + 255) / 256;
+  constexpr int W_IT = (BN * WQ + NT - 1) / NT;
   constexpr int NSL = 9 * CK / 16;      // K slices
   __shared__ __attribute__((aligned(16))) _Float16 Ws[BN * L::LDW];
   __shared__ __attribute__((aligned(16))) _Float16 Ps[PR * L::RH];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pb = wave % PB, cb = wave / PB;
+  const int co0 = blockIdx.y * BN;  // this work-group's output channels co0 .. co0 + BN - 1
   const int tiles_x = (p.Wo + TW - 1) / TW, tiles_y = (p.Ho + TH - 1) / TH;
   const int tiles_img = tiles_x * tiles_y, ntiles = p.batch * tiles_img;
   const int G = gridDim.x, r = xcd_tile(blockIdx.x, G);
@@ -214,17 +215,17 @@ __global__ void __launch_bounds__(256, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(con
   // weights [BN][9 CK] (implicit-GEMM packing, k = tap * CK + ci), once per launch
   {
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<__half *>(p.w), (short)0, BN * p.kpad * 2, kBufDword3);
+        const_cast<__half *>(p.w + (long)co0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
     h8 rw[W_IT];
 #pragma unroll
     for (int i = 0; i < W_IT; ++i) {
-      const int e = tid + i * 256, row = e / WQ;
+      const int e = tid + i * NT, row = e / WQ;
       rw[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
           wr, row < BN ? (unsigned)((row * p.kpad + (e - row * WQ) * 8) * 2) : kBufOOB, 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < W_IT; ++i) {
-      const int e = tid + i * 256, row = e / WQ;
+      const int e = tid + i * NT, row = e / WQ;
       if (row < BN) *reinterpret_cast<h8 *>(Ws + row * L::LDW + (e - row * WQ) * 8) = rw[i];
     }
   }
@@ -233,20 +234,20 @@ __global__ void __launch_bounds__(256, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(con
 #pragma unroll
   for (int v4 = 0; v4 < 16; v4 += 4) {
     float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + cb * 32 + F::row(lane, v4));
+    if (p.bias) b4 = *reinterpret_cast<const float4 *>(p.bias + co0 + cb * 32 + F::row(lane, v4));
     bv[v4] = b4.x;
     bv[v4 + 1] = b4.y;
     bv[v4 + 2] = b4.z;
     bv[v4 + 3] = b4.w;
   }
 
-  // patch pieces of this thread: e = tid + 256 i -> pixel e / CQ = (row py, column px) of
+  // patch pieces of this thread: e = tid + NT i -> pixel e / CQ = (row py, column px) of
   // the (2TH+1) x 33 patch, piece e % CQ; packed as py << 8 | px (0xffff: none)
   const int q8 = (tid % CQ) * 8;
   int pyx[P_IT];
 #pragma unroll
   for (int i = 0; i < P_IT; ++i) {
-    const int pp = (tid + i * 256) / CQ, py = pp / 33;
+    const int pp = (tid + i * NT) / CQ, py = pp / 33;
     pyx[i] = pp < PR * 33 ? (py << 8) | (pp - py * 33) : 0xffff;
   }
   // channels >= Cin of a ragged pixel are zeroed bitwise (their bits never reach the MFMAs)
@@ -359,7 +360,7 @@ __global__ void __launch_bounds__(256, CK == 16 ? 4 : 2) conv3x3s2_pk_kernel(con
         const auto s0 = __builtin_amdgcn_permlane32_swap(lo[0], hi[0], false, false);
         const auto s1 = __builtin_amdgcn_permlane32_swap(lo[1], hi[1], false, false);
         const u4q q = {s0[0], s1[0], s0[1], s1[1]};
-        const int c = cb * 32 + F::row(lane, v4) - 4 * (lane >> 5) + 8 * (lane >> 5);
+        const int c = co0 + cb * 32 + F::row(lane, v4) - 4 * (lane >> 5) + 8 * (lane >> 5);
         if (c < p.Cout)
           __builtin_amdgcn_raw_buffer_store_b128(q, yr, yo == kBufOOB ? kBufOOB : yo + (unsigned)c * 2u, 0, 0);
       }
@@ -421,8 +422,13 @@ namespace {
 constexpr int kS2PkCUs = 256;
 }  // namespace
 
-int s2pk_ck(int cfg) { return cfg == 2 || cfg == 3 ? 16 : 32; }
+// persistent configs: 2: 16 channels in, one 32-channel block, 8 x 16 tiles; 3: 16 in, two
+// blocks, 4 x 16; 4, 5: the same with 32 channels in; 6: 64 channels in, two blocks, 8 x 16
+// tiles, eight waves (Cout beyond 64 in further 64-channel blocks on grid.y)
+int s2pk_ck(int cfg) { return cfg == 2 || cfg == 3 ? 16 : (cfg == 6 ? 64 : 32); }
 int s2pk_cb(int cfg) { return cfg == 2 || cfg == 4 ? 1 : 2; }
+int s2pk_pb(int cfg) { return cfg == 6 ? 4 : 4 / s2pk_cb(cfg); }
+int s2pk_th(int cfg) { return 2 * s2pk_pb(cfg); }
 
 bool s2pk_views_ok(const ConvParams & p)
 {
@@ -437,31 +443,35 @@ bool s2pk_views_ok(const ConvParams & p)
 
 long s2pk_tiles(const ConvParams & p)
 {
-  const int cb = s2pk_cb(p.s2 - 1), th = 8 / cb;
+  const int th = s2pk_th(p.s2 - 1);
   return (long)p.batch * ((p.Ho + th - 1) / th) * ((p.Wo + 15) / 16);
 }
 
-template <int CK, int CB>
+template <int CK, int CB, int PB>
 static void launch_s2pk_act(const ConvParams & p, hipStream_t s)
 {
-  // work-groups per CU: 4 with 16 channels (38 KB of LDS, <= 128 VGPRs), 2 with 32 (64 KB)
-  const long per_cu = CK == 16 ? 4 : 2;
-  const dim3 grid((unsigned)std::min<long>(s2pk_tiles(p), per_cu * kS2PkCUs)), block(256);
+  // work-groups per CU: 4 with 16 channels (38 KB of LDS, <= 128 VGPRs), 2 with 32 (64 KB),
+  // 1 with 64 (157 KB); output-channel blocks on grid.y share the CUs
+  const long per_cu = CK == 16 ? 4 : (CK == 32 ? 2 : 1);
+  const int ncb = (p.Cout + 32 * CB - 1) / (32 * CB);
+  const long gx = std::min<long>(s2pk_tiles(p), std::max<long>(1, per_cu * kS2PkCUs / ncb));
+  const dim3 grid((unsigned)gx, (unsigned)ncb), block(64 * PB * CB);
   switch (p.act) {
-  case kActSiLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActSiLU>), grid, block, 0, s, p); break;
-  case kActReLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActReLU>), grid, block, 0, s, p); break;
-  case kActHSwish: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActHSwish>), grid, block, 0, s, p); break;
-  default: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, kActNone>), grid, block, 0, s, p); break;
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, PB, kActSiLU>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, PB, kActReLU>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, PB, kActHSwish>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s2_pk_kernel<CK, CB, PB, kActNone>), grid, block, 0, s, p); break;
   }
 }
 
 static void launch_conv_s2pk(const ConvParams & p, hipStream_t s)
 {
   switch (p.s2 - 1) {
-  case 2: launch_s2pk_act<16, 1>(p, s); break;
-  case 3: launch_s2pk_act<16, 2>(p, s); break;
-  case 4: launch_s2pk_act<32, 1>(p, s); break;
-  default: launch_s2pk_act<32, 2>(p, s); break;
+  case 2: launch_s2pk_act<16, 1, 4>(p, s); break;
+  case 3: launch_s2pk_act<16, 2, 2>(p, s); break;
+  case 4: launch_s2pk_act<32, 1, 4>(p, s); break;
+  case 5: launch_s2pk_act<32, 2, 2>(p, s); break;
+  default: launch_s2pk_act<64, 2, 4>(p, s); break;
   }
 }
 

@@ -1947,12 +1947,13 @@ void Model::validate(const Launch & l) const
       }
       if (p.s2 > 2) {
         const int cfg = p.s2 - 1, ck = s2pk_ck(cfg), cb = s2pk_cb(cfg);
-        if (cfg > 5 || p.halo || p.res || p.pipe || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
-            p.cin8 != ck || p.Cin > ck || p.Cout > 32 * cb || p.th != 8 / cb || p.tw != 16 || p.kpad < 9 * ck ||
+        if (cfg > 6 || p.halo || p.res || p.pipe || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||
+            p.cin8 != ck || p.Cin > ck || p.Cout > (cfg == 6 ? 128 : 32 * cb) || p.th != s2pk_th(cfg) ||
+            p.tw != 16 || p.kpad < 9 * ck ||
             p.Ho != (p.H - 1) / 2 + 1 || p.Wo != (p.W - 1) / 2 + 1 || !s2pk_views_ok(p) ||
             (p.act != kActNone && p.act != kActSiLU && p.act != kActReLU && p.act != kActHSwish))
           throw std::runtime_error("persistent stride-2 geometry");
-        check(p.w, 0, (long)32 * cb * p.kpad - 1, 2, "persistent stride-2 w");
+        check(p.w, 0, (long)(p.Cout + 32 * cb - 1) / (32 * cb) * 32 * cb * p.kpad - 1, 2, "persistent stride-2 w");
       } else if (p.s2) {
         const int cfg = p.s2 - 1;
         if (cfg < 0 || cfg > 1 || p.halo || p.K != 3 || p.S != 2 || p.P != 1 || p.ksplit != 1 ||

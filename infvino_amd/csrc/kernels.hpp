@@ -81,9 +81,10 @@ void launch_conv_pw(const ConvParams & p, hipStream_t s);
 
 // conv_s2.hip: 3x3 stride-2 pad-1 convs with 8 < Cin <= 16, Cout <= 64 (configs 0, 1: one
 // tile per work-group), and the persistent resident-weight kernel (configs 2-5: 16 or 32
-// input channels, Cout <= 32 or <= 64)
+// input channels, Cout <= 32 or <= 64; config 6: 64 input channels, Cout <= 128)
 int s2pk_ck(int cfg);                       // input-channel chunk of a persistent config
 int s2pk_cb(int cfg);                       // 32-channel output blocks of a persistent config
+int s2pk_th(int cfg);                       // output tile rows of a persistent config (16 columns)
 bool s2pk_views_ok(const ConvParams & p);   // output NHWC 16-byte stores, no residual, 32-bit offsets
 long s2pk_tiles(const ConvParams & p);      // output tiles (p.s2 set)
 constexpr long kS2PkMinTiles = 512;

@@ -280,6 +280,9 @@ def test_conv3x3_s2(tmp_path, cin, cout, H, W, batch):
     (28, 40, 97, 131, 8, pw.ACT_RELU),     # Cin 28 (ragged 32-channel chunk), odd map: ragged tiles
     (12, 24, 130, 70, 20, pw.ACT_HSWISH),  # Cin 12 (ragged 16-channel chunk), 8 x 16 tiles
     (32, 32, 64, 96, 48, pw.ACT_SILU),     # 32 -> 32 (one 32-channel block)
+    (64, 128, 80, 80, 36, pw.ACT_SILU),    # the YOLOv8 64->128 downsample: 64 channels in, two 64-channel blocks
+    (64, 64, 80, 80, 36, pw.ACT_RELU),     # the neck's 64->64 downsample
+    (60, 96, 66, 90, 40, pw.ACT_HSWISH),   # Cin 60 (ragged 64-channel chunk), Cout 96 (half-empty second block)
 ])
 def test_conv3x3_s2_persistent(tmp_path, cin, cout, H, W, batch, act):
     """3x3 stride-2 convs through the persistent resident-weight kernel of conv_s2.hip vs the
