@@ -53,8 +53,8 @@ def test_dry_run_plans_and_bounds(plans, name):
 
 def test_kernel_choice_yolov8(plans):
     """Planner choices at batch 64: the stem kernel for the Cin = 3 conv, the persistent
-    stride-2 kernel for the 16->32 and 32->64 downsamples, the implicit GEMM for the wider
-    ones (64->128 and up), the
+    stride-2 kernel for the 16->32, 32->64 and 64->128 downsamples, the implicit GEMM for the
+    wider ones (128->256), the
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
     Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
     40x40 maps (enough items for its persistent grid), the fused pair kernel for the three
@@ -67,7 +67,8 @@ def test_kernel_choice_yolov8(plans):
     assert by["conv3x3 3x640x640->16x320x320 k3 s2 g1 act1"] == "conv_stem"
     assert by["conv3x3 16x320x320->32x160x160 k3 s2 g1 act1"] == "conv_s2p"
     assert by["conv3x3 32x160x160->64x80x80 k3 s2 g1 act1"] == "conv_s2p"
-    assert by["conv3x3 64x80x80->128x40x40 k3 s2 g1 act1"] == "conv_igemm"
+    assert by["conv3x3 64x80x80->128x40x40 k3 s2 g1 act1"] == "conv_s2p"
+    assert by["conv3x3 128x40x40->256x20x20 k3 s2 g1 act1"] == "conv_igemm"
     s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), int(i["desc"].split()[1].split("x")[1]),
            "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
 
