@@ -103,6 +103,22 @@ __global__ void __launch_bounds__(256, 2) conv1x1_pw_kernel(const ConvParams p, 
       b[sl] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
   };
+  // Cin not a multiple of 8: the channels of the last 8-channel piece past Cin (a channels-
+  // last view's padding, which need not hold finite values) are zeroed bitwise
+  auto mask_ragged = [&](long s, h8 (&b)[NSL]) __attribute__((always_inline)) {
+    const int ch = (int)(s % g.nch);
+#pragma unroll
+    for (int sl = 0; sl < NSL; ++sl) {
+      const int k = ch * KC + sl * 16 + kq;
+      if (k < p.Cin && k + 8 > p.Cin) {
+        u16x8 keep;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) keep[e] = k + e < p.Cin ? (unsigned short)0xffff : (unsigned short)0;
+        b[sl] = __builtin_bit_cast(h8, __builtin_bit_cast(u16x8, b[sl]) & keep);
+      }
+    }
+  };
+  const bool ragged = p.Cin != p.cin8;
 
   acc_t acc[CB];
 #pragma unroll
@@ -157,7 +173,8 @@ __global__ void __launch_bounds__(256, 2) conv1x1_pw_kernel(const ConvParams p, 
       for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
     }
   };
-  auto step = [&](long s, const h8 (&b)[NSL]) __attribute__((always_inline)) {
+  auto step = [&](long s, h8 (&b)[NSL]) __attribute__((always_inline)) {
+    if (ragged) mask_ragged(s, b);
     const int ch = (int)(s % g.nch);
 #pragma unroll
     for (int sl = 0; sl < NSL; ++sl)

@@ -319,6 +319,7 @@ def test_conv3x3_s2_persistent_no_act(tmp_path):
     (48, 40, 97, 61, 8, pw.ACT_HSWISH),    # K 48 (a partly empty chunk), Cout 40, odd pixel count
     (512, 24, 20, 30, 64, pw.ACT_RELU),    # K 512 (eight chunks), Cout 24 (ragged 32-channel block)
     (64, 56, 80, 80, 6, pw.ACT_SILU),      # Cout 56 (ragged second 32-channel block)
+    (51, 48, 80, 80, 6, pw.ACT_SILU),      # Cin 51: the last 8-channel piece masked past Cin
     (64, 64, 40, 40, 24, pw.ACT_NONE),     # no activation
 ])
 def test_conv1x1_streaming(tmp_path, cin, cout, H, W, batch, act):
