@@ -708,11 +708,11 @@ __global__ void __launch_bounds__(256) dw_generic_kernel(const ConvParams p, Fas
   vst(p.y, b, c, hw, v);
 }
 
-// Channel-planar (NCHW in and out) depthwise with K in {3, 5}: one lane = PX consecutive
-// output pixels of one row of one channel plane (strips of a plane on neighbouring lanes,
-// then the next channel), grid (strips of all planes, image); each input row segment of the
-// strip is loaded once for its PX outputs.  Same tap order and roundings as the other
-// kernels.
+// Channel-planar depthwise (NCHW input, output in any layout) with K in {3, 5}: one lane =
+// PX consecutive output pixels of one row of one channel plane (strips of a plane on
+// neighbouring lanes, then the next channel), grid (strips of all planes, image); each input
+// row segment of the strip is loaded once for its PX outputs.  Same tap order and roundings
+// as the other kernels.
 template <int K, int S, int PX>
 __global__ void __launch_bounds__(256) dw_nchw_kernel(const ConvParams p, FastDiv d_strips, FastDiv d_plane)
 {
@@ -747,7 +747,6 @@ __global__ void __launch_bounds__(256) dw_nchw_kernel(const ConvParams p, FastDi
       for (int j = 0; j < PX; ++j) acc[j] += xr[j * S + kx] * w[ky * K + kx];
   }
   const float bias = p.bias ? p.bias[c] : 0.0f;
-  _Float16 * yp = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + (long)c * p.y.cs;
 #pragma unroll
   for (int j = 0; j < PX; ++j) {
     const int ox = ox0 + j;
@@ -755,7 +754,7 @@ __global__ void __launch_bounds__(256) dw_nchw_kernel(const ConvParams p, FastDi
     const int hw = oy * p.Wo + ox;
     float v = (float)(_Float16)act_f(acc[j] + bias, p.act);
     if (p.r.ptr) v += vld(p.r, b, c, hw);
-    yp[hw] = (_Float16)v;
+    vst(p.y, b, c, hw, v);  // channel planes or channels-last
   }
 }
 
@@ -906,8 +905,7 @@ static bool dw_use_strip(const ConvParams & p)
 std::string dw_launch_tag(const ConvParams & p)
 {
   if (!dwconv_vectorizable(p))
-    return p.x.layout == kNCHW && p.y.layout == kNCHW && (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2)
-               ? "planar px=4" : "generic";
+    return p.x.layout == kNCHW && (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2) ? "planar px=4" : "generic";
   if (dw_use_strip(p)) return "strip px=4";
   const DwPick d = dw_pick(p);
   char b[128];
@@ -920,8 +918,8 @@ void launch_dwconv(const ConvParams & p, hipStream_t s)
   if (!dwconv_vectorizable(p)) {
     if (p.Cin > 65535 || p.batch > 65535) throw std::runtime_error("depthwise: grid");
     const dim3 grid(nblk((long)p.Ho * p.Wo, 256), (unsigned)p.Cin, (unsigned)p.batch);
-    const bool planar = p.x.layout == kNCHW && p.y.layout == kNCHW && (long)p.H * p.W < (1L << 31) &&
-                        (p.K == 3 || p.K == 5) && (p.S == 1 || p.S == 2);
+    const bool planar = p.x.layout == kNCHW && (long)p.H * p.W < (1L << 31) && (p.K == 3 || p.K == 5) &&
+                        (p.S == 1 || p.S == 2);
     if (planar) {
       constexpr int PX = 4;
       const int strips = (p.Wo + PX - 1) / PX;
