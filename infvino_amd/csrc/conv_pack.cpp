@@ -182,9 +182,10 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   // where it was measured faster than the implicit GEMM (MI355X, batch 64, kernel trace):
   // every Cout <= 32 (32->32 at 160x160: 37.5 vs 46.4 us, 48->32: 49.2 vs 53.0), Cout <= 64
   // with K <= 96 (64->64 at 80x80: 24.2 vs 25.9, 96->64: 28.8 vs 31.8) or K = 128 at 80x80
-  // and up (33.4 vs 35.0); the implicit GEMM stays faster for 192->64 at 80x80 (44.8 vs
-  // 47.3) and 128->64 at 40x40 (12.0 vs 13.3).
-  const bool pw_wins = p.Cout <= 32 || p.cin8 <= 96 || (p.cin8 <= 128 && pw_blocks(p) >= 8192);
+  // and up (33.4 vs 35.0).  The implicit GEMM stays faster for 48->64 at 160x160 (99.7 vs
+  // 104.0), 192->64 at 80x80 (44.8 vs 47.3) and 128->64 at 40x40 (12.0 vs 13.3).
+  const bool pw_wins = p.Cout <= 32 || (p.cin8 <= 96 && p.cin8 != 48) ||
+                       (p.cin8 > 96 && p.cin8 <= 128 && pw_blocks(p) >= 8192);
   if (p.K == 1 && !(s.flags & IVH_FLAG_NO_PW) && pw_plan(p) && pw_blocks(p) >= kPwMinBlocks && pw_wins) {
     p.pw = 1;
     p.ksplit = 1;

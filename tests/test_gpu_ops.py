@@ -316,7 +316,7 @@ def test_conv3x3_s2_persistent_no_act(tmp_path):
 @pytest.mark.parametrize("cin,cout,H,W,batch,act", [
     (32, 32, 160, 160, 2, pw.ACT_SILU),    # the YOLOv8 C2f 1x1 at 160x160
     (96, 64, 80, 80, 6, pw.ACT_SILU),      # 96 -> 64: two 64-channel K chunks (one half empty), two 32-channel blocks
-    (48, 40, 97, 61, 8, pw.ACT_HSWISH),    # K 48 (a partly empty chunk), Cout 40, odd pixel count
+    (48, 24, 97, 61, 8, pw.ACT_HSWISH),    # K 48 (a partly empty chunk), Cout 24, odd pixel count
     (512, 24, 20, 30, 64, pw.ACT_RELU),    # K 512 (eight chunks), Cout 24 (ragged 32-channel block)
     (64, 56, 80, 80, 6, pw.ACT_SILU),      # Cout 56 (ragged second 32-channel block)
     (51, 48, 80, 80, 6, pw.ACT_SILU),      # Cin 51: the last 8-channel piece masked past Cin
@@ -389,14 +389,17 @@ def test_split_k(tmp_path, cin, cout, hw, k, s, batch):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
-@pytest.mark.parametrize("internal", [False, True], ids=["nchw_input", "channels_last"])
+@pytest.mark.parametrize("internal,post", [(False, False), (True, False), (False, True)],
+                         ids=["nchw_input", "channels_last", "nchw_in_channels_last_out"])
 @pytest.mark.parametrize("c,hw,k,s,act", [(16, 112, 3, 2, 3), (96, 14, 5, 1, 3), (72, 28, 5, 2, 3),
                                           (20, 9, 3, 1, 2), (24, 10, 5, 2, 4), (64, 23, 3, 1, 1)])
-def test_depthwise(tmp_path, c, hw, k, s, act, internal):
-    """Depthwise convs on the plan's NCHW graph input (one lane per element) and on an
-    internal channels-last tensor (8 channels x a strip of pixels per lane; odd widths leave
-    partial strips)."""
-    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=act, pre_relu=internal)
+def test_depthwise(tmp_path, c, hw, k, s, act, internal, post):
+    """Depthwise convs on the plan's NCHW graph input (a strip of pixels of one channel plane
+    per lane), on an internal channels-last tensor (8 channels x a strip of pixels per lane;
+    odd widths leave partial strips), and from the NCHW input into an internal channels-last
+    tensor (the planar kernel storing through the output view)."""
+    path, _ = pw.single_conv(str(tmp_path), c, c, hw, hw, k=k, s=s, groups=c, act=act, pre_relu=internal,
+                             post_relu=post)
     assert _conv_kernel(path, 2) == "dwconv"
     _check_f32(path, 2, lo=-1.0)
 
