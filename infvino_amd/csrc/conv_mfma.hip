@@ -398,7 +398,9 @@ ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb)
 std::string igemm_launch_tag(const ConvParams & p)
 {
   char b[160];
-  if (p.pw)
+  if (p.pw == 2)
+    snprintf(b, sizeof b, "blocks=%ld lds=%zu planar-out%s", pw_blocks(p), pwt_lds_bytes(p), p.xt ? " planar-in" : "");
+  else if (p.pw)
     snprintf(b, sizeof b, "blocks=%ld lds=%zu", pw_blocks(p), pw_lds_bytes(p));
   else if (p.pipe)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d items=%ld", p.pipe - 1, p.th, p.tw, pipe_items(p));

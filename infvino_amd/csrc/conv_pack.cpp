@@ -175,6 +175,17 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
         (reinterpret_cast<uintptr_t>(p.x.ptr) % 16) || p.K != 1 || p.S != 1 || p.P != 0)
       throw std::runtime_error("implicit-GEMM input view: NCHW planes of 8-pixel pieces expected");
     p.xt = 1;
+    // the streaming pointwise kernel with planar output when y is NCHW planes too (the plan's
+    // conv1x1 op on graph tensors, Cin <= 64, Cout <= 128).  Measured against the implicit
+    // GEMM on MI355X (SiLU, kernel time): 64->128 at 80x80 57.3 -> 32.4 us at batch 64 (2.7 ->
+    // 4.9 TB/s), 9.5 -> 5.5 us at batch 1; 64->64 at 80x80 38.8 -> 23.0 us; faster on every
+    // shape tried from batch 1 to 64 but 32->64 at 160x160 batch 64 (114 vs 108 us, where both
+    // fall to ~2.8 TB/s on a 315 MB footprint).
+    if (!(s.flags & IVH_FLAG_NO_PW) && pwt_plan(p)) {
+      p.pw = 2;
+      p.ksplit = 1;
+      p.ws = nullptr;
+    }
     return kLaunchIgemm;
   }
   // 1x1 stride 1 with Cout <= 64 on channels-last views: the streaming pointwise kernel of
@@ -184,6 +195,18 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   // with K <= 96 (64->64 at 80x80: 24.2 vs 25.9, 96->64: 28.8 vs 31.8) or K = 128 at 80x80
   // and up (33.4 vs 35.0).  The implicit GEMM stays faster for 48->64 at 160x160 (99.7 vs
   // 104.0), 192->64 at 80x80 (44.8 vs 47.3) and 128->64 at 40x40 (12.0 vs 13.3).
+  // 1x1 from channels-last x to NCHW planes (the heads' last convs, whose outputs are graph
+  // tensors): the planar-output streaming kernel, measured against the implicit GEMM on
+  // MI355X (YOLOv8n-pose heads, batch 64 / 1): 51->51 at 80x80 22.5 -> 18.5 / 5.8 -> 4.6 us,
+  // 64->64 at 80x80 23.9 -> 21.9 / 5.4 -> 4.6 us, at 20x20 6.1 -> 5.2 / 6.4 -> 4.0 us.  Not
+  // for a single class plane (64->1 at 80x80: 13.4 vs 14.5 us at batch 64), where its 64
+  // computed channels are mostly padding.
+  if (p.K == 1 && !(s.flags & IVH_FLAG_NO_PW) && p.y.layout == kNCHW && p.Cout >= 16 && pwt_plan(p)) {
+    p.pw = 2;
+    p.ksplit = 1;
+    p.ws = nullptr;
+    return kLaunchIgemm;
+  }
   const bool pw_wins = p.Cout <= 32 || (p.cin8 <= 96 && p.cin8 != 48) ||
                        (p.cin8 > 96 && p.cin8 <= 128 && pw_blocks(p) >= 8192);
   if (p.K == 1 && !(s.flags & IVH_FLAG_NO_PW) && pw_plan(p) && pw_blocks(p) >= kPwMinBlocks && pw_wins) {

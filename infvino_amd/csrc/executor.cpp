@@ -1885,7 +1885,7 @@ void Model::validate(const Launch & l) const
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
     // the resident-weight, pipelined and persistent stride-2 kernels write 4- or 8-channel
     // groups into the view's padding channels
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.s2 > 2 || p.pw ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.s2 > 2 || p.pw == 1 ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
           "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
@@ -1893,7 +1893,7 @@ void Model::validate(const Launch & l) const
     if (l.kind == Launch::kIgemm) {
       if (p.xt) {
         if (p.x.layout != kNCHW || p.K != 1 || p.S != 1 || p.P != 0 || p.halo || p.res || p.s2 || p.pipe || p.x.cs != HW ||
-            HW % 8 || p.x.img % 8)
+            HW % 8 || p.x.img % 8 || (p.pw && p.pw != 2))
           throw std::runtime_error("igemm planar input geometry");
         check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "igemm planar x");
       } else {
@@ -1937,7 +1937,12 @@ void Model::validate(const Launch & l) const
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 14)) throw std::runtime_error("pipelined conv geometry too large");
         check(p.w, 0, (long)(p.Cout + 127) / 128 * 128 * p.kpad - 1, 2, "pipelined conv w");
       }
-      if (p.pw) {
+      if (p.pw == 2) {
+        if (p.ksplit != 1 || p.halo || p.res || p.pipe || p.s2 || !pwt_plan(p) || pwt_lds_bytes(p) > 65536)
+          throw std::runtime_error("planar pointwise streaming geometry");
+        check(p.w, 0, (long)(p.Cout - 1) * p.kpad + p.cin8 - 1, 2, "planar pointwise w");
+        if (!p.xt) check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "planar pointwise x");
+      } else if (p.pw) {
         if (p.K != 1 || p.S != 1 || p.P != 0 || p.G != 1 || p.H != p.Ho || p.W != p.Wo || p.Cout > 64 || p.Cout < 1 ||
             p.cin8 > 512 || p.kpad < p.cin8 || p.ksplit != 1 || p.halo || p.res || p.pipe || p.s2 || p.xt ||
             !pw_views_ok(p) || pw_lds_bytes(p) > 65536 ||
@@ -2355,7 +2360,7 @@ std::string Model::nodeKernel(int i)
   const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
   case Launch::kIgemm:
-    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.pw ? "conv_pw" : l.cp.s2 ? (l.cp.s2 > 2 ? "conv_s2p" : "conv_s2") : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
+    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.pw == 2 ? "conv_pw_planar" : l.cp.pw ? "conv_pw" : l.cp.s2 ? (l.cp.s2 > 2 ? "conv_s2p" : "conv_s2") : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";

@@ -76,6 +76,11 @@ bool pw_views_ok(const ConvParams & p);
 bool pw_plan(const ConvParams & p);         // eligible (shape, activation, views, LDS)
 long pw_blocks(const ConvParams & p);       // 32-pixel blocks of the batch
 size_t pw_lds_bytes(const ConvParams & p);  // weights and bias in LDS
+// planar-output variant (p.pw == 2): NCHW y, x NCHW planes (p.xt) or channels-last,
+// Cin <= 64, Cout <= 128
+bool pwt_views_ok(const ConvParams & p);
+bool pwt_plan(const ConvParams & p);
+size_t pwt_lds_bytes(const ConvParams & p);
 constexpr long kPwMinBlocks = 1024;
 void launch_conv_pw(const ConvParams & p, hipStream_t s);
 

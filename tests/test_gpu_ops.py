@@ -340,6 +340,25 @@ def test_conv1x1_streaming(tmp_path, cin, cout, H, W, batch, act):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (64, 128, 80, 80, 6, pw.ACT_SILU),     # the plan's conv1x1 op at the reference's benchmark shape
+    (48, 96, 40, 56, 16, pw.ACT_HSWISH),   # K 48 in a 64-channel step, Cout 96 (a half-empty last block)
+    (24, 40, 56, 57, 11, pw.ACT_RELU),     # K 24, Cout 40; 3192-pixel planes (blocks straddle images, ragged last block)
+    (5, 17, 48, 48, 16, pw.ACT_NONE),      # 5 input planes, 17 output planes, no activation
+])
+def test_conv1x1_planar(tmp_path, cin, cout, H, W, batch, act):
+    """1x1 convs from NCHW planes to NCHW planes (graph input to graph output) through the
+    planar-output streaming kernel of conv_pw.hip, vs the oracle and vs the implicit GEMM."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=1, act=act)
+    print(f"planar 1x1 {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    assert _kernels(path, batch).count("conv_pw_planar") == 1
+    assert "conv_pw_planar" not in _kernels(path, batch, ia.IVH_FLAG_NO_PW)
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PW)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
 def test_halo_residual_chain(tmp_path):
     """Bottleneck chain (3x3, 3x3 + residual) on 48x48: halo kernel with the fused residual."""
     def build(pb):
@@ -542,13 +561,18 @@ def test_pool_chain_without_concat(tmp_path):
 ])
 def test_conv1x1_planar_input(tmp_path, cin, cout, hw, batch):
     """1x1 convs reading the plan's NCHW graph input (BASELINE config 1's shape class): the
-    implicit GEMM loads 8-pixel pieces of each channel plane and transposes them in LDS."""
+    implicit GEMM (IVH_FLAG_NO_PW) loads 8-pixel pieces of each channel plane and transposes
+    them in LDS; by default Cin <= 64, Cout <= 128 go to the planar streaming kernel."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=1, act=pw.ACT_SILU)
-    kern = _conv_kernel(path, batch)
+    kern = _conv_kernel(path, batch, ia.IVH_FLAG_NO_PW)
     assert kern == "conv_direct" if (hw * hw) % 8 else kern in ("conv_igemm", "conv_igemm_sk")
-    _check_f32(path, batch, lo=-1.0)
+    planar = (hw * hw) % 8 == 0 and cin <= 64 and cout <= 128
+    assert (_conv_kernel(path, batch) == "conv_pw_planar") == planar
+    _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PW)
+    if planar:
+        _check_f32(path, batch, lo=-1.0)
     if kern == "conv_igemm_sk":
-        _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_SPLITK)
+        _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PW | ia.IVH_FLAG_NO_SPLITK)
 
 
 @pytest.mark.parametrize("C,H,heads,batch", [(256, 20, 4, 3), (128, 20, 2, 2), (256, 16, 4, 2), (128, 12, 2, 3),

@@ -80,9 +80,25 @@ def test_kernel_choice_yolov8(plans):
         return k == ("conv_pipe" if cin > 64 and hw >= 40 else "conv_halo")
     assert s1 and all(want(k, cin, hw, res) for k, cin, hw, res in s1)
     assert sum(k == "conv_res" for k, _, _, _ in s1) >= 16
+    # the heads' last 1x1 convs (box 64 and keypoint 51 planes at three scales) write the NCHW
+    # head tensors through the planar-output streaming kernel; the single class plane stays on
+    # the implicit GEMM
+    planar = sorted(i["desc"].split()[1] for i in info if i["kernel"] == "conv_pw_planar")
+    assert planar == sorted(f"{c}x{hw}x{hw}->{o}x{hw}x{hw}" for hw in (80, 40, 20) for c, o in ((51, 51), (64, 64)))
     assert sum(k == "conv_pipe" for k, _, _, _ in s1) >= 3
     assert sum(k == "conv_pair" for k, _, _, _ in s1) == 4 and sum(k == "(fused)" for k, _, _, _ in s1) == 4
     m.close()
+
+
+def test_kernel_choice_conv1x1_config(tmp_path):
+    """The plan's conv1x1 op on graph tensors (NCHW in and out, 64 -> 128 at 80x80) takes the
+    planar streaming kernel at batch 1 and 64, and the implicit GEMM with IVH_FLAG_NO_PW."""
+    path, _ = pw.conv1x1_config(str(tmp_path))
+    for b, fl, want in ((1, 0, "conv_pw_planar"), (64, 0, "conv_pw_planar"), (64, ia.IVH_FLAG_NO_PW, "conv_igemm")):
+        m = ia.PlanModel(path, 0, b, DRY | fl)
+        m.run(b)
+        assert m.nodeInfo(0)["kernel"] == want
+        m.close()
 
 
 @pytest.mark.parametrize("name,cin,cout,H,W,k,s,g,act", pw.CONV_SWEEP, ids=[c[0] for c in pw.CONV_SWEEP])
