@@ -75,7 +75,10 @@ def calibrate(ia, pw):
 
 def sweep_plan(pw, d, name):
     """Plan of one conv sweep layer in the layout it has inside a model: the stem reads the
-    NCHW graph input, every other conv sits between two ReLUs (channels-last tensors)."""
+    NCHW graph input, every other conv sits between two ReLUs (channels-last tensors).
+    "config1": the plan's conv1x1 op on graph tensors (64->128 at 80x80, NCHW in and out)."""
+    if name == "config1":
+        return pw.conv1x1_config(d)[0]
     _, cin, cout, H, W, k, s, g, act = next(c for c in pw.CONV_SWEEP if c[0] == name)
     pb = pw.PlanBuilder(d, seed=0)
     x = pb.input("x", [1, cin, H, W])
@@ -334,7 +337,7 @@ def main():
     ap.add_argument("--no-models", action="store_true", help="skip the MobileNetV3 / YOLO11n lines")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch node by node instead of replaying the captured HIP graph")
-    ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer for --phase layer")
+    ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer (or config1) for --phase layer")
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
                     help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
     ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer"],
