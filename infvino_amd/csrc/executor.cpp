@@ -1275,28 +1275,31 @@ void Model::findPairs()
       if (in != "-") readers[in].push_back((int)i);
   std::set<std::string> outs(outputs_.begin(), outputs_.end());
   auto act_ok = [](int a) { return a == kActNone || a == kActSiLU || a == kActReLU || a == kActHSwish; };
-  // channels of a conv that can be a pair member, else 0
-  auto pair_c = [&](const PlanNode & n) {
+  // (input, output) channels of a conv that can be a pair member (3x3 stride 1 pad 1, same
+  // map size), else (0, 0)
+  auto pair_io = [&](const PlanNode & n) {
+    const std::pair<int, int> none{0, 0};
     if (n.op != "conv3x3" || n.ins.size() < 2 || n.outs.size() != 1 || n.i("stride", 1) != 1 || n.i("pad", 1) != 1)
-      return 0;
+      return none;
     const Tensor & w = *T_.at(n.ins[1]);
     const Tensor & x = *T_.at(n.ins[0]);
-    const int c = x.C;
-    const bool ok = (c == 16 || c == 32) && w.dims.size() == 4 && w.dims[0] == c && w.dims[1] == c &&
-                    w.dims[2] == 3 && w.dims[3] == 3 && n.i("Hout") == x.H && n.i("Wout") == x.W && act_ok(n.i("act"));
-    return ok ? c : 0;
+    const bool ok = w.dims.size() == 4 && w.dims[1] == x.C && w.dims[2] == 3 && w.dims[3] == 3 &&
+                    n.i("Hout") == x.H && n.i("Wout") == x.W && act_ok(n.i("act"));
+    return ok ? std::pair<int, int>{x.C, (int)w.dims[0]} : none;
   };
   std::vector<char> used(nodes_.size(), 0);
   for (size_t i = 0; i < nodes_.size(); ++i) {
     const PlanNode & a = nodes_[i];
-    const int c = used[i] ? 0 : pair_c(a);
-    if (!c || (a.ins.size() > 3 && a.ins[3] != "-")) continue;
+    if (used[i]) continue;
+    const auto io = pair_io(a);
+    const int c = io.first, mid = io.second;
+    if (!pair_channels_ok(c, mid) || (a.ins.size() > 3 && a.ins[3] != "-")) continue;
     const std::string & t = a.outs[0];
     const auto it = readers.find(t);
     if (it == readers.end() || it->second.size() != 1 || outs.count(t)) continue;
     const int j = it->second[0];
     const PlanNode & b = nodes_[j];
-    if (j <= (int)i || used[j] || pair_c(b) != c || b.ins[0] != t) continue;
+    if (j <= (int)i || used[j] || pair_io(b) != std::pair<int, int>{mid, c} || b.ins[0] != t) continue;
     if (b.ins.size() > 3 && b.ins[3] != "-" && b.ins[3] != a.ins[0]) continue;
     if (T_.at(b.ins[0])->H != T_.at(a.ins[0])->H || T_.at(b.ins[0])->W != T_.at(a.ins[0])->W) continue;
     pair_next_[i] = j;
@@ -1311,9 +1314,11 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   Launch A = convLaunch(ni, batch), B = convLaunch((size_t)nj, batch);
   if (A.kind != Launch::kIgemm || B.kind != Launch::kIgemm) return false;
   // both convs' LDS-patch packing of one channel chunk: [C rows][taps][C channels], 9 taps
-  // with C = 32, 10 (a zero tenth) with C = 16
-  const int C = A.cp.Cin, hi = C == 16 ? 0 : 1, kpad = halo_taps(C) * C;  // halo segments 0: ck 16, 1: ck 32
-  if ((C != 16 && C != 32) || B.cp.Cin != C || A.cp.Cout != C || B.cp.Cout != C) return false;
+  // with C = 32, 10 (a zero tenth) with C = 16.  A narrower middle (C = 16, 8 channels) runs
+  // as C: the first conv's rows past 8 and the second conv's channels past 8 are the
+  // packing's zero padding, so the padded channels of t are act(0) = 0 and add nothing.
+  const int C = A.cp.Cin, M = A.cp.Cout, hi = C == 16 ? 0 : 1, kpad = halo_taps(C) * C;  // halo segments 0: ck 16, 1: ck 32
+  if (!pair_channels_ok(C, M) || B.cp.Cin != M || B.cp.Cout != C) return false;
   const std::pair<ConvParams *, size_t> convs[2] = {{&A.cp, ni}, {&B.cp, (size_t)nj}};
   for (const auto & pr : convs) {
     const Packed & pk = packed_[pr.second];
@@ -1861,7 +1866,7 @@ void Model::validate(const Launch & l) const
     const long HW = (long)p.H * p.W;
     if (p.batch < 1 || p.batch > 65535 || a.batch != p.batch) throw std::runtime_error("batch out of grid range");
     const int C = a.Cin;
-    if ((C != 16 && C != 32) || a.Cout != C || p.Cin != C || p.Cout != C || a.K != 3 || p.K != 3 || a.S != 1 ||
+    if (!pair_channels_ok(C, a.Cout) || p.Cin != a.Cout || p.Cout != C || a.K != 3 || p.K != 3 || a.S != 1 ||
         p.S != 1 || a.P != 1 || p.P != 1 || a.H != p.H || a.W != p.W || p.Ho != p.H || p.Wo != p.W ||
         a.kpad != halo_taps(C) * C || p.kpad != halo_taps(C) * C)
       throw std::runtime_error("conv pair geometry");

@@ -218,19 +218,25 @@ def test_pipe_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     (16, 33, 35, 3, False, pw.ACT_HSWISH, pw.ACT_RELU),  # 16 channels: ragged tiles, no shortcut
     (16, 20, 20, 6, True, pw.ACT_RELU, pw.ACT_NONE),     # 16 channels: tiles across image boundaries
     (16, 160, 160, 9, True, pw.ACT_SILU, pw.ACT_SILU),   # 16 channels: several tiles per work-group
+    (-16, 160, 160, 2, True, pw.ACT_SILU, pw.ACT_SILU),  # 16 -> 8 -> 16: the YOLO11 C3k2 bottleneck at 160x160
+    (-16, 33, 35, 3, False, pw.ACT_HSWISH, pw.ACT_RELU), # 8-channel middle: ragged tiles, no shortcut
+    (-16, 20, 20, 6, True, pw.ACT_RELU, pw.ACT_NONE),    # 8-channel middle: tiles across image boundaries
 ])
 def test_conv_pair(tmp_path, C, H, W, batch, res, act1, act2):
     """A bottleneck of C = 16 or 32 channels (3x3 -> 3x3, optionally + the block input) as one
-    launch of the fused pair kernel vs the oracle and vs the two convs run apart."""
+    launch of the fused pair kernel vs the oracle and vs the two convs run apart; C < 0: -C
+    outer channels with a middle of half as many (16 -> 8 -> 16)."""
+    mid = -C // 2 if C < 0 else C
+    C = abs(C)
     def build(pb):
         x = pb.unary(pb.input("x", [1, C, H, W]), pw.UN_RELU)
-        t = pb.conv(x, C, 3, act=act1)
+        t = pb.conv(x, mid, 3, act=act1)
         t = pb.conv(t, C, 3, act=act2)
         if res:
             t = pb.binary(x, t, 0)
         return pb.unary(t, pw.UN_RELU)
     path = _small_plan(tmp_path, build)
-    print(f"conv pair C {C} {H}x{W} batch {batch} res {res} acts {act1} {act2}", flush=True)
+    print(f"conv pair C {C} mid {mid} {H}x{W} batch {batch} res {res} acts {act1} {act2}", flush=True)
     assert _kernels(path, batch).count("conv_pair") == 1
     assert "conv_pair" not in _kernels(path, batch, ia.IVH_FLAG_NO_FUSE_PAIR)
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
