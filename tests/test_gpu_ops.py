@@ -117,8 +117,12 @@ def test_conv_shapes(tmp_path, cin, cout, hw, k, s, act):
     (the graph input)."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=k, s=s, act=act, pre_relu=cin > 3)
     kern = _conv_kernel(path, 3)
-    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res", "conv_pipe")
+    assert kern == "conv_stem" if cin <= 3 else kern in ("conv_igemm", "conv_igemm_sk", "conv_halo", "conv_res", "conv_pipe",
+                                                         "conv_pw_planar")
     _check_f32(path, 3, lo=-1.0)
+    if kern == "conv_pw_planar":  # the implicit GEMM on the same layer too
+        assert _conv_kernel(path, 3, ia.IVH_FLAG_NO_PW) == "conv_igemm"
+        _check_f32(path, 3, lo=-1.0, flags=ia.IVH_FLAG_NO_PW)
 
 
 @pytest.mark.parametrize("cin,cout,H,W,batch,s", [
