@@ -364,7 +364,9 @@ int igemm_kpad(int cout, int kk)
 }
 
 // Split-K factor: convs whose output tiles cannot fill the chip (batch 1, 20x20 / 40x40
-// feature maps) and whose K loop is long get their K range split across work-groups.
+// feature maps) and whose K loop is long get their K range split across work-groups, by 3
+// or more: a split by 2 did not pay for its reduce launch (MI355X, YOLOv8n-pose batch 1:
+// 32->64 s2 at 160x160 12.0 vs 8.7 us, 256->128 1x1 at 40x40 11.1 vs 9.8 us).
 int igemm_ksplit(long M, int cout, int kpad)
 {
   const int bn = igemm_bn(cout);
@@ -374,7 +376,7 @@ int igemm_ksplit(long M, int cout, int kpad)
   int s = (int)((384 + tiles - 1) / tiles);
   s = s < nk / 4 ? s : nk / 4;
   s = s < 16 ? s : 16;
-  return s < 2 ? 1 : s;
+  return s < 3 ? 1 : s;
 }
 
 // Batch chunk that keeps a conv's input view below 2^31 bytes (the kernels' buffer ranges
