@@ -109,6 +109,29 @@ def test_kernel_choice_yolo11_pairs(plans):
     m.close()
 
 
+@pytest.mark.parametrize("cin,cout,hw,pre,post,batch,want", [
+    (64, 128, 80, False, False, 64, "conv_pw_planar"),   # NCHW planes in and out
+    (5, 17, 48, False, False, 16, "conv_pw_planar"),     # few planes, ragged Cout
+    (64, 128, 10, False, False, 2, "conv_direct"),       # 100-pixel planes: not 8-pixel pieces
+    (96, 64, 40, False, False, 4, "conv_igemm"),         # Cin > 64: the implicit GEMM's planar loads
+    (64, 136, 40, False, False, 4, "conv_igemm"),        # Cout > 128
+    (64, 64, 40, True, False, 4, "conv_pw_planar"),      # channels-last in, NCHW planes out
+    (64, 8, 40, True, False, 4, "conv_igemm"),           # a few output planes: the implicit GEMM
+    (64, 64, 80, True, True, 64, "conv_pw"),             # channels-last in and out
+])
+def test_kernel_choice_pointwise(tmp_path, cin, cout, hw, pre, post, batch, want):
+    """Which 1x1 kernel the planner picks by layout and shape (dry run): the planar-output
+    streaming kernel for NCHW outputs with Cin <= 64, Cout <= 128 (Cout >= 16 from a
+    channels-last input) and 8-pixel pieces, the channels-last one for channels-last
+    outputs, the implicit GEMM (or the direct kernel) otherwise."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, hw, hw, k=1, act=pw.ACT_SILU, pre_relu=pre, post_relu=post)
+    m = ia.PlanModel(path, 0, batch, DRY)
+    m.run(batch)
+    kern = next(m.nodeInfo(i)["kernel"] for i in range(m.nodeCount()) if m.nodeInfo(i)["op"].startswith("conv"))
+    m.close()
+    assert kern == want
+
+
 def test_kernel_choice_conv1x1_config(tmp_path):
     """The plan's conv1x1 op on graph tensors (NCHW in and out, 64 -> 128 at 80x80) takes the
     planar streaming kernel at batch 1 and 64, and the implicit GEMM with IVH_FLAG_NO_PW."""
