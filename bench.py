@@ -28,6 +28,9 @@ table goes to stderr.
                  matrix cores draw more power on random data and the clock drops, so the
                  random-operand rate is the practical MFMA roof; conv_sweep rows of MFMA-bound
                  layers carry frac_practical against it
+  hbm_stream_probe  plain torch fill / copy / broadcast-copy rates on the box: the practical
+                 HBM roof of a streaming kernel's traffic pattern; config1's batch-64 line
+                 carries frac_practical against the broadcast copy (1 read : 2 writes)
   cpu_baseline   the CPU oracle (oracle/, C + OpenMP) on a bounded sample of the same
                  workload on this host's cores -- a reported baseline, not a target; it
                  records the probe for a CPU OpenCL runtime that could run the reference's own
@@ -266,6 +269,54 @@ def mfma_roof_probe():
     return res
 
 
+def hbm_stream_probe():
+    """Runs `bench.py --phase hbm` as a child process (torch initialises its own HIP context
+    there, away from the library's) and returns its JSON line, or a note."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--phase", "hbm"], capture_output=True,
+                           text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return {"note": "probe timed out"}
+    if r.returncode != 0:
+        return {"note": f"probe failed: {r.stderr.strip()[-200:]}"}
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"[bench] HBM stream probe: {res}")
+    return res
+
+
+def hbm_stream_rates():
+    """Plain torch kernels with the traffic patterns of the streaming convs, timed with
+    events: a fill of 104.9 MB (writes only), a 52.4 MB copy (1:1) and a broadcast copy of
+    52.4 MB into 104.9 MB (1 read : 2 writes, the pattern of the conv1x1 config 64 -> 128).
+    What they reach on this box is the practical HBM roof of such a stream (below the 8 TB/s
+    peak); footprints under 256 MB are partly served by the Infinity Cache between passes."""
+    import torch
+    n = 52428800 // 2
+    x = torch.randn(n, device="cuda:0", dtype=torch.float16)
+    y = torch.empty(2 * n, device="cuda:0", dtype=torch.float16)
+    z = torch.empty(n, device="cuda:0", dtype=torch.float16)
+
+    def rate(fn, nbytes, iters=50):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(nbytes / (e0.elapsed_time(e1) / iters * 1e-3) / 1e9, 1)
+
+    y2 = y.view(2, n)
+    res = {"fill_gbs": rate(lambda: y.fill_(1.0), 4 * n),
+           "copy_gbs": rate(lambda: z.copy_(x), 4 * n),
+           "broadcast_1r2w_gbs": rate(lambda: y2.copy_(x.unsqueeze(0).expand(2, n)), 6 * n),
+           "unit": "GB/s of algorithmic bytes", "source": "torch fill_ / copy_ kernels"}
+    return res
+
+
 def model_lines(ia, pw, specs, steps, warmup):
     """The other model configurations: images/s of graph replays at each batch (inputs
     resident in HBM) and the synchronous batch-1 latency."""
@@ -340,16 +391,20 @@ def main():
     ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer (or config1) for --phase layer")
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
                     help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
-    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer"],
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
                          "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE; "
-                         "sweep: the conv sweep only; layer: --steps passes of one sweep layer (--layer)")
+                         "sweep: the conv sweep only; layer: --steps passes of one sweep layer (--layer); "
+                         "hbm: the torch HBM stream probe alone (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the batch axis would shard as independent replicas, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    if args.phase == "hbm":  # before the library touches the GPU
+        print(json.dumps(hbm_stream_rates()))
+        return
     import infvino_amd as ia
     from infvino_amd import planwriter as pw
 
@@ -457,6 +512,10 @@ def main():
     m1.close()
 
     c1 = None if args.no_sweep else config1(ia, pw, max(args.profile_iters, 10))
+    hbm_probe = hbm_stream_probe()
+    if c1 and hbm_probe.get("broadcast_1r2w_gbs"):
+        c1["b64"]["roofline"]["frac_practical"] = round(
+            c1["b64"]["roofline"]["achieved"] / hbm_probe["broadcast_1r2w_gbs"], 4)
     probe = mfma_roof_probe()
     sweep = None
     if not args.no_sweep:
@@ -517,6 +576,7 @@ def main():
         "roofline": roof,
         "roofline_step": roof_step,
         "mfma_roof_probe": probe,
+        "hbm_stream_probe": hbm_probe,
         "config1": c1,
         "conv_sweep": sweep,
         "attention": attn,
