@@ -77,6 +77,12 @@ ConvPacking conv_packing(const ConvSpec & s)
         pk.kpad_halo[hi] = (cin_g + ck - 1) / ck * halo_taps(ck) * ck;
         pk.halo[hi] = seg((size_t)rows * pk.kpad_halo[hi] * 2);
       }
+      // 16 input channels: also one 32-channel chunk (zero past 16), the packing of the
+      // second conv of a 32 -> 16 -> 32 bottleneck run as a fused pair of 32 channels
+      if (cin_g == 16 && s.Cout == 32 && pk.halo[1] == kNoSeg) {
+        pk.kpad_halo[1] = halo_taps(32) * 32;
+        pk.halo[1] = seg((size_t)rows * pk.kpad_halo[1] * 2);
+      }
     }
   } else if (pk.family == kFamDirect && s.G == 1 && cin_g <= 3 && s.K == 3 && s.Cout <= 32) {
     const int rows = (s.Cout + 15) / 16 * 16;

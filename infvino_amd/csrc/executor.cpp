@@ -1314,9 +1314,9 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   Launch A = convLaunch(ni, batch), B = convLaunch((size_t)nj, batch);
   if (A.kind != Launch::kIgemm || B.kind != Launch::kIgemm) return false;
   // both convs' LDS-patch packing of one channel chunk: [C rows][taps][C channels], 9 taps
-  // with C = 32, 10 (a zero tenth) with C = 16.  A narrower middle (C = 16, 8 channels) runs
-  // as C: the first conv's rows past 8 and the second conv's channels past 8 are the
-  // packing's zero padding, so the padded channels of t are act(0) = 0 and add nothing.
+  // with C = 32, 10 (a zero tenth) with C = 16.  A middle of M = C / 2 channels runs as C:
+  // the first conv's rows past M and the second conv's channels past M are the packing's
+  // zero padding, so the padded channels of t are act(0) = 0 and add nothing.
   const int C = A.cp.Cin, M = A.cp.Cout, hi = C == 16 ? 0 : 1, kpad = halo_taps(C) * C;  // halo segments 0: ck 16, 1: ck 32
   if (!pair_channels_ok(C, M) || B.cp.Cin != M || B.cp.Cout != C) return false;
   const std::pair<ConvParams *, size_t> convs[2] = {{&A.cp, ni}, {&B.cp, (size_t)nj}};

@@ -66,8 +66,8 @@ void launch_conv_pipe(const ConvParams & p, hipStream_t s);
 // one launch
 bool pair_plan(int C, int H, int W, int batch, int * th, int * tw);  // output tile; false: not eligible
 // channels of a fused bottleneck pair: outer C (the block's input and output) and middle
-// M (the first conv's output): C = 16 or 32 with M = C, or C = 16 with M = 8
-inline bool pair_channels_ok(int c, int m) { return (c == 16 || c == 32) && (m == c || (c == 16 && m == 8)); }
+// M (the first conv's output): C = 16 or 32 with M = C or M = C / 2
+inline bool pair_channels_ok(int c, int m) { return (c == 16 || c == 32) && (m == c || 2 * m == c); }
 bool pair_tile_ok(int C, int th, int tw);  // the tile fits the kernel's ring, patch and rows
 long pair_tiles(int H, int W, int batch, int th, int tw);
 // a: the first conv (x, weights / bias / act of conv 1), b: the second (y, residual,

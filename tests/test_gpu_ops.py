@@ -225,11 +225,13 @@ def test_pipe_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     (-16, 160, 160, 2, True, pw.ACT_SILU, pw.ACT_SILU),  # 16 -> 8 -> 16: the YOLO11 C3k2 bottleneck at 160x160
     (-16, 33, 35, 3, False, pw.ACT_HSWISH, pw.ACT_RELU), # 8-channel middle: ragged tiles, no shortcut
     (-16, 20, 20, 6, True, pw.ACT_RELU, pw.ACT_NONE),    # 8-channel middle: tiles across image boundaries
+    (-32, 80, 80, 2, True, pw.ACT_SILU, pw.ACT_SILU),    # 32 -> 16 -> 32: the YOLO11 C3k2 bottleneck at 80x80
+    (-32, 33, 35, 3, False, pw.ACT_HSWISH, pw.ACT_RELU), # 16-channel middle: ragged tiles, no shortcut
 ])
 def test_conv_pair(tmp_path, C, H, W, batch, res, act1, act2):
     """A bottleneck of C = 16 or 32 channels (3x3 -> 3x3, optionally + the block input) as one
     launch of the fused pair kernel vs the oracle and vs the two convs run apart; C < 0: -C
-    outer channels with a middle of half as many (16 -> 8 -> 16)."""
+    outer channels with a middle of half as many (16 -> 8 -> 16, 32 -> 16 -> 32)."""
     mid = -C // 2 if C < 0 else C
     C = abs(C)
     def build(pb):

@@ -91,18 +91,20 @@ def test_kernel_choice_yolov8(plans):
 
 
 def test_kernel_choice_yolo11_pairs(plans):
-    """YOLO11n-pose at batch 64: the C3k2 bottleneck 16 -> 8 -> 16 at 160x160 (with its
-    shortcut) and the two 32-channel bottlenecks at 40x40 run as fused pairs; with
-    IVH_FLAG_NO_FUSE_PAIR none do."""
+    """YOLO11n-pose at batch 64: the C3k2 bottlenecks 16 -> 8 -> 16 at 160x160 and 32 -> 16 ->
+    32 at 80x80 (with their shortcuts) and the two 32-channel bottlenecks at 40x40 run as
+    fused pairs; with IVH_FLAG_NO_FUSE_PAIR none do."""
     m = ia.PlanModel(plans("yolo11n-pose")[0], 0, 64, DRY)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
     m.close()
     pairs = sorted(i["desc"] for i in info if i["kernel"] == "conv_pair")
     assert pairs == sorted(["conv3x3 16x160x160->8x160x160 k3 s1 g1 act1"] +
+                           ["conv3x3 32x80x80->16x80x80 k3 s1 g1 act1"] * 2 +
                            ["conv3x3 32x40x40->32x40x40 k3 s1 g1 act1"] * 2)
     fused = [i["desc"] for i in info if i["kernel"] == "(fused)" and i["op"] == "conv3x3"]
     assert "conv3x3 8x160x160->16x160x160 k3 s1 g1 act1 +res" in fused
+    assert fused.count("conv3x3 16x80x80->32x80x80 k3 s1 g1 act1 +res") == 2
     m = ia.PlanModel(plans("yolo11n-pose")[0], 0, 64, DRY | ia.IVH_FLAG_NO_FUSE_PAIR)
     m.run(64)
     assert not any(m.nodeInfo(i)["kernel"] == "conv_pair" for i in range(m.nodeCount()))
