@@ -357,12 +357,18 @@ def test_conv1x1_streaming(tmp_path, cin, cout, H, W, batch, act):
     (48, 96, 40, 56, 16, pw.ACT_HSWISH),   # K 48 in a 64-channel step, Cout 96 (a half-empty last block)
     (24, 40, 56, 57, 11, pw.ACT_RELU),     # K 24, Cout 40; 3192-pixel planes (blocks straddle images, ragged last block)
     (5, 17, 48, 48, 16, pw.ACT_NONE),      # 5 input planes, 17 output planes, no activation
+    (-51, 51, 40, 40, 4, pw.ACT_SILU),     # channels-last in (Cin 51: the last piece masked), planes out
+    (-64, 64, 20, 20, 3, pw.ACT_NONE),     # the heads' box conv at 20x20 (two blocks straddle images)
+    (-24, 100, 24, 16, 5, pw.ACT_HSWISH),  # channels-last K 24 in one 32-channel step, Cout 100
 ])
 def test_conv1x1_planar(tmp_path, cin, cout, H, W, batch, act):
-    """1x1 convs from NCHW planes to NCHW planes (graph input to graph output) through the
-    planar-output streaming kernel of conv_pw.hip, vs the oracle and vs the implicit GEMM."""
-    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=1, act=act)
-    print(f"planar 1x1 {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    """1x1 convs into NCHW planes (graph outputs) through the planar-output streaming kernel
+    of conv_pw.hip, vs the oracle and vs the implicit GEMM: from NCHW planes (the graph
+    input), or, with cin < 0, from a channels-last internal tensor (a ReLU first)."""
+    pre = cin < 0
+    cin = abs(cin)
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=1, act=act, pre_relu=pre)
+    print(f"planar 1x1 {cin}->{cout} {H}x{W} batch {batch} act {act} channels-last in {pre}", flush=True)
     assert _kernels(path, batch).count("conv_pw_planar") == 1
     assert "conv_pw_planar" not in _kernels(path, batch, ia.IVH_FLAG_NO_PW)
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
