@@ -79,6 +79,11 @@ public:
   {
   }
 
+  /** An int second argument is rejected at compile time: it would otherwise convert to
+   * `profiling` (an older signature took a maximum batch there). */
+  template <class Info, class = decltype(std::declval<const Info &>().plan)>
+  HipBackend(const Info & info, int) = delete;
+
   /** The same with a maximum batch (images per infer) and ivh.h flags. */
   template <class Info, class = decltype(std::declval<const Info &>().plan)>
   HipBackend(const Info & info, bool profiling, int max_batch, uint32_t flags = 0)

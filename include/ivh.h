@@ -111,8 +111,9 @@ int ivh_set_input_f32(ivh_model * m, const float * host, int batch);
    first call; this one streams it through a fixed 8 MiB array that every GPU the library
    runs on holds until the process ends, 2^21 floats at a time, so no batch is too large for
    it (batch is checked against the model's maximum, as for ivh_set_input_f32).  Results are
-   bit-identical to ivh_set_input_f32's.  Calls that overlap on one GPU (two models, or two
-   threads) share the array and race: serialise them per device. */
+   bit-identical to ivh_set_input_f32's.  Calls on one GPU (two models, or two threads) share
+   the array; each call holds a per-device lock until its copies and conversions have
+   finished, so such calls run one after the other. */
 int ivh_set_input_f32_noalloc(ivh_model * m, const float * host, int batch);
 int ivh_run(ivh_model * m, int batch);
 int ivh_sync(ivh_model * m);
@@ -137,7 +138,9 @@ int ivh_node_info(ivh_model * m, int i, char * op, size_t op_len, char * kernel,
                   char * desc, size_t desc_len, double * flops, double * bytes);
 /* Runtime tag of node i: the kernel label of ivh_node_info followed by its launch detail
  * (tile config, channel chunk, K step, split, build), as PlanProfile::NodeRow::tag carries the
- * data path (include/infvino/PlanModel.hpp:208). */
+ * data path (include/infvino/PlanModel.hpp:208).  Kernel labels and tags describe the batch of
+ * the model's last ivh_run / ivh_profile_nodes call (max_batch before the first), since kernel
+ * and tile choices depend on the batch. */
 int ivh_node_tag(ivh_model * m, int i, char * tag, size_t tag_len);
 int ivh_memory_info(const ivh_model * m, int batch, size_t * arena_bytes, size_t * weight_bytes);
 

@@ -142,12 +142,14 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
     }
   }
   // ---- softmax over the keys: lane-local, then with the partner lane holding the other 16.
-  // exp(T - m) = exp2(T log2e - m log2e): one fma and one v_exp_f32 per score, kept in fp32
-  // registers for the probabilities (the softmax node evaluates it twice).
+  // exp(T - m) = exp2((T - m) log2e): the difference first, in fp32 (exact for the scores
+  // near the maximum, which carry the probability mass), then one multiply and one v_exp_f32
+  // per score; the exponentials stay in fp32 registers for the probabilities (the softmax
+  // node evaluates them twice).  Folding m log2e into one fma would round m log2e to fp32,
+  // an exponent error of ulp(m log2e) that exceeds fp16's half ulp once |m| is large.
   float m = fmaxf((float)mx[0], (float)mx[1]);
   m = fmaxf(m, __shfl_xor(m, 32));
   constexpr float kLog2e = 1.4426950408889634f;
-  const float mb = -m * kLog2e;
   float e[NB][16];
   float sum = 0.0f;
 #pragma unroll
@@ -155,7 +157,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
     if (kb >= nb) continue;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      e[kb][v] = __builtin_amdgcn_exp2f(fmaf((float)T[kb][v / 2][v % 2], kLog2e, mb));
+      e[kb][v] = __builtin_amdgcn_exp2f(((float)T[kb][v / 2][v % 2] - m) * kLog2e);
       sum += e[kb][v];
     }
   }
@@ -207,7 +209,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
 int attn_key_blocks(int n)
 {
   const int nb = (n + 31) / 32;
-  return nb <= 4 ? 4 : nb <= 8 ? 8 : nb <= 13 ? 13 : nb <= 16 ? 16 : 0;
+  return nb <= 4 ? 4 : nb <= 8 ? 8 : nb <= 13 ? 13 : 0;
 }
 
 void launch_attention(const AttnParams & a, hipStream_t s)
@@ -217,7 +219,7 @@ void launch_attention(const AttnParams & a, hipStream_t s)
   case 4: hipLaunchKernelGGL(attn_kernel<4>, grid, blk, 0, s, a); break;
   case 8: hipLaunchKernelGGL(attn_kernel<8>, grid, blk, 0, s, a); break;
   case 13: hipLaunchKernelGGL(attn_kernel<13>, grid, blk, 0, s, a); break;
-  default: hipLaunchKernelGGL(attn_kernel<16>, grid, blk, 0, s, a); break;
+  default: throw std::runtime_error("fused attention: more than 416 tokens");
   }
 }
 

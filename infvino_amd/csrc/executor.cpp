@@ -1756,7 +1756,28 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
     out.push_back(L);
     return;
   }
-  if (op == "bmm" || op == "gemm") {
+  if (op == "gemm") {
+    // C[M][N] = A[M][K] . B[K][N] with M = A.dims[0], K = A.dims[1] and N = numel(B) / K, so
+    // B may have any rank (src/PlanModel.cpp:3935-3940); A and B are read row-major.
+    const Tensor & at = *T_[n.ins.at(0)];
+    const Tensor & bt = *T_[n.ins.at(1)];
+    q.a = view(at.name, batch);
+    q.b = view(bt.name, batch);
+    if (at.dims.size() < 2) fail("gemm rank");
+    const long M = at.dims[0], K = at.dims[1];
+    if (M <= 0 || K <= 0) fail("gemm dims");
+    const long Nn = bt.numel / K;
+    if (Nn <= 0) fail("gemm: B smaller than K");
+    if (M * Nn != yt.numel) fail("gemm output numel");
+    if (M > INT32_MAX || Nn > INT32_MAX) fail("gemm dims");
+    q.i0 = 1; q.i1 = (int)M; q.i2 = (int)K; q.i3 = (int)Nn;
+    q.op = 0;
+    if (q.a.layout != kNCHW || q.b.layout != kNCHW || q.y.layout != kNCHW) fail("matmul needs NCHW");
+    L.small = kBmm;
+    out.push_back(L);
+    return;
+  }
+  if (op == "bmm") {
     const Tensor & at = *T_[n.ins.at(0)];
     const Tensor & bt = *T_[n.ins.at(1)];
     q.a = view(at.name, batch);
@@ -2084,6 +2105,7 @@ void Model::dryRun(int batch)
 {
   check_batch(batch, max_batch_);
   (void)launches(batch);
+  last_batch_ = batch;
 }
 
 void Model::enqueue(const std::vector<Launch> & L, size_t b, size_t e)
@@ -2146,9 +2168,10 @@ void Model::setInputF32Trunc(const float * host, int batch)
 
 // The f32 input passes through the GPU's fixed 8 MiB scratch array in chunks: each chunk is
 // copied in and converted before the next copy overwrites the array (one stream orders the
-// copy after the previous chunk's kernel), so any batch fits and nothing is allocated.  Two
-// models converting on the same GPU at the same time share the array and race: callers on
-// one device serialise these calls.
+// copy after the previous chunk's kernel), so any batch fits and nothing is allocated.  Every
+// model on the GPU shares the array, so the call holds the device's scratch lock from the
+// first copy until its stream has drained (also when a HIP call fails midway): calls from
+// models on one device, in any threads, run one after the other.
 void Model::setInputF32TruncNoAlloc(const float * host, int batch)
 {
   check_batch(batch, max_batch_);
@@ -2157,14 +2180,20 @@ void Model::setInputF32TruncNoAlloc(const float * host, int batch)
   float * sc = boundary_scratch(device_);
   const long n = (long)inputNumel();
   const long img = roots_[T_[input_name_]->root]->per_image;
-  for (int b = 0; b < batch; ++b)
-    for (long off = 0; off < n; off += kBoundaryScratchFloats) {
-      const long len = std::min(n - off, kBoundaryScratchFloats);
-      HIPCHECK(hipMemcpyAsync(sc, host + (long)b * n + off, (size_t)len * 4, hipMemcpyHostToDevice, stream_));
-      launch_f32_to_f16_trunc(sc, static_cast<__half *>(input_buf_) + (long)b * img + off, len, stream_);
-    }
-  HIPCHECK(hipGetLastError());
-  HIPCHECK(hipStreamSynchronize(stream_));
+  std::lock_guard<std::mutex> lock(boundary_scratch_lock(device_));
+  try {
+    for (int b = 0; b < batch; ++b)
+      for (long off = 0; off < n; off += kBoundaryScratchFloats) {
+        const long len = std::min(n - off, kBoundaryScratchFloats);
+        HIPCHECK(hipMemcpyAsync(sc, host + (long)b * n + off, (size_t)len * 4, hipMemcpyHostToDevice, stream_));
+        launch_f32_to_f16_trunc(sc, static_cast<__half *>(input_buf_) + (long)b * img + off, len, stream_);
+      }
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipStreamSynchronize(stream_));
+  } catch (...) {
+    (void)hipStreamSynchronize(stream_);  // nothing of this call may still use the array
+    throw;
+  }
 }
 
 void Model::run(int batch)
@@ -2174,6 +2203,7 @@ void Model::run(int batch)
   HIPCHECK(hipSetDevice(device_));
   const auto t0 = std::chrono::steady_clock::now();
   const LaunchPlan & P = launches(batch);
+  last_batch_ = batch;
   const auto & L = P.L;
   if (flags_ & IVH_FLAG_PROFILE) {
     runProfiled(P);
@@ -2317,6 +2347,7 @@ std::vector<double> Model::profileNodes(int batch, int iters)
   check_batch(batch, max_batch_);
   HIPCHECK(hipSetDevice(device_));
   const LaunchPlan & P = launches(batch);
+  last_batch_ = batch;
   const auto & L = P.L;
   iters = std::max(iters, 1);
   std::vector<double> ms(nodes_.size(), 0.0);
@@ -2346,7 +2377,7 @@ std::vector<double> Model::profileNodes(int batch, int iters)
 std::string Model::nodeTag(int i)
 {
   std::string k = nodeKernel(i);
-  const LaunchPlan & P = launches(max_batch_);
+  const LaunchPlan & P = launches(labelBatch());
   if (P.begin.at(i) == P.end.at(i)) return k;
   const Launch & l = P.L[P.begin[i]];
   if (l.kind == Launch::kIgemm) return k + " " + igemm_launch_tag(l.cp);
@@ -2360,7 +2391,7 @@ std::string Model::nodeTag(int i)
 std::string Model::nodeKernel(int i)
 {
   const NodeStat & s = stats_.at(i);
-  const LaunchPlan & P = launches(max_batch_);
+  const LaunchPlan & P = launches(labelBatch());
   if (P.begin.at(i) == P.end.at(i)) return P.covered.at(i) ? "(fused)" : "(view)";
   const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
@@ -2411,10 +2442,15 @@ void Model::buildStats()
       s.desc = buf;
     } else {
       s.kernel = skip_[ni] ? "(view)" : n.op;
-      if (n.op == "bmm" || n.op == "gemm") {
+      if (n.op == "bmm") {
         const Tensor & at = *T_[n.ins[0]];
         const Tensor & bt = *T_[n.ins[1]];
         s.flops = 2.0 * at.numel * (double)bt.dims.back();
+      }
+      if (n.op == "gemm" && T_[n.ins[0]]->dims.size() >= 2) {  // M K N, N = numel(B) / K
+        const Tensor & at = *T_[n.ins[0]];
+        const double M = (double)at.dims[0], K = (double)at.dims[1];
+        s.flops = K > 0 ? 2.0 * M * K * (double)(T_[n.ins[1]]->numel / at.dims[1]) : 0.0;
       }
       if (n.op == "attention") {
         const double N = n.i("n"), h = n.i("heads");

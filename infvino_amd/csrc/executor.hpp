@@ -81,10 +81,13 @@ class Model {
   void clearProfile();
   int nodeCount() const { return (int)nodes_.size(); }
   const NodeStat & nodeStat(int i) const { return stats_.at(i); }
-  // kernel family node i launches at the largest batch (conv_halo / conv_igemm / conv_stem ...)
+  // kernel family node i launches (conv_halo / conv_igemm / conv_stem ...) at the batch of the
+  // last run, dry run or profileNodes call (the largest batch before the first): kernel and
+  // tile choices depend on the batch
   std::string nodeKernel(int i);
-  // nodeKernel plus the launch detail (tile config, K step, split, build) at the largest batch
+  // nodeKernel plus the launch detail (tile config, K step, split, build) at the same batch
   std::string nodeTag(int i);
+  int labelBatch() const { return last_batch_ > 0 ? last_batch_ : max_batch_; }
   size_t arenaBytes(int batch) const { return (size_t)arena_elems1_ * batch * 2; }
   size_t weightBytes() const { return weight_bytes_; }
 
@@ -172,6 +175,7 @@ class Model {
   std::map<int, hipGraphExec_t> graphs_;
   std::vector<NodeStat> stats_;
   double last_run_ms_ = 0.0;
+  int last_batch_ = 0;  // batch of the last run / dry run / profileNodes (0: none yet)
   bool dry_ = false;
   uintptr_t fake_next_ = (uintptr_t)1 << 44;
   std::vector<std::pair<uintptr_t, size_t>> allocs_;

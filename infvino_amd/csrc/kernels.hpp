@@ -4,6 +4,7 @@
 
 #include "ivh_internal.hpp"
 
+#include <mutex>
 #include <string>
 
 namespace ivh {
@@ -143,6 +144,8 @@ void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t
 // 8 MiB) for ivh_set_input_f32_noalloc; `device` must be the current device.
 constexpr long kBoundaryScratchFloats = 1L << 21;
 float * boundary_scratch(int device);
+// one mutex per device, held by a caller while its copies and kernels use that device's array
+std::mutex & boundary_scratch_lock(int device);
 void launch_f16_to_f32(const __half * in, float * out, long n, hipStream_t s);
 
 }  // namespace ivh

@@ -12,6 +12,7 @@
 #include <type_traits>
 #include <initializer_list>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -1850,11 +1851,27 @@ void launch_f32_to_f16_trunc(const float * in, __half * out, long n, hipStream_t
 // the device address of the current GPU's copy, resolved once per device.
 static __device__ __align__(256) float scratch[kBoundaryScratchFloats];
 
-float * boundary_scratch(int device)
+namespace {
+std::mutex & scratch_map_mutex()
 {
   static std::mutex mu;
+  return mu;
+}
+}  // namespace
+
+std::mutex & boundary_scratch_lock(int device)
+{
+  static std::map<int, std::unique_ptr<std::mutex>> lock_of;
+  std::lock_guard<std::mutex> lock(scratch_map_mutex());
+  auto & m = lock_of[device];
+  if (!m) m = std::make_unique<std::mutex>();
+  return *m;
+}
+
+float * boundary_scratch(int device)
+{
   static std::map<int, float *> ptr_of;
-  std::lock_guard<std::mutex> lock(mu);
+  std::lock_guard<std::mutex> lock(scratch_map_mutex());
   const auto it = ptr_of.find(device);
   if (it != ptr_of.end()) return it->second;
   int cur = -1;

@@ -572,18 +572,42 @@ def single_conv(out_dir, cin, cout, H, W, k=1, s=1, groups=1, act=ACT_SILU, seed
     return pb.write(), pb.flops
 
 
-def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0):
-    """The C2PSA attention block alone: input [1, C, H, H] -> ReLU -> qkv 1x1, per-head q^T k * scale
-    over H*H tokens, softmax, v attn^T, + depthwise 3x3 positional conv of v, 1x1 projection
-    (ultralytics Attention, attn_ratio 0.5: head_dim C / heads, key_dim head_dim / 2).
+def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0, W=None):
+    """The C2PSA attention block alone: input [1, C, H, W] (W = H by default) -> ReLU -> qkv
+    1x1, per-head q^T k * scale over H*W tokens, softmax, v attn^T, + depthwise 3x3
+    positional conv of v, 1x1 projection (ultralytics Attention, attn_ratio 0.5: head_dim
+    C / heads, key_dim head_dim / 2).
     Returns (plan path, FLOPs/image of the attention core: q^T k and v attn^T)."""
+    W = H if W is None else W
     pb = PlanBuilder(out_dir, seed=seed)
     # a ReLU first, so that the block reads an internal (channels-last) tensor as in the model
-    x = pb.unary(pb.input("images", [1, C, H, H]), UN_RELU)
+    x = pb.unary(pb.input("images", [1, C, H, W]), UN_RELU)
     pb.output(_attention(pb, x, heads))
-    N, hd = H * H, C // heads
+    N, hd = H * W, C // heads
     core = 2.0 * heads * N * N * (hd // 2) + 2.0 * heads * hd * N * N
     return pb.write(), core
+
+
+def gemm_plan(out_dir, M, N, K, b_dims=None, seed=0):
+    """One plan-level `gemm` node, C[M][N] = A[M][K] . B[K][N] (src/PlanModel.cpp:3935-3990):
+    A is an init [M, K], B the plan input with dims b_dims (numel K*N, any rank; default
+    [K, N]), C a [M, N] tensor.  A and B are drawn as scripts/kernel_check.py:34-38 draws
+    them (default_rng(seed).random, A first, then B, rounded to fp16).  onnx2plan never
+    emits this op; a hand-written plan may.  Returns (plan path, B as fp16 [K, N])."""
+    b_dims = list(b_dims) if b_dims is not None else [K, N]
+    if int(np.prod(b_dims)) != K * N:
+        raise ValueError("b_dims must hold K*N elements")
+    rng = np.random.default_rng(seed)
+    a = rng.random((M, K)).astype(np.float16)
+    b = rng.random((K, N)).astype(np.float16)
+    pb = PlanBuilder(out_dir, seed)
+    x = pb.input("b", b_dims)
+    w = pb.init(a.astype(np.float32), "a")
+    y = pb.tensor([M, N])
+    pb.node("gemm", [w, x], [y])
+    pb.flops += 2 * M * N * K
+    pb.output(y)
+    return pb.write(), b
 
 
 def conv1x1_config(out_dir, seed=0):

@@ -176,8 +176,9 @@ static int unary_to_canonical(int op)
  *   family 1 (conv1x1_gemv_f16, N == 1): fp32 accumulation, half(s) + half(b)
  *     in fp16, half(act), + half(res) (conv1x1.cl:170,186-196).
  *   family 2 (conv_general): fp32 accumulation with the bias preloaded,
- *     half(act(acc)) (conv_general.cl:27-47; canonical activation codes, see the
- *     note on legacy codes in the design notes). */
+ *     half(act(acc)) (conv_general.cl:27-47).  Activation codes are the canonical
+ *     ones onnx2plan emits (onnx2plan.py:138); conv_general.cl:43-46 itself reads
+ *     legacy codes (2 HardSwish, 3 ReLU). */
 void ivo_conv2d(const uint16_t *x, int Cin, int H, int W,
                 const uint16_t *w, int Cout, int K, int S, int P, int G,
                 const uint16_t *bias, const uint16_t *res,
@@ -194,7 +195,10 @@ void ivo_conv2d(const uint16_t *x, int Cin, int H, int W,
 #pragma omp for schedule(dynamic, 1)
     for (int co = 0; co < Cout; ++co) {
       const int g = co / cout_g;
-      for (long i = 0; i < HWo; ++i) acc[i] = 0.0f;
+      /* conv_general preloads the bias into its fp32 accumulator (conv_general.cl:27) */
+      const float b = bias ? ivo_h2f(bias[co]) : 0.0f;
+      const float acc0 = (mode == IVO_REF && family == 2) ? b : 0.0f;
+      for (long i = 0; i < HWo; ++i) acc[i] = acc0;
       for (int cl = 0; cl < cin_g; ++cl) {
         const int ci = g * cin_g + cl;
         const float *xp = xf + (size_t)ci * H * W;
@@ -221,7 +225,6 @@ void ivo_conv2d(const uint16_t *x, int Cin, int H, int W,
             }
           }
       }
-      const float b = bias ? ivo_h2f(bias[co]) : 0.0f;
       for (long i = 0; i < HWo; ++i) {
         const size_t oi = (size_t)co * HWo + i;
         float v;
@@ -230,7 +233,7 @@ void ivo_conv2d(const uint16_t *x, int Cin, int H, int W,
           v = rh(ivo_act(v, act));
           if (res) v = rh(v + ivo_h2f(res[oi]));
         } else if (mode == IVO_REF) {
-          v = rh(ivo_act(acc[i] + b, act));
+          v = rh(ivo_act(acc[i], act));
           if (res) v = rh(v + ivo_h2f(res[oi]));
         } else {
           v = ivo_act(acc[i] + b, act);

@@ -267,9 +267,14 @@ def run_node(p: Plan, n: Node, T: dict, mode: int) -> None:
         N = bd[-1]
         L.ivo_bmm(g(0), g(1), y, B0 * B1, M, K, N)
     elif op == "gemm":
-        ad, bd = p.dims[n.ins[0]], p.dims[n.ins[1]]
-        M, K, N = ad[-2], ad[-1], bd[-1]
-        L.ivo_bmm(g(0), g(1), y, 1, M, K, N)
+        # src/PlanModel.cpp:3935-3940: M = A.dims[0], K = A.dims[1], N = numel(B) / K (B of
+        # any rank); the kernel is gemm_f16 (kernels/gemm.cl:183-669), i.e. a 1x1 conv
+        # with W = A [M][K] and X = B [K][N] pixels, no bias, no activation (family 0).
+        ad = p.dims[n.ins[0]]
+        M, K = ad[0], ad[1]
+        N = p.numel(n.ins[1]) // K
+        a, b = g(0)[:M * K], g(1)[:K * N]
+        y[:] = conv2d(b, a, None, None, K, N, 1, M, 1, 1, 0, 1, N, 1, 0, mode, 0)
     else:
         raise RuntimeError(f"unknown op: {op}")
     T[out] = y

@@ -75,6 +75,53 @@ def test_model_parity(tmp_path, name, imgsz, batch):
     m.close()
 
 
+@pytest.mark.parametrize("name,imgsz,batch,check", [
+    ("yolov8n-pose", 640, 64, (0, 31, 63)),       # the timed configuration of the bench
+    ("yolo11n-pose", 640, 64, (0, 40, 63)),
+    ("mobilenetv3-small", 224, 256, (0, 128, 255)),
+])
+def test_timed_batch_plans(tmp_path, name, imgsz, batch, check):
+    """The plans the bench times, at their batch and flags (graph replay, asynchronous runs),
+    with the two-input protocol: frame 2's images `check` against the oracle (pose heads per
+    row group); every image of frame 2 again, bit for bit, from a run with the batch rotated
+    by 17 positions (kernels and tiles do not depend on where an image sits in the batch);
+    and the checked images run alone at batch 1 on the same model, where the planner picks
+    other kernels (split-K, no persistent or pipelined kernels), within fp32 summation noise."""
+    path, _ = pw.MODELS[name](str(tmp_path), seed=0, imgsz=imgsz)
+    p = O.Plan.load(path)
+    n_in, per = p.numel(p.input_name), p.numel(p.outputs[0])
+    print(f"{name}@{imgsz} batch {batch}: images {check}", flush=True)
+    m = ia.PlanModel(path, 0, batch, ia.IVH_FLAG_ASYNC)
+    m.setInput(_inputs(p, batch, 1), batch)
+    m.run(batch)
+    xb = _inputs(p, batch, 2)
+    m.setInput(xb, batch)
+    m.run(batch)
+    got = m.readOutput(0, batch).reshape(batch, per)
+    sel = np.concatenate([xb[i * n_in:(i + 1) * n_in] for i in check])
+    ref = O.run_plan(p, sel, len(check))[0].reshape(len(check), per)
+    for j, i in enumerate(check):
+        label = f"{name}@{imgsz} b{batch} image {i}"
+        if name.endswith("-pose"):
+            assert _pose_heads_ok(got[i], ref[j], 1, label)
+        else:
+            assert _model_ok(got[i], ref[j], label)
+    shift = 17
+    m.setInput(np.roll(xb.reshape(batch, n_in), shift, axis=0).ravel(), batch)
+    m.run(batch)
+    rolled = np.roll(m.readOutput(0, batch).reshape(batch, per), -shift, axis=0)
+    assert np.array_equal(rolled, got), "an image's result depends on its position in the batch"
+    for i in check:
+        m.setInput(xb[i * n_in:(i + 1) * n_in], 1)
+        m.run(1)
+        one = m.readOutput(0, 1)
+        mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(one), O.h2f(got[i]))
+        print(f"  image {i} alone vs in the batch: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e} "
+              f"bit-identical {np.array_equal(one, got[i])}")
+        assert mean_rel < 1e-3 and max_rel < 1e-2
+    m.close()
+
+
 def test_batch_and_replay_consistency(tmp_path):
     """Without split-K, image i of a batch equals the same image run alone (bit-exact); with
     split-K (batch-dependent K partitioning) it agrees within fp32 summation noise and is

@@ -608,3 +608,80 @@ def test_attention_fused(tmp_path, C, H, heads, batch):
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(nodes[0]))
     print(f"fused vs node by node: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
     assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+@pytest.mark.parametrize("H,W,fused", [(12, 30, True), (20, 24, False)])
+def test_attention_rectangular(tmp_path, H, W, fused):
+    """Non-square maps: 12x30 = 360 tokens (12 key blocks, fused) and 20x24 = 480 tokens
+    (more keys than the fused kernel holds: the planner keeps the four nodes), each against
+    the oracle and against the node-by-node plan."""
+    path, _ = pw.c2psa_attention(str(tmp_path), C=128, H=H, W=W, heads=2)
+    print(f"attention {H}x{W} fused {fused}", flush=True)
+    assert ("attention" in _kernels(path, 2)) == fused
+    got = _check_f32(path, 2, lo=-1.0, ref_mode=False)
+    _, _, nodes = _run(path, 2, lo=-1.0, flags=ia.IVH_FLAG_NO_FUSE_ATTN)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(nodes[0]))
+    print(f"fused vs node by node: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def test_attention_large_scores(tmp_path):
+    """Inputs in [-30, 30]: scores in the thousands, so exp(T - m) must take the difference
+    before the exponent (an fp32 rounding of m log2e alone would exceed fp16's half ulp); the
+    fused core against the node-by-node plan and the oracle."""
+    path, _ = pw.c2psa_attention(str(tmp_path), C=128, H=12, heads=2)
+    assert "attention" in _kernels(path, 2)
+    p, x, got = _run(path, 2, lo=-30.0, hi=30.0)
+    _, _, nodes = _run(path, 2, lo=-30.0, hi=30.0, flags=ia.IVH_FLAG_NO_FUSE_ATTN)
+    ref = O.run_plan(p, x, 2)[0].ravel()
+    g = O.h2f(got[0])
+    assert np.isfinite(g).all()
+    mean_rel, max_rel, _, _ = O.rel_errors(g, O.h2f(nodes[0]))
+    print(f"fused vs node by node: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+    # against the oracle at the model bar (scripts/model_check.py:25,196-201): a one-ulp
+    # difference of an fp16 score in the thousands moves exp(T - m) by tens of percent
+    mean_rel, max_rel, _, scale_rel = O.rel_errors(g, O.h2f(ref))
+    print(f"fused vs oracle: mean_rel={mean_rel:.2e} max_rel={max_rel:.2e} scale_rel={scale_rel:.2e}")
+    assert (mean_rel < 2e-2 and max_rel < 5e-2) or scale_rel < 5e-3
+
+
+@pytest.mark.parametrize("M,N,K,bdims", [
+    (6400, 64, 64, None),            # scripts/kernel_check.py:25-31, the reference's gemm shapes
+    (1600, 128, 128, None),
+    (400, 256, 256, None),
+    (1024, 1024, 1024, None),
+    (4096, 512, 512, None),
+    (48, 480, 64, [1, 64, 20, 24]),  # B of rank 4: N = numel(B) / K = 20*24
+])
+def test_gemm_op(tmp_path, M, N, K, bdims):
+    """The plan's gemm op, C[M][N] = A[M][K] . B[K][N] (src/PlanModel.cpp:3935-3990), at
+    batch 2: image 0 is kernel_check's own B (default_rng(0), A the init), checked against
+    kernel_check's reference (a.f32 @ b.f32 -> fp16) with its contract; both images against
+    the fp32 oracle and, where the fp16-accumulating restatement is cheap, the
+    reference-rounding oracle."""
+    path, b = pw.gemm_plan(str(tmp_path), M, N, K, b_dims=bdims)
+    p = O.Plan.load(path)
+    a = O.h2f(next(iter(p.inits.values()))).reshape(M, K)
+    x1 = O.f2h(np.random.default_rng(7).random(K * N).astype(np.float32))
+    x = np.concatenate([b.view(np.uint16).ravel(), x1])
+    print(f"gemm M {M} N {N} K {K} B dims {bdims or [K, N]} batch 2", flush=True)
+    m = ia.PlanModel(path, 0, 2)
+    m.setInput(x, 2)
+    m.run(2)
+    got = m.readOutput(0, 2).reshape(2, M * N)
+    m.close()
+    kc = (a @ b.astype(np.float32).reshape(K, N)).astype(np.float16).astype(np.float32).ravel()
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), kc)
+    print(f"   vs kernel_check reference mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < OP_MEAN and max_rel < OP_MAX
+    ref = O.run_plan(p, x, 2)[0]
+    for i in range(2):
+        mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[i]), O.h2f(ref[i]))
+        print(f"   image {i} vs f32 oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+        assert mean_rel < F32_MEAN and max_rel < F32_MAX
+    if M * N * K <= 30_000_000:
+        refr = O.run_plan(p, x[:K * N], 1, mode=O.REF)[0]
+        mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(refr[0]))
+        print(f"   vs reference-rounding oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+        assert mean_rel < OP_MEAN and max_rel < OP_MAX

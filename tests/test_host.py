@@ -239,6 +239,26 @@ def test_malformed_plans_raise(tmp_path, text, bins, msg):
         m.run(1)
 
 
+def test_gemm_op_dims_dry_run(tmp_path):
+    """The plan's gemm op takes M = A.dims[0], K = A.dims[1], N = numel(B) / K
+    (src/PlanModel.cpp:3935-3940): a rank-4 B [1, K, H, W] plans as an M x K x H*W product
+    (host bounds check included); an output whose numel is not M*N is rejected."""
+    path, _ = pw.gemm_plan(str(tmp_path), 48, 20 * 24, 64, b_dims=[1, 64, 20, 24])
+    m = ia.PlanModel(path, 0, 3, DRY)
+    m.run(3)
+    info = [m.nodeInfo(i) for i in range(m.nodeCount())]
+    g = next(i for i in info if i["op"] == "gemm")
+    assert g["flops"] == 2.0 * 48 * 64 * 480
+    m.close()
+    text = open(path).read().replace("tensor t2 48 480", "tensor t2 48 479")
+    assert text != open(path).read()
+    bad = tmp_path / "bad.plan"
+    bad.write_text(text)
+    with pytest.raises(RuntimeError, match="gemm output numel"):
+        m = ia.PlanModel(str(bad), 0, 1, DRY)
+        m.run(1)
+
+
 def test_batch_range_checked(plans):
     m = ia.PlanModel(plans("mobilenetv3-small")[0], 0, 2, DRY)
     with pytest.raises(RuntimeError, match="out of range"):
@@ -309,10 +329,19 @@ def test_cpp_headers_compile(tmp_path):
     src.write_text('#include "infvino_hip/HipBackend.hpp"\n'
                    'struct MI { std::string plan, device; };\n'
                    'int main() { MI m{"x.plan", "GPU.0"}; (void)sizeof(infvino_hip::HipBackend); '
-                   'if (0) { infvino_hip::HipBackend b(m); } return 0; }\n')
+                   'if (0) { infvino_hip::HipBackend b(m); infvino_hip::HipBackend c(m, true); '
+                   'infvino_hip::HipBackend d(m, false, 8); } return 0; }\n')
     r = subprocess.run(["g++", "-std=c++17", "-Wall", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+    # an int second argument (an older max_batch signature) does not compile
+    bad = tmp_path / "bad.cpp"
+    bad.write_text('#include "infvino_hip/HipBackend.hpp"\n'
+                   'struct MI { std::string plan, device; };\n'
+                   'int main() { MI m{"x.plan", "GPU.0"}; if (0) { infvino_hip::HipBackend b(m, 4); } return 0; }\n')
+    r = subprocess.run(["g++", "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), str(bad)],
+                       capture_output=True, text=True)
+    assert r.returncode != 0 and "deleted" in r.stderr, r.stderr
 
 
 def test_py_backend_image_slicing():
@@ -369,6 +398,23 @@ def test_launch_plans_per_batch(plans):
     m.run(1)
     k2 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
     assert k1 == k2
+    m.close()
+
+
+def test_labels_follow_last_batch(plans):
+    """Kernel labels describe the batch of the last run: YOLOv8n-pose at 640 splits K at
+    batch 1 (grids too small to fill the chip) and not at batch 64, and the pipelined 3x3
+    kernel runs only at batch 64."""
+    m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
+    m.run(64)
+    k64 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    t64 = [m.nodeTag(i) for i in range(m.nodeCount())]
+    m.run(1)
+    k1 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
+    assert "conv_igemm_sk" in k1 and "conv_igemm_sk" not in k64
+    assert "conv_pipe" in k64 and "conv_pipe" not in k1
+    m.run(64)
+    assert [m.nodeTag(i) for i in range(m.nodeCount())] == t64
     m.close()
 
 

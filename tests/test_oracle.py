@@ -406,3 +406,63 @@ def test_ew_unary_code_table():
         if code in (2, 4, 9):
             assert ulps.max() == 0, code
         assert (ulps == 0).mean() > 0.99, code
+
+
+# ------------------------------------------------------------------ plan-level gemm and REF families
+
+def test_gemm_op_dims_rule(tmp_path):
+    """The plan's gemm op (src/PlanModel.cpp:3935-3940): M = A.dims[0], K = A.dims[1],
+    N = numel(B) / K, so a rank-4 B [1, K, H, W] is a [K][H*W] matrix.  A non-square A and
+    a B whose last dim is not N make each plausible slip fail: N taken from B.dims[-1] (4,
+    not 12), M and K swapped, or A read transposed."""
+    from infvino_amd import planwriter as pw
+    M, K, H, W = 5, 7, 3, 4
+    path, b = pw.gemm_plan(str(tmp_path), M, H * W, K, b_dims=[1, K, H, W], seed=2)
+    p = O.Plan.load(path)
+    a = O.h2f(next(iter(p.inits.values()))).reshape(M, K)
+    y = O.h2f(O.run_plan(p, b.view(np.uint16).ravel(), 1)[0]).reshape(M, H * W)
+    want = a.astype(np.float64) @ b.astype(np.float64).reshape(K, H * W)
+    np.testing.assert_allclose(y, want, rtol=2 ** -10, atol=1e-6)
+    # the same product with the default [K, N] B is identical
+    path2, b2 = pw.gemm_plan(str(tmp_path / "k"), M, H * W, K, seed=2)
+    assert np.array_equal(b2, b)
+    y2 = O.run_plan(O.Plan.load(path2), b2.view(np.uint16).ravel(), 1)[0]
+    assert np.array_equal(O.h2f(y2).reshape(M, H * W), y)
+
+
+def test_ref_family1_gemv_closed_forms():
+    """Family 1 (conv1x1_gemv_f16, conv1x1.cl:170-196): fp32 accumulation, then (half)s,
+    then + bias in fp16.  x = [2048, 1, 1] . 1 sums to 2050 exactly in fp32 (fp16
+    accumulation, family 0, would stay at 2048); x = [1024, 1024, 1] with bias 1: s = 2049
+    rounds to 2048 before the bias is added, and 2048 + 1 rounds to 2048 again (one
+    rounding of s + b, the fp32 mode, gives 2050)."""
+    w = O.f2h(np.ones(3, np.float32))
+    def run(xv, bv, mode, fam):
+        x = O.f2h(np.array(xv, np.float32))
+        b = O.f2h(np.array([bv], np.float32))
+        return float(O.h2f(O.conv2d(x, w, b, None, 3, 1, 1, 1, 1, 1, 0, 1, 1, 1, 0, mode, fam))[0])
+    assert run([2048, 1, 1], 0, O.REF, 1) == 2050.0
+    assert run([2048, 1, 1], 0, O.REF, 0) == 2048.0
+    assert run([1024, 1024, 1], 1, O.REF, 1) == 2048.0
+    assert run([1024, 1024, 1], 1, O.F32, 1) == 2050.0
+
+
+def test_ref_family2_conv_general_bias_preload():
+    """Family 2 (conv_general.cl:27-47) starts its fp32 accumulator at the bias.  With bias
+    2048 and terms 1, 2^-13, 2^-13 the tiny terms vanish one by one (2049 + 2^-13 is a tie
+    that rounds back to 2049) and half(2049) = 2048; adding the bias last (fp32 mode) keeps
+    them: 2049 + 2^-12 rounds to 2050.  With a zero bias both modes agree bit for bit."""
+    w = O.f2h(np.ones(3, np.float32))
+    x = O.f2h(np.array([1.0, 2.0 ** -13, 2.0 ** -13], np.float32))
+    b = O.f2h(np.array([2048.0], np.float32))
+    ref = O.h2f(O.conv2d(x, w, b, None, 3, 1, 1, 1, 1, 1, 0, 1, 1, 1, 0, O.REF, 2))[0]
+    f32 = O.h2f(O.conv2d(x, w, b, None, 3, 1, 1, 1, 1, 1, 0, 1, 1, 1, 0, O.F32, 2))[0]
+    assert ref == 2048.0 and f32 == 2050.0
+    rng = np.random.default_rng(5)
+    xs = O.f2h(rng.normal(0, 1, 8 * 9 * 9).astype(np.float32))
+    ws = O.f2h(rng.normal(0, 0.3, 8 * 1 * 9).astype(np.float32))
+    zero = O.f2h(np.zeros(8, np.float32))
+    for act in (0, 1, 3):
+        a = O.conv2d(xs, ws, zero, None, 8, 9, 9, 8, 3, 1, 1, 8, 9, 9, act, O.REF, 2)
+        c = O.conv2d(xs, ws, zero, None, 8, 9, 9, 8, 3, 1, 1, 8, 9, 9, act, O.F32, 2)
+        assert np.array_equal(a, c), act

@@ -45,3 +45,40 @@ def test_set_input_f32_noalloc_matches(tmp_path):
     big = np.zeros(n * 4, np.float32)
     assert L.ivh_set_input_f32_noalloc(m._h, big.ctypes.data_as(C.c_void_p), 4) != 0
     m.close()
+
+
+def test_set_input_f32_noalloc_two_models_threads(tmp_path):
+    """Two models on one GPU converting in alternation from two threads (ctypes releases the
+    GIL, so the calls overlap): the per-device lock keeps each model's input bit-identical to
+    the reference truncation of its own data."""
+    import threading
+    n = 3 * 1024 * 1024
+    path = tmp_path / "io.plan"
+    path.write_text(f"input x 1 3 1024 1024\ntensor y 1 3 1024 1024\nnode ew_unary x y op=2 n={n}\noutput y\n")
+    L = ia.lib()
+    models = [ia.PlanModel(str(path), 0, 2) for _ in range(2)]
+    data = [_inputs(n, 2, 10 + k) for k in range(2)]
+    want = [O.f2h_trunc(d) for d in data]
+    errors = []
+
+    def worker(k):
+        try:
+            for it in range(6):
+                rc = L.ivh_set_input_f32_noalloc(models[k]._h, data[k].ctypes.data_as(C.c_void_p), 2)
+                if rc != 0:
+                    errors.append((k, it, L.ivh_last_error()))
+                    return
+                if not np.array_equal(models[k].readTensor("x", 2), want[k]):
+                    errors.append((k, it, "mismatch"))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((k, -1, repr(e)))
+
+    ts = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    for m in models:
+        m.close()
+    assert not any(t.is_alive() for t in ts)
+    assert not errors, errors
