@@ -5,6 +5,8 @@
 // bmm and ops.cl:181-197 softmax in the reference):
 //   S = q^T k          bmm, per head [N x kd] x [kd x N], fp32 accumulation, fp16 store
 //   T = S * scale      ew_binary mul by a scalar init, fp32, fp16 store
+// (ultralytics 8.4 exports scale q^T instead, before the product: T = (q^T scale) k; the
+// kernel takes either form, AttnParams::scale_q)
 //   P = softmax(T)     over the last axis: m = max, s = sum exp(T - m), fp16(exp(T - m) / s)
 //   O = v P^T          bmm, per head [hd x N] x [N x N]^T, fp32 accumulation, fp16 store
 // which moves the N x N score matrix through HBM five times.  Here one work-group owns an
@@ -93,24 +95,30 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
     const int e = tid + 256 * i, d = e / (NP / 8), j = (e - d * (NP / 8)) * 8;
     if (e < VPC) *reinterpret_cast<h8 *>(Vs + d * VP + j) = vr[i];
   }
+  // scale_q: the plan multiplies q^T by the scale (an ew_binary node: fp32 product, fp16
+  // store) before the product; the product of two fp16 values is exact in fp32, so one fp16
+  // multiply rounds it the same way
+  const _Float16 sc16 = (_Float16)a.scale;  // an fp16 value (the plan's init)
+  const h2v sc2 = {sc16, sc16};
+  const h2v qs2 = a.scale_q ? sc2 : h2v{(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
   for (int i = 0; i < QI; ++i) {
     const int e = tid + 256 * i, c = e % (KD / 2), qi = (e / (KD / 2)) * 8;
     if (e < QPC) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) *reinterpret_cast<h2v *>(Qt + (qi + t) * KTP + 2 * c) = h2v{qr[i][0][t], qr[i][1][t]};
+      for (int t = 0; t < 8; ++t)
+        *reinterpret_cast<h2v *>(Qt + (qi + t) * KTP + 2 * c) = h2v{qr[i][0][t], qr[i][1][t]} * qs2;
     }
   }
   __syncthreads();
   const int qw = q0 + wave * 32;  // this wave's first query
   if (qw >= N) return;            // no barrier follows
 
-  // ---- T^T = fp16(fp16(k^T q) * scale), one query per lane (column), 16 keys per block.
-  // The product of two fp16 values is exact in fp32, so one packed fp16 multiply rounds it
-  // exactly as the ew_binary node (fp32 multiply, fp16 store) does.
+  // ---- T^T = fp16(fp16(k^T q) * scale) (or fp16(k^T q) of the scaled q), one query per lane
+  // (column), 16 keys per block.  One packed fp16 multiply rounds the exact product as the
+  // ew_binary node (fp32 multiply, fp16 store) does.
   const int nb = (N + 31) / 32;
-  const _Float16 sc16 = (_Float16)a.scale;  // an fp16 value (the plan's init)
-  const h2v sc2 = {sc16, sc16};
+  const h2v ss2 = a.scale_q ? h2v{(_Float16)1.0f, (_Float16)1.0f} : sc2;
   const _Float16 ninf = (_Float16)(-__builtin_inff());
   const int hi = lane >> 5;
   h2v T[NB][8];  // (keys of v = 2j, 2j + 1) of each block: scores, then probabilities
@@ -132,7 +140,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnParams a)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const h2v s2 = {(_Float16)acc[2 * j], (_Float16)acc[2 * j + 1]};
-      h2v t2 = s2 * sc2;
+      h2v t2 = s2 * ss2;
       if (tail) {
         if (kb * 32 + F::row(lane, 2 * j) >= N) t2[0] = ninf;
         if (kb * 32 + F::row(lane, 2 * j + 1) >= N) t2[1] = ninf;

@@ -313,14 +313,21 @@ void Model::fuseResidual()
 }
 
 // Attention core -> one fused node.  After fusePermuteMatmul, ultralytics' Attention reads
+// in one of two export forms:
 //   S = bmm(q, k; ta)  [h][kd][N]^T x [h][kd][N] -> [h][N][N]
 //   T = ew_binary mul (S, scalar init)
+// or (ultralytics 8.4 exports, the reference's plans: the scale on q^T before the product)
+//   q' = permute_0213 mode 1 (q)        [h][kd][N] -> [h][N][kd]
+//   q" = ew_binary mul (q', scalar init)
+//   T = bmm(q", k)
+// then in both
 //   P = softmax_axis (T) over the last axis
 //   O = bmm(v, P; tb)  [h][hd][N] x [h][N][N]^T -> [h][hd][N]
-// each intermediate with that single reader; the four become node "attention" (q, k, v ->
-// O) with the scale's fp16 bits, run by attn_kernel (attention.hip), which keeps every
-// node's fp16 rounding.  kd 32, hd 64, N a multiple of 8 up to kAttnMaxN; anything else
-// stays node by node (as does everything with IVH_FLAG_NO_FUSE_ATTN).
+// each intermediate with that single reader; the nodes become node "attention" (q, k, v ->
+// O) with the scale's fp16 bits and where it applies (scale_q), run by attn_kernel
+// (attention.hip), which keeps every node's fp16 rounding.  kd 32, hd 64, N a multiple of 8
+// up to the kernel's limit; anything else stays node by node (as does everything with
+// IVH_FLAG_NO_FUSE_ATTN).
 void Model::fuseAttention()
 {
   if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_ATTN)) return;
@@ -349,16 +356,44 @@ void Model::fuseAttention()
   };
   std::vector<char> remove(nodes_.size(), 0);
   std::map<int, PlanNode> replace;
+  // a scalar multiply by a one-value init; the other operand's name in `x`
+  auto scalar_mul = [&](const PlanNode & e, const std::string & x, std::string & sc) {
+    if (e.op != "ew_binary" || e.i("op") != 2 || e.ins.size() < 2 || (e.ins[0] != x && e.ins[1] != x)) return false;
+    sc = e.ins[0] == x ? e.ins[1] : e.ins[0];
+    return T_.count(sc) && T_.at(sc)->kind == Tensor::kInit && T_.at(sc)->numel == 1;
+  };
   for (size_t i = 0; i < nodes_.size(); ++i) {
     const PlanNode & m1 = nodes_[i];
-    if (m1.op != "bmm" || m1.ins.size() < 2 || m1.i("ta") != 1 || m1.i("tb") == 1 || remove[i]) continue;
-    const int ie = sole_reader(m1.outs[0]);
-    if (ie < 0) continue;
-    const PlanNode & e = nodes_[ie];
-    if (e.op != "ew_binary" || e.i("op") != 2 || e.ins.size() < 2) continue;
-    const std::string sc = e.ins[0] == m1.outs[0] ? e.ins[1] : e.ins[0];
-    if (T_.count(sc) == 0 || T_.at(sc)->kind != Tensor::kInit || T_.at(sc)->numel != 1) continue;
-    const int is = sole_reader(e.outs[0]);
+    if (m1.op != "bmm" || m1.ins.size() < 2 || m1.i("tb") == 1 || remove[i]) continue;
+    std::string sc, q;
+    int is = -1, scale_q = 0;
+    std::vector<int> extra;  // the scale (and permute) nodes folded in
+    if (m1.i("ta") == 1) {   // S = q^T k, then T = S * scale
+      const int ie = sole_reader(m1.outs[0]);
+      if (ie < 0 || !scalar_mul(nodes_[ie], m1.outs[0], sc)) continue;
+      is = sole_reader(nodes_[ie].outs[0]);
+      q = m1.ins[0];
+      extra = {ie};
+    } else {                 // T = (q^T * scale) k
+      auto pe = producer.find(m1.ins[0]);
+      if (pe == producer.end() || sole_reader(m1.ins[0]) != (int)i) continue;
+      const PlanNode & e = nodes_[pe->second];
+      if (e.ins.size() < 2) continue;
+      const std::string qt = T_.at(e.ins[0])->kind == Tensor::kInit ? e.ins[1] : e.ins[0];
+      if (!scalar_mul(e, qt, sc)) continue;
+      auto pp = producer.find(qt);
+      if (pp == producer.end() || sole_reader(qt) != pe->second) continue;
+      const PlanNode & pm = nodes_[pp->second];
+      if (pm.op != "permute_0213" || pm.i("mode") != 1 || pm.ins.empty()) continue;
+      const auto & qd = T_.at(pm.ins[0])->dims;
+      const auto & td = T_.at(qt)->dims;
+      if (qd.size() < 2 || td.size() != qd.size() || qd.back() != td[td.size() - 2] || td.back() != qd[qd.size() - 2])
+        continue;
+      q = pm.ins[0];
+      is = sole_reader(m1.outs[0]);
+      scale_q = 1;
+      extra = {pe->second, pp->second};
+    }
     if (is < 0) continue;
     const PlanNode & sm = nodes_[is];
     if (sm.op != "softmax_axis" || sm.i("inner", 1) != 1) continue;
@@ -367,7 +402,7 @@ void Model::fuseAttention()
     const PlanNode & m2 = nodes_[i2];
     if (m2.op != "bmm" || m2.ins.size() < 2 || m2.i("tb") != 1 || m2.i("ta") == 1 || m2.ins[1] != sm.outs[0]) continue;
     int64_t hq, kd, n, hk, kd2, nk, hv, hd, nv, ho, hd2, no, hs, ns1, ns2;
-    if (!dims3(m1.ins[0], hq, kd, n) || !dims3(m1.ins[1], hk, kd2, nk) || !dims3(m2.ins[0], hv, hd, nv) ||
+    if (!dims3(q, hq, kd, n) || !dims3(m1.ins[1], hk, kd2, nk) || !dims3(m2.ins[0], hv, hd, nv) ||
         !dims3(m2.outs[0], ho, hd2, no) || !dims3(sm.outs[0], hs, ns1, ns2))
       continue;
     if (kd != kAttnKD || kd2 != kd || hd != kAttnHD || hd2 != hd || nk != n || nv != n || no != n || ns1 != n ||
@@ -382,12 +417,14 @@ void Model::fuseAttention()
     }
     PlanNode fz;
     fz.op = "attention";
-    fz.ins = {m1.ins[0], m1.ins[1], m2.ins[0]};
+    fz.ins = {q, m1.ins[1], m2.ins[0]};
     fz.outs = {m2.outs[0]};
     fz.attr["heads"] = std::to_string(hq);
     fz.attr["n"] = std::to_string(n);
     fz.attr["scale_bits"] = std::to_string(bits);
-    remove[i] = remove[ie] = remove[is] = 1;
+    fz.attr["scale_q"] = std::to_string(scale_q);
+    remove[i] = remove[is] = 1;
+    for (int x : extra) remove[x] = 1;
     replace[i2] = fz;
   }
   std::vector<PlanNode> kept;
@@ -475,15 +512,20 @@ void Model::fusePermuteMatmul()
 
 // ============================================================= decode-tail fusion
 
-// The export form of a Detect / Pose head's decode (ultralytics head.py Detect._inference,
-// Pose.kpts_decode) as a plan holds it:
-//   box+cls per scale [4R + nc, H, W] -> reshape, concat over anchors -> copy_c box rows ->
-//   reshape [4, R, A] -> permute_0213 -> softmax over the R bins -> conv1x1 with the bin
-//   weights (DFL) -> copy_c lt / rb -> anchors - lt, anchors + rb -> centre = sum / 2 (or
-//   * 0.5), size = x2y2 - x1y1 -> concat -> * strides;  copy_c class rows -> sigmoid;
+// The export form of a Detect / Pose head's decode (ultralytics head.py Detect decode,
+// Pose.kpts_decode) as a plan holds it, in either of two export forms:
+//   ultralytics 8.4 (the reference's plans): box distributions per scale [4R, H, W] and class
+//   scores per scale [nc, H, W], each reshaped and concatenated over the anchors on its own;
+//   older exports: box + classes per scale [4R + nc, H, W] -> one concat over the anchors ->
+//   copy_c box rows / class rows;
+// then box rows -> reshape [4, R, A] -> permute_0213 -> softmax over the R bins -> conv1x1
+//   with the bin weights (DFL) -> lt / rb (slice_axis, or copy_c in older exports) ->
+//   anchors - lt, anchors + rb -> centre = sum / 2 (or * 0.5), size = x2y2 - x1y1 -> concat
+//   -> * strides;  class rows -> sigmoid;
 //   keypoints per scale [3 nk, H, W] -> concat over anchors -> slice xy -> * 2 + (anchors -
 //   0.5) -> * strides; slice visibility -> sigmoid -> concat [nk, 3, A];
-//   output = concat [box (4), classes (nc), keypoints (3 nk)] over A anchors.
+//   output = concat [box (4), classes (nc), keypoints (3 nk)] over A anchors (one three-way
+//   concat, or two nested concats in older exports).
 // About 35 nodes, each streaming the anchors through memory, become one "pose_decode" node
 // whose kernel reads each head pixel once and writes the output once, rounding to fp16
 // after every step where a node would have stored its result.  The match runs from each
@@ -504,8 +546,8 @@ void Model::fuseDecode()
 
   struct Match {
     std::set<int> region;
-    std::vector<std::string> X, K;  // per-scale head tensors
-    std::vector<int> hw;            // pixels per scale
+    std::vector<std::string> X, C, K;  // per-scale head tensors (C: separate class scores)
+    std::vector<int> hw;               // pixels per scale
     std::string wd, anc, st, ancm, cbox, ckpt;
     int R = 0, nc = 0, nk = 0, box_div = 1;
   };
@@ -610,11 +652,22 @@ void Model::fuseDecode()
       if (m.hw.empty()) m.hw = hw;
       return m.hw == hw;
     };
-    // concat [dbox * strides (4), sigmoid(classes) (nc)] over A anchors
-    auto box = [&](const PlanNode * x) -> bool {
-      if (!x || x->ins.size() < 2 || x->i("ca") != 4 || x->i("cb") < 1 || !concat2(x, 1, A, 4, x->i("cb"))) return false;
-      m.nc = x->i("cb");
-      const PlanNode * bx = take(x->ins[0], "ew_binary");
+    // lt (c0 = 0) / rb (c0 = 2) rows of the [4, A] DFL distances: a Slice over axis 1
+    // (slice_axis) or, in older exports, a channel copy
+    auto dist_rows = [&](const std::string & t, int c0) -> const PlanNode * {
+      const PlanNode * n = peek(t);
+      if (n && n->op == "slice_axis") {
+        n = take(t, "slice_axis");
+        const bool ok = n && n->i("outer", 1) == 1 && n->i("axdim") == 4 && n->i("inner", 1) == A &&
+                        n->i("start") == c0 && n->i("len") == 2;
+        return ok ? n : nullptr;
+      }
+      n = take(t, "copy_c");
+      return copy_rows(n, c0, 2) ? n : nullptr;
+    };
+    // [dbox * strides (4), sigmoid(classes) (nc)]: the first two inputs of the output concat
+    auto box = [&](const std::string & dbox_t, const std::string & cls_t) -> bool {
+      const PlanNode * bx = take(dbox_t, "ew_binary");
       if (!bx || !init_n(bx->ins.at(1), A) || !ew(bx, 2, 4 * A, id, [A](long i) { return i % A; })) return false;
       m.st = bx->ins[1];
       const PlanNode * db = take(bx->ins[0], "concat4");
@@ -635,9 +688,9 @@ void Model::fuseDecode()
       m.anc = n1->ins[0];
       const std::string rbt = n2->ins[0] == m.anc ? n2->ins[1] : (n2->ins[1] == m.anc ? n2->ins[0] : std::string());
       if (rbt.empty() || rbt == m.anc) return false;
-      const PlanNode * lt = take(n1->ins[1], "copy_c");
-      const PlanNode * rb = take(rbt, "copy_c");
-      if (!copy_rows(lt, 0, 2) || !copy_rows(rb, 2, 2) || lt->ins[0] != rb->ins[0] || !act_n(lt->ins[0], 4 * A)) return false;
+      const PlanNode * lt = dist_rows(n1->ins[1], 0);
+      const PlanNode * rb = dist_rows(rbt, 2);
+      if (!lt || !rb || lt->ins[0] != rb->ins[0] || !act_n(lt->ins[0], 4 * A)) return false;
       const PlanNode * cv = take(unreshape(lt->ins[0]), "conv1x1");
       if (!cv || cv->ins.size() < 2 || cv->i("act") != 0) return false;
       if ((cv->ins.size() > 2 && cv->ins[2] != "-") || (cv->ins.size() > 3 && cv->ins[3] != "-")) return false;
@@ -650,12 +703,18 @@ void Model::fuseDecode()
       if (!sm || sm->i("outer", 1) != 1 || sm->i("axdim") != m.R || sm->i("inner", 1) != 4 * A) return false;
       const PlanNode * pm = take(sm->ins[0], "permute_0213");
       if (!pm || pm->i("mode") != 0 || pm->i("D1", 1) != 4 || pm->i("D2", 1) != m.R || pm->i("I", 1) != A) return false;
-      const PlanNode * bsl = take(unreshape(pm->ins[0]), "copy_c");
+      const PlanNode * sg = sigmoid_of(cls_t);
+      if (!sg || !act_n(cls_t, (long)m.nc * A) || !act_n(sg->ins[0], (long)m.nc * A)) return false;
+      const std::string bsrc = unreshape(pm->ins[0]);
+      const PlanNode * bp = peek(bsrc);
+      if (bp && bp->op == "concat4") {  // separate box and class concats over the anchors
+        const PlanNode * cp = peek(sg->ins[0]);
+        return cp && cp->op == "concat4" && scales(bsrc, 4 * m.R, m.X) && scales(sg->ins[0], m.nc, m.C);
+      }
+      const PlanNode * bsl = take(bsrc, "copy_c");  // one [4R + nc, A] concat, rows copied out
       if (!copy_rows(bsl, 0, 4 * m.R)) return false;
-      const PlanNode * sg = sigmoid_of(x->ins[1]);
-      const PlanNode * csl = sg ? take(sg->ins[0], "copy_c") : nullptr;
+      const PlanNode * csl = take(sg->ins[0], "copy_c");
       if (!copy_rows(csl, 4 * m.R, m.nc) || csl->ins[0] != bsl->ins[0]) return false;
-      if (!act_n(x->ins[1], (long)m.nc * A) || !act_n(sg->ins[0], (long)m.nc * A)) return false;
       return scales(bsl->ins[0], 4 * m.R + m.nc, m.X);
     };
     // [nk, 3, A] = concat [(xy * 2 + (anchors - 0.5)) * strides, sigmoid(visibility)]
@@ -693,17 +752,28 @@ void Model::fuseDecode()
       if (fin && fin->i("outer", 1) == 1 && fin->ins.size() >= 2) {
         A = fin->i("inner", 1);
         const PlanNode * first = peek(fin->ins[0]);
-        if (A > 0 && first && first->op == "concat4") {  // pose: [box + classes, keypoints]
-          ok = box(take(fin->ins[0], "concat4")) && keypoints(fin->ins[1]) &&
+        if (A > 0 && first && first->op == "concat4" && first->i("ca") == 4 && first->i("cb") >= 1) {
+          // pose, two nested concats: [[box, classes], keypoints]
+          const PlanNode * bc = take(fin->ins[0], "concat4");
+          m.nc = bc->i("cb");
+          ok = concat2(bc, 1, A, 4, m.nc) && box(bc->ins[0], bc->ins[1]) && keypoints(fin->ins[1]) &&
                concat2(fin, 1, A, 4 + m.nc, 3 * m.nk) && act_n(fin->ins[1], 3L * m.nk * A);
-        } else if (A > 0) {                               // detect: box + classes only
-          ok = box(fin);
+        } else if (A > 0 && fin->ins.size() >= 3 && fin->i("cc") > 0) {
+          // pose, one concat: [box, classes, keypoints]
+          m.nc = fin->i("cb");
+          ok = fin->i("ca") == 4 && m.nc >= 1 && fin->i("cd") == 0 && box(fin->ins[0], fin->ins[1]) &&
+               keypoints(fin->ins[2]) && fin->i("cc") == 3 * m.nk && act_n(fin->ins[2], 3L * m.nk * A);
+        } else if (A > 0) {  // detect: box + classes only
+          m.nc = fin->i("cb");
+          ok = concat2(fin, 1, A, 4, m.nc) && m.nc >= 1 && box(fin->ins[0], fin->ins[1]);
         }
       }
     } catch (const std::exception &) {
       ok = false;
     }
-    if (!ok || m.X.size() > 4 || m.X.empty() || (m.nk && m.K.size() != m.X.size())) continue;
+    if (!ok || m.X.size() > 4 || m.X.empty() || (m.nk && m.K.size() != m.X.size()) ||
+        (!m.C.empty() && m.C.size() != m.X.size()))
+      continue;
     // nothing outside the region may read what the region computes
     for (int ni : m.region)
       for (const auto & o : nodes_[ni].outs) {
@@ -717,6 +787,7 @@ void Model::fuseDecode()
     PlanNode f;
     f.op = "pose_decode";
     f.ins = m.X;
+    f.ins.insert(f.ins.end(), m.C.begin(), m.C.end());
     if (m.nk) f.ins.insert(f.ins.end(), m.K.begin(), m.K.end());
     for (const std::string & s : {m.wd, m.anc, m.st, m.nk ? m.ancm : std::string("-"), m.cbox,
                                   m.nk ? m.ckpt : std::string("-")})
@@ -728,6 +799,7 @@ void Model::fuseDecode()
     f.attr["nk"] = std::to_string(m.nk);
     f.attr["A"] = std::to_string(A);
     f.attr["box_div"] = std::to_string(m.box_div);
+    f.attr["split"] = m.C.empty() ? "0" : "1";
     for (size_t s = 0; s < m.hw.size(); ++s) f.attr["hw" + std::to_string(s)] = std::to_string(m.hw[s]);
     const int last = *m.region.rbegin();
     std::vector<PlanNode> kept;
@@ -1431,6 +1503,7 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
     a.heads = n.i("heads");
     a.n = n.i("n");
     a.scale = h2f((uint16_t)n.i("scale_bits"));
+    a.scale_q = n.i("scale_q");
     a.q = view(n.ins.at(0), batch);
     a.k = view(n.ins.at(1), batch);
     a.v = view(n.ins.at(2), batch);
@@ -1459,9 +1532,12 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
     d.nk = n.i("nk");
     d.A = n.i("A");
     d.box_div = n.i("box_div");
+    const int split = n.i("split");
     if (d.nscale < 1 || d.nscale > 4 || d.R < 1 || d.R > 64 || d.nc < 1 || d.nk < 0 || d.A < 1) fail("decode attributes");
-    const int no = 4 * d.R + d.nc, nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
-    const size_t base = (size_t)d.nscale * (d.nk ? 2 : 1);
+    // per scale: box (4R) + classes (nc) in one tensor, or (split) box and classes apart
+    const int no = 4 * d.R + (split ? 0 : d.nc), nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
+    const size_t base = (size_t)d.nscale * (1 + (split ? 1 : 0) + (d.nk ? 1 : 0));
+    const size_t kfirst = (size_t)d.nscale * (split ? 2 : 1);
     if (n.ins.size() != base + 6) fail("decode inputs");
     // the heads stay NCHW (the decode is no channels-last reader): per-channel reads are
     // coalesced and the narrow head convs (1 or 51 channels) write NCHW rows faster
@@ -1474,8 +1550,17 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
       if (xt.C != no || (long)xt.H * xt.W != hw || xt.numel != no * hw) fail("decode head geometry");
       d.x[s] = view(xt.name, batch);
       if (d.x[s].layout != kNCHW) d.nchw = 0;
+      if (split) {
+        const Tensor & ct = *T_.at(n.ins[d.nscale + s]);
+        if (ct.C != d.nc || (long)ct.H * ct.W != hw || ct.numel != (long)d.nc * hw) fail("decode class geometry");
+        d.c[s] = view(ct.name, batch);
+        if (d.c[s].layout != kNCHW) d.nchw = 0;
+      } else {  // the class channels follow the 4R box channels of the same tensor
+        d.c[s] = d.x[s];
+        d.c[s].ptr = d.x[s].ptr + (d.x[s].layout == kNCHW ? (long)4 * d.R * d.x[s].cs : (long)4 * d.R);
+      }
       if (d.nk) {
-        const Tensor & kt = *T_.at(n.ins[d.nscale + s]);
+        const Tensor & kt = *T_.at(n.ins[kfirst + s]);
         if (kt.C != nkc || (long)kt.H * kt.W != hw || kt.numel != nkc * hw) fail("decode keypoint geometry");
         d.k[s] = view(kt.name, batch);
         if (d.k[s].layout != kNCHW) d.nchw = 0;
@@ -1862,11 +1947,12 @@ void Model::validate(const Launch & l) const
   if (l.kind == Launch::kDecode) {
     const DecodeParams & d = l.dp;
     if (d.batch < 1 || d.batch > 65535 || d.nscale < 1 || d.nscale > 4) throw std::runtime_error("decode grid");
-    const int no = 4 * d.R + d.nc, nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
+    const int nkc = 3 * d.nk, ny = 4 + d.nc + nkc;
     for (int s = 0; s < d.nscale; ++s) {
       const long hw = (s + 1 < d.nscale ? d.off[s + 1] : d.A) - d.off[s];
       if (hw < 1) throw std::runtime_error("decode scale offsets");
-      check(d.x[s].ptr, 0, vlast(d.x[s], d.batch, no, hw), 2, "decode head");
+      check(d.x[s].ptr, 0, vlast(d.x[s], d.batch, 4 * d.R, hw), 2, "decode head");
+      check(d.c[s].ptr, 0, vlast(d.c[s], d.batch, d.nc, hw), 2, "decode classes");
       if (d.nk) check(d.k[s].ptr, 0, vlast(d.k[s], d.batch, nkc, hw), 2, "decode keypoints");
     }
     check(d.dflw, 0, d.R - 1, 2, "decode bin weights");

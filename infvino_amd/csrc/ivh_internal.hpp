@@ -122,13 +122,15 @@ struct AttnParams {
   View q, k, v, y;
   int batch = 1, heads = 1, n = 0;
   float scale = 1.0f;
+  int scale_q = 0;  // 1: the scale multiplies q (rounded to fp16) before q^T k; 0: the scores
 };
 
 // Fused Detect / Pose head decode: per-scale head tensors in, [4 + nc + 3 nk][A] out per image
 // (the plan's decode tail, matched by the executor).  Anchor a of scale s is pixel a - off[s]
 // of that scale's tensors.
 struct DecodeParams {
-  View x[4];                      // per scale: box distributions (4R ch) + classes (nc ch)
+  View x[4];                      // per scale: box distributions (4R ch)
+  View c[4];                      // per scale: class scores (nc ch; may be x's channels 4R..)
   View k[4];                      // per scale: keypoints (3 nk ch; unused when nk == 0)
   View y;                         // [4 + nc + 3 nk][A], channel stride A
   const __half * dflw = nullptr;  // R bin weights of the DFL projection

@@ -1702,8 +1702,8 @@ __device__ __forceinline__ float hv(const __half * p, long i) { return (float)re
 
 // R_ / NC_ / NK_ > 0: compile-time channel counts (loops unroll, fx / fk index registers);
 // 0: the run-time counts in p.
-template <int R_, int NC_, int NK_, class FX, class FK>
-__device__ __forceinline__ void decode_anchor(const DecodeParams & p, int b, int a, FX && fx, FK && fk)
+template <int R_, int NC_, int NK_, class FX, class FC, class FK>
+__device__ __forceinline__ void decode_anchor(const DecodeParams & p, int b, int a, FX && fx, FC && fc, FK && fk)
 {
   const int R = R_ > 0 ? R_ : p.R, nc = NC_ > 0 ? NC_ : p.nc, nk = NK_ > 0 ? NK_ : p.nk;
   _Float16 * y = reinterpret_cast<_Float16 *>(p.y.ptr) + (long)b * p.y.img + a;
@@ -1733,7 +1733,7 @@ __device__ __forceinline__ void decode_anchor(const DecodeParams & p, int b, int
   y[2 * ys] = (_Float16)(rh(x2 - x1) * st);
   y[3 * ys] = (_Float16)(rh(y2 - y1) * st);
 #pragma unroll
-  for (int c = 0; c < nc; ++c) y[(4 + c) * ys] = (_Float16)act_f(fx(4 * R + c), kActSigmoid);
+  for (int c = 0; c < nc; ++c) y[(4 + c) * ys] = (_Float16)act_f(fc(c), kActSigmoid);
   if (nk > 0) {
     const float ck = hv(p.ckpt, 0), mx = hv(p.ancm, a), my = hv(p.ancm, (long)p.A + a);
     _Float16 * yk = y + (4 + nc) * ys;
@@ -1768,15 +1768,18 @@ __device__ __forceinline__ int decode_scale(const DecodeParams & p, int a)
 template <int R, int NC, int NK>
 __global__ void __launch_bounds__(256) pose_decode_nchw_kernel(const DecodeParams p)
 {
-  constexpr int NX = 4 * R + NC, NKC = 3 * NK;
+  constexpr int NX = 4 * R, NKC = 3 * NK;
   const int a = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
   if (a >= p.A) return;
   const int s = decode_scale(p, a), i = a - p.off[s];
-  const View xv = pick_view(p.x, s);
+  const View xv = pick_view(p.x, s), cv = pick_view(p.c, s);
   const _Float16 * xp = reinterpret_cast<const _Float16 *>(xv.ptr) + (long)b * xv.img + i;
-  _Float16 x[NX];
+  const _Float16 * cp = reinterpret_cast<const _Float16 *>(cv.ptr) + (long)b * cv.img + i;
+  _Float16 x[NX], cl[NC];
 #pragma unroll
   for (int c = 0; c < NX; ++c) x[c] = xp[(long)c * xv.cs];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) cl[c] = cp[(long)c * cv.cs];
   _Float16 k[NKC > 0 ? NKC : 1];
   if (NK > 0) {
     const View kv = pick_view(p.k, s);
@@ -1784,7 +1787,8 @@ __global__ void __launch_bounds__(256) pose_decode_nchw_kernel(const DecodeParam
 #pragma unroll
     for (int c = 0; c < NKC; ++c) k[c] = kp[(long)c * kv.cs];
   }
-  decode_anchor<R, NC, NK>(p, b, a, [&](int c) { return (float)x[c]; }, [&](int c) { return (float)k[c]; });
+  decode_anchor<R, NC, NK>(p, b, a, [&](int c) { return (float)x[c]; }, [&](int c) { return (float)cl[c]; },
+                           [&](int c) { return (float)k[c]; });
 }
 
 // any layout, run-time channel counts (decode_anchor's unroll requests cannot be met here)
@@ -1795,11 +1799,12 @@ __global__ void __launch_bounds__(256) pose_decode_kernel(const DecodeParams p)
   const int a = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
   if (a >= p.A) return;
   const int s = decode_scale(p, a), i = a - p.off[s];
-  const View xv = pick_view(p.x, s), kv = pick_view(p.k, s);
+  const View xv = pick_view(p.x, s), cv = pick_view(p.c, s), kv = pick_view(p.k, s);
   auto at = [&](const View & v, int c) {
     return hv(v.ptr, (long)b * v.img + (v.layout == kNHWC ? (long)i * v.cs + c : (long)c * v.cs + i));
   };
-  decode_anchor<0, 0, 0>(p, b, a, [&](int c) { return at(xv, c); }, [&](int c) { return at(kv, c); });
+  decode_anchor<0, 0, 0>(p, b, a, [&](int c) { return at(xv, c); }, [&](int c) { return at(cv, c); },
+                         [&](int c) { return at(kv, c); });
 }
 #pragma clang diagnostic pop
 }  // namespace

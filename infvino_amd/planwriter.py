@@ -311,27 +311,37 @@ def _anchors(sizes, strides):
     return np.concatenate(pts, 1).astype(np.float32), np.concatenate(st, 1)
 
 
-def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False):
-    """ultralytics Pose head in export form (Detect._inference + kpts_decode)."""
+def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False, legacy=False):
+    """ultralytics Pose head in export form (Detect decode + Pose.kpts_decode).
+
+    Default: the form of ultralytics 8.4 exports (requirements-export.txt pins 8.4.166), which
+    is what the reference's own lowered plans hold (config/tuning.json's signatures): the box
+    distributions, class scores and keypoints of the three scales are concatenated over the
+    anchors separately ([4R, A], [nc, A], [3 nk, A]); the DFL distances are split into lt / rb
+    by two Slice nodes (slice_axis); the output is one concat of the decoded boxes, the
+    sigmoid scores and the decoded keypoints.
+    legacy=True: the older export form, per scale box and class channels concatenated first,
+    one [4R + nc, A] concat over the anchors split by channel copies (copy_c), the output
+    built by two nested concats."""
     ch0 = pb.shapes[feats[0]][1]
     c2 = max(16, ch0 // 4, reg_max * 4)
     c3 = max(ch0, min(nc, 100))
-    nkk = nk[0] * nk[1]
+    nkk = nk[0] * nk[1] if nk else 0
     c4 = max(ch0 // 4, nkk)
     strides = [8, 16, 32]
     sizes = [tuple(pb.shapes[f][2:]) for f in feats]
     A = sum(h * w for h, w in sizes)
     # keypoint branch: cv4[i] -> view(bs, nk, -1) -> cat(-1)
     kp = []
-    for f in feats:
+    for f in feats if nkk else []:
         t = pb.conv(f, c4, 3)
         t = pb.conv(t, c4, 3)
         t = pb.conv(t, nkk, 1, act=ACT_NONE)
         _, _, h, w = pb.shapes[t]
         kp.append(pb.reshape(t, [1, nkk, h * w]))
-    kpt = _concat_many(pb, kp, axis=2)
-    # box/cls branches
-    xs = []
+    kpt = _concat_many(pb, kp, axis=2) if kp else None
+    # box / class branches
+    bs, cs = [], []
     for f in feats:
         b = pb.conv(f, c2, 3)
         b = pb.conv(b, c2, 3)
@@ -346,11 +356,17 @@ def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False):
             c = pb.conv(f, c3, 3)
             c = pb.conv(c, c3, 3)
         c = pb.conv(c, nc, 1, act=ACT_NONE)
-        xs.append(pb.concat([b, c]))
-    no = 4 * reg_max + nc
-    flat = [pb.reshape(x, [1, no, pb.shapes[x][2] * pb.shapes[x][3]]) for x in xs]
-    xcat = _concat_many(pb, flat, axis=2)
-    box, cls = pb.split(xcat, [4 * reg_max, nc])
+        bs.append(b)
+        cs.append(c)
+    flat = lambda x: pb.reshape(x, [1, pb.shapes[x][1], pb.shapes[x][2] * pb.shapes[x][3]])  # noqa: E731
+    if legacy:
+        no = 4 * reg_max + nc
+        xs = [pb.concat([b, c]) for b, c in zip(bs, cs)]
+        xcat = _concat_many(pb, [pb.reshape(x, [1, no, pb.shapes[x][2] * pb.shapes[x][3]]) for x in xs], axis=2)
+        box, cls = pb.split(xcat, [4 * reg_max, nc])
+    else:
+        box = _concat_many(pb, [flat(b) for b in bs], axis=2)   # [1, 4R, A]
+        cls = _concat_many(pb, [flat(c) for c in cs], axis=2)   # [1, nc, A]
     # DFL: view(b,4,16,a).transpose(2,1).softmax(1) -> conv 16->1 (arange weights)
     d = pb.reshape(box, [1, 4, reg_max, A])
     d = pb.permute(d, [0, 2, 1, 3])
@@ -360,7 +376,10 @@ def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False):
     d = pb.reshape(d, [1, 4, A])
     anc, strd = _anchors(sizes, strides)
     anc_c = pb.const(anc[None], "anchors")            # [1, 2, A]
-    lt, rb = pb.split(d, [2, 2])
+    if legacy:
+        lt, rb = pb.split(d, [2, 2])
+    else:
+        lt, rb = pb.slice(d, 1, 0, 2), pb.slice(d, 1, 2, 2)
     x1y1 = pb.binary(anc_c, lt, 1)
     x2y2 = pb.binary(anc_c, rb, 0)
     two = pb.const(np.array([2.0], np.float32), "two")
@@ -369,7 +388,9 @@ def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False):
     dbox = pb.concat([cxy, wh])
     st_c = pb.const(strd, "strides")                  # [1, A]
     dbox = pb.binary(dbox, st_c, 2)
-    x = pb.concat([dbox, pb.unary(cls, UN_SIGMOID)])
+    scores = pb.unary(cls, UN_SIGMOID)
+    if not nkk:
+        return pb.concat([dbox, scores])
     # kpts_decode (export): view(bs,17,3,-1); (y[:,:,:2]*2 + (anchors-0.5))*strides; sigmoid vis
     y = pb.reshape(kpt, [1, nk[0], nk[1], A])
     xy = pb.slice(y, 2, 0, 2)
@@ -379,7 +400,9 @@ def _pose_head(pb, feats, nc=1, nk=(17, 3), reg_max=16, dw_cls=False):
     vis = pb.unary(pb.slice(y, 2, 2, 1), UN_SIGMOID)
     a = pb.concat([xy, vis], axis=2)
     a = pb.reshape(a, [1, nkk, A])
-    return pb.concat([x, a])
+    if legacy:
+        return pb.concat([pb.concat([dbox, scores]), a])
+    return pb.concat([dbox, scores, a])
 
 
 def _concat_many(pb, xs, axis):
@@ -388,8 +411,9 @@ def _concat_many(pb, xs, axis):
     return pb.concat(xs, axis) if len(xs) > 1 else xs[0]
 
 
-def yolov8n_pose(out_dir, seed=0, imgsz=640):
-    """YOLOv8n-pose (ultralytics yolov8-pose.yaml, depth 0.33 width 0.25), 17x3 keypoints."""
+def yolov8n_pose(out_dir, seed=0, imgsz=640, legacy=False):
+    """YOLOv8n-pose (ultralytics yolov8-pose.yaml, depth 0.33 width 0.25), 17x3 keypoints.
+    legacy=True lowers the head in the older export form (see _pose_head)."""
     pb = PlanBuilder(out_dir, seed)
     x = pb.input("images", [1, 3, imgsz, imgsz])
     x = pb.conv(x, 16, 3, 2)             # 0
@@ -410,7 +434,7 @@ def yolov8n_pose(out_dir, seed=0, imgsz=640):
     o4 = _c2f(pb, x, 128, 1, False)              # 18
     x = pb.concat([pb.conv(o4, 128, 3, 2), p5])  # 19, 20
     o5 = _c2f(pb, x, 256, 1, False)              # 21
-    out = _pose_head(pb, [o3, o4, o5])
+    out = _pose_head(pb, [o3, o4, o5], legacy=legacy)
     pb.output(out)
     path = pb.write()
     return path, pb.flops
@@ -443,8 +467,13 @@ def _c3k2(pb, x, c2, n, c3k, shortcut=True, e=0.5):
     return pb.conv(_concat_many(pb, ys, 1), c2, 1)
 
 
-def _attention(pb, x, num_heads):
-    """ultralytics Attention (attn_ratio 0.5): qkv 1x1, q^T k * scale, softmax, v attn^T, + pe(v)."""
+def _attention(pb, x, num_heads, legacy=False):
+    """ultralytics Attention (attn_ratio 0.5): qkv 1x1, q^T k * scale, softmax, v attn^T, + pe(v).
+
+    The scale multiplies q^T (a [heads, N, key_dim] tensor) before the product, as in the
+    reference's lowered plans (config/tuning.json holds a scalar Mul over 2 x 32 x 400 =
+    25600 elements and none over the 2 x 400 x 400 scores); legacy=True multiplies the
+    scores after the product instead."""
     _, C, H, W = pb.shapes[x]
     N = H * W
     hd = C // num_heads
@@ -454,8 +483,11 @@ def _attention(pb, x, num_heads):
     qkv = pb.reshape(qkv, [1, num_heads, kd * 2 + hd, N])
     q, k, v = pb.split(qkv, [kd, kd, hd], axis=2)
     qt = pb.permute(q, [0, 1, 3, 2])                  # [1, nh, N, kd]
-    attn = pb.matmul(qt, k)                           # [1, nh, N, N]
-    attn = pb.binary(attn, pb.const(np.array([kd ** -0.5], np.float32), "scale"), 2)
+    scale = pb.const(np.array([kd ** -0.5], np.float32), "scale")
+    if legacy:
+        attn = pb.binary(pb.matmul(qt, k), scale, 2)  # [1, nh, N, N]
+    else:
+        attn = pb.matmul(pb.binary(qt, scale, 2), k)
     attn = pb.softmax(attn, 3)
     at = pb.permute(attn, [0, 1, 3, 2])
     o = pb.matmul(v, at)                              # [1, nh, hd, N]
@@ -466,20 +498,22 @@ def _attention(pb, x, num_heads):
     return pb.conv(o, C, 1, act=ACT_NONE)
 
 
-def _c2psa(pb, x, c2, n=1, e=0.5):
+def _c2psa(pb, x, c2, n=1, e=0.5, legacy=False):
     c = int(c2 * e)
     y = pb.conv(x, 2 * c, 1)
     a, b = pb.split(y, [c, c])
     for _ in range(n):
-        b = pb.binary(b, _attention(pb, b, num_heads=c // 64), 0)
+        b = pb.binary(b, _attention(pb, b, num_heads=c // 64, legacy=legacy), 0)
         f = pb.conv(b, c * 2, 1)
         f = pb.conv(f, c, 1, act=ACT_NONE)
         b = pb.binary(b, f, 0)
     return pb.conv(pb.concat([a, b]), c2, 1)
 
 
-def yolo11n_pose(out_dir, seed=0, imgsz=640):
-    """YOLO11n-pose (ultralytics yolo11-pose.yaml, depth 0.5 width 0.25)."""
+def yolo11n_pose(out_dir, seed=0, imgsz=640, legacy=False):
+    """YOLO11n-pose (ultralytics yolo11-pose.yaml, depth 0.5 width 0.25).
+    legacy=True lowers the head and the C2PSA attention scale in the older export forms
+    (see _pose_head and _attention)."""
     pb = PlanBuilder(out_dir, seed)
     x = pb.input("images", [1, 3, imgsz, imgsz])
     x = pb.conv(x, 16, 3, 2)                 # 0
@@ -492,7 +526,7 @@ def yolo11n_pose(out_dir, seed=0, imgsz=640):
     x = pb.conv(p4, 256, 3, 2)               # 7
     x = _c3k2(pb, x, 256, 1, True)           # 8
     x = _sppf(pb, x, 256)                    # 9
-    p5 = _c2psa(pb, x, 256)                  # 10
+    p5 = _c2psa(pb, x, 256, legacy=legacy)   # 10
     x = pb.concat([pb.upsample(p5), p4])     # 11, 12
     n13 = _c3k2(pb, x, 128, 1, False)        # 13
     x = pb.concat([pb.upsample(n13), p3])    # 14, 15
@@ -501,7 +535,7 @@ def yolo11n_pose(out_dir, seed=0, imgsz=640):
     o4 = _c3k2(pb, x, 128, 1, False)         # 19
     x = pb.concat([pb.conv(o4, 128, 3, 2), p5])  # 20, 21
     o5 = _c3k2(pb, x, 256, 1, True)          # 22
-    out = _pose_head(pb, [o3, o4, o5], dw_cls=True)
+    out = _pose_head(pb, [o3, o4, o5], dw_cls=True, legacy=legacy)
     pb.output(out)
     return pb.write(), pb.flops
 
@@ -572,7 +606,7 @@ def single_conv(out_dir, cin, cout, H, W, k=1, s=1, groups=1, act=ACT_SILU, seed
     return pb.write(), pb.flops
 
 
-def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0, W=None):
+def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0, W=None, legacy=False):
     """The C2PSA attention block alone: input [1, C, H, W] (W = H by default) -> ReLU -> qkv
     1x1, per-head q^T k * scale over H*W tokens, softmax, v attn^T, + depthwise 3x3
     positional conv of v, 1x1 projection (ultralytics Attention, attn_ratio 0.5: head_dim
@@ -582,7 +616,7 @@ def c2psa_attention(out_dir, C=256, H=20, heads=4, seed=0, W=None):
     pb = PlanBuilder(out_dir, seed=seed)
     # a ReLU first, so that the block reads an internal (channels-last) tensor as in the model
     x = pb.unary(pb.input("images", [1, C, H, W]), UN_RELU)
-    pb.output(_attention(pb, x, heads))
+    pb.output(_attention(pb, x, heads, legacy=legacy))
     N, hd = H * W, C // heads
     core = 2.0 * heads * N * N * (hd // 2) + 2.0 * heads * hd * N * N
     return pb.write(), core

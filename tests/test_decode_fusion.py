@@ -26,15 +26,19 @@ def _kernels(path, flags=0, batch=2):
     return ks
 
 
-@pytest.mark.parametrize("name", ["yolov8n-pose", "yolo11n-pose"])
-def test_decode_tail_fused(plans, name):
-    path = plans(name)[0]
+@pytest.mark.parametrize("name,legacy", [("yolov8n-pose", False), ("yolo11n-pose", False),
+                                         ("yolov8n-pose", True), ("yolo11n-pose", True)])
+def test_decode_tail_fused(plans, name, legacy):
+    """Both export forms of the head: ultralytics 8.4's (separate box / score concats, lt / rb
+    by slice_axis, one three-way output concat) and the older one (one box + class concat
+    split by copy_c, nested output concats)."""
+    path = plans(name, legacy=True)[0] if legacy else plans(name)[0]
     fused = _kernels(path)
     chain = _kernels(path, ia.IVH_FLAG_NO_FUSE_DECODE)
     assert fused.count("pose_decode") == 1 and "pose_decode" not in chain
     assert "pose_decode" not in _kernels(path, ia.IVH_FLAG_NO_FUSE)
     # the tail's softmax, permute and slices are gone (YOLO11's attention keeps its own)
-    for k, n in (("softmax_axis", 1), ("permute_0213", 1), ("slice_axis", 2)):
+    for k, n in (("softmax_axis", 1), ("permute_0213", 1), ("slice_axis", 2 if legacy else 4)):
         assert chain.count(k) - fused.count(k) == n, k
     launches = lambda ks: sum(k != "(view)" for k in ks)
     assert launches(chain) - launches(fused) >= 15
@@ -77,11 +81,15 @@ def test_decode_tail_mismatch_not_fused(plans, tmp_path):
 # ------------------------------------------------------------- the fused formula on CPU
 
 def _heads(p):
-    """Per-scale head tensors feeding the anchor concats: (box+cls list, keypoint list)."""
+    """Per-scale head tensors feeding the anchor concats: (box list, class list, keypoint
+    list); in the older export form the box list holds box + class channels and the class
+    list is empty."""
     src = {n.outs[0]: n.ins[0] for n in p.nodes if n.op == "reshape"}
-    cats = [n for n in p.nodes if n.op == "concat4" and n.i("inner", 1) == 1 and n.i("outer", 1) > 1]
+    cats = [n for n in p.nodes if n.op == "concat4" and n.i("inner", 1) == 1 and n.i("ca") > 1]
     by_outer = {n.i("outer"): [src[t] for t in n.ins if t != "-"] for n in cats}
-    return by_outer[65], by_outer[51]
+    if 65 in by_outer:
+        return by_outer[65], [], by_outer[51]
+    return by_outer[64], by_outer[1], by_outer[51]
 
 
 def _rh(v):
@@ -91,9 +99,11 @@ def _rh(v):
 def _decode_restated(p, T):
     """Pose decode of one image from its head tensors, each node's fp16 rounding kept (the
     fused kernel's formula, with the oracle's softmax division)."""
-    xs, ks = _heads(p)
+    xs, cs, ks = _heads(p)
     f = lambda t: O.h2f(T[t]).reshape(p.dims[t][1], -1)
     X = np.concatenate([f(t) for t in xs], 1)
+    if cs:
+        X = np.concatenate([X, np.concatenate([f(t) for t in cs], 1)], 0)
     K = np.concatenate([f(t) for t in ks], 1)
     A = X.shape[1]
     init = lambda stem: O.h2f(next(v for k, v in p.inits.items() if k.startswith(stem)))
@@ -125,8 +135,9 @@ def _ulps(a, b):
     return np.abs(key(a) - key(b))
 
 
-def test_decode_formula_matches_chain(plans):
-    path = plans("yolov8n-pose", imgsz=128)[0]
+@pytest.mark.parametrize("legacy", [False, True])
+def test_decode_formula_matches_chain(plans, legacy):
+    path = plans("yolov8n-pose", imgsz=128, legacy=legacy)[0]
     p = O.Plan.load(path)
     x = O.f2h(np.random.default_rng(4).random(p.numel(p.input_name)).astype(np.float32))
     outs, kept = O.run_plan(p, x, 1, keep=True)
@@ -142,7 +153,7 @@ def test_decode_formula_matches_chain(plans):
 
 # ------------------------------------------------------------------ GPU: fused vs chain
 
-def _small_pose(out_dir, nc, nk):
+def _small_pose(out_dir, nc, nk, legacy=False):
     """A 128x128 toy backbone (strides 8 / 16 / 32) under a pose head with nc classes and
     nk keypoints: counts the decode kernel has no compile-time instance for."""
     pb = pw.PlanBuilder(out_dir, seed=3)
@@ -151,22 +162,42 @@ def _small_pose(out_dir, nc, nk):
     f3 = pb.conv(x, 32, 3, 2)
     f4 = pb.conv(f3, 64, 3, 2)
     f5 = pb.conv(f4, 64, 3, 2)
-    pb.output(pw._pose_head(pb, [f3, f4, f5], nc=nc, nk=(nk, 3)))
+    pb.output(pw._pose_head(pb, [f3, f4, f5], nc=nc, nk=(nk, 3), legacy=legacy))
     return pb.write()
 
 
-def test_decode_tail_fused_other_counts(tmp_path):
-    assert _kernels(_small_pose(str(tmp_path), 2, 5)).count("pose_decode") == 1
+@pytest.mark.parametrize("legacy", [False, True])
+def test_decode_tail_fused_other_counts(tmp_path, legacy):
+    assert _kernels(_small_pose(str(tmp_path), 2, 5, legacy)).count("pose_decode") == 1
+
+
+def test_detect_head_fused(tmp_path):
+    """A Detect head (80 classes, no keypoints; ultralytics 8.4 form) takes the decode too."""
+    pb = pw.PlanBuilder(str(tmp_path), seed=3)
+    x = pb.input("images", [1, 3, 128, 128])
+    x = pb.conv(pb.conv(x, 16, 3, 2), 32, 3, 2)
+    f3 = pb.conv(x, 32, 3, 2)
+    f4 = pb.conv(f3, 64, 3, 2)
+    f5 = pb.conv(f4, 64, 3, 2)
+    pb.output(pw._pose_head(pb, [f3, f4, f5], nc=80, nk=None))
+    assert _kernels(pb.write()).count("pose_decode") == 1
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,batch,flags", [("yolov8n-pose", 3, 0), ("yolo11n-pose", 2, 0),
                                                ("yolov8n-pose", 2, ia.IVH_FLAG_NCHW_ONLY),
-                                               ("small-nc2-nk5", 3, 0)])
+                                               ("small-nc2-nk5", 3, 0), ("legacy-yolov8n-pose", 2, 0),
+                                               ("legacy-small-nc2-nk5", 3, 0)])
 def test_decode_fused_vs_chain_gpu(plans, tmp_path, name, batch, flags):
     """The YOLO heads take the compile-time-count kernel, the toy head (2 classes, 5
-    keypoints) the run-time-count one."""
-    path = _small_pose(str(tmp_path), 2, 5) if name.startswith("small") else plans(name)[0]
+    keypoints) the run-time-count one; both export forms of the head."""
+    legacy = name.startswith("legacy-")
+    base = name[len("legacy-"):] if legacy else name
+    print(f"decode {name} batch {batch} flags {flags:#x}", flush=True)
+    if base.startswith("small"):
+        path = _small_pose(str(tmp_path), 2, 5, legacy)
+    else:
+        path = plans(base, legacy=True)[0] if legacy else plans(base)[0]
     p = O.Plan.load(path)
     x = O.f2h(np.random.default_rng(7).random(p.numel(p.input_name) * batch).astype(np.float32))
     res = {}

@@ -593,14 +593,18 @@ def test_conv1x1_planar_input(tmp_path, cin, cout, hw, batch):
         _check_f32(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PW | ia.IVH_FLAG_NO_SPLITK)
 
 
-@pytest.mark.parametrize("C,H,heads,batch", [(256, 20, 4, 3), (128, 20, 2, 2), (256, 16, 4, 2), (128, 12, 2, 3),
-                                             (128, 8, 2, 5)])
-def test_attention_fused(tmp_path, C, H, heads, batch):
+@pytest.mark.parametrize("C,H,heads,batch,legacy", [(256, 20, 4, 3, False), (128, 20, 2, 2, False),
+                                                    (256, 16, 4, 2, False), (128, 12, 2, 3, False),
+                                                    (128, 8, 2, 5, False), (128, 20, 2, 2, True),
+                                                    (256, 12, 4, 3, True)])
+def test_attention_fused(tmp_path, C, H, heads, batch, legacy):
     """The C2PSA attention block (ultralytics Attention: qkv 1x1, q^T k * scale, softmax,
     v P^T, + depthwise positional conv, 1x1 projection) with the core as one fused kernel,
     against the oracle and against the same plan run node by node (IVH_FLAG_NO_FUSE_ATTN);
-    400 / 256 / 144 / 64 tokens (13 / 8 / 5 / 2 key blocks of 32)."""
-    path, _ = pw.c2psa_attention(str(tmp_path), C=C, H=H, heads=heads)
+    400 / 256 / 144 / 64 tokens (13 / 8 / 5 / 2 key blocks of 32); the scale on q^T before
+    the product (ultralytics 8.4 exports) and, legacy, on the scores after it."""
+    print(f"attention C {C} {H}x{H} heads {heads} batch {batch} legacy {legacy}", flush=True)
+    path, _ = pw.c2psa_attention(str(tmp_path), C=C, H=H, heads=heads, legacy=legacy)
     assert "attention" in _kernels(path, batch)
     assert "attention" not in _kernels(path, batch, ia.IVH_FLAG_NO_FUSE_ATTN)
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
