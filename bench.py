@@ -25,9 +25,11 @@ table goes to stderr.
                  latency
   mfma_roof_probe  the fp16 MFMA rate of the conv kernels' inner-loop shape with no global
                  traffic (infvino_amd/tools/mfma_roof), for zero and for random operands: the
-                 matrix cores draw more power on random data and the clock drops, so the
-                 random-operand rate is the practical MFMA roof; conv_sweep rows of MFMA-bound
-                 layers carry frac_practical against it
+                 matrix cores draw more power on random data and the clock drops
+  vendor_gemm_probe  torch.matmul fp16 on random 8192^3 operands (the ROCm BLAS GEMM) on
+                 the box: conv_sweep rows of MFMA-bound layers carry frac_practical against
+                 it (a fraction above 1 against any probe is not reported: that probe is no
+                 roof there)
   hbm_stream_probe  plain torch fill / copy / broadcast-copy rates on the box: the practical
                  HBM roof of a streaming kernel's traffic pattern; config1's batch-64 line
                  carries frac_practical against the broadcast copy (1 read : 2 writes), the
@@ -203,8 +205,8 @@ def attention(ia, pw, iters):
                 infos = [m.nodeInfo(i) for i in range(m.nodeCount())]
                 m.close()
             core = [i for i, inf in enumerate(infos) if inf["op"] == "attention"]
-            if not core:
-                first = next(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
+            if not core:  # q's permute and scale (when the scale is on q^T) through the last bmm
+                first = next(i for i, inf in enumerate(infos) if inf["op"] in ("bmm", "permute_0213"))
                 last = max(i for i, inf in enumerate(infos) if inf["op"] == "bmm")
                 core = list(range(first, last + 1))
             t_core = float(sum(prof[i] for i in core)) * 1e-3
@@ -325,6 +327,49 @@ def hbm_stream_rates():
     return res
 
 
+def vendor_gemm_rate():
+    """torch.matmul (the ROCm BLAS libraries' fp16 GEMM) on random 8192 x 8192 x 8192
+    operands, timed with events: what a vendor GEMM sustains on this box on random data
+    (the matrix cores draw more power on random operands and the clock drops), the roof the
+    MFMA-bound conv layers are rated against."""
+    import torch
+    n = 8192
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    a = torch.rand(n, n, device="cuda:0", dtype=torch.float16, generator=g) - 0.5
+    b = torch.rand(n, n, device="cuda:0", dtype=torch.float16, generator=g) - 0.5
+    c = torch.empty(n, n, device="cuda:0", dtype=torch.float16)
+    for _ in range(3):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    iters = 20
+    e0.record()
+    for _ in range(iters):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+    return {"gemm_f16_tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_FP16_TFLOPS, 4), "ms": round(ms, 4),
+            "shape": [n, n, n], "operands": "uniform [-0.5, 0.5) fp16, fp32 accumulate (torch.matmul)",
+            "torch": torch.__version__}
+
+
+def vendor_gemm_probe():
+    """Runs `bench.py --phase gemm` as a child process and returns its JSON line, or a note."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--phase", "gemm"], capture_output=True,
+                           text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return {"note": "probe timed out"}
+    if r.returncode != 0:
+        return {"note": f"probe failed: {r.stderr.strip()[-200:]}"}
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"[bench] vendor GEMM probe: {res}")
+    return res
+
+
 def model_lines(ia, pw, specs, steps, warmup):
     """The other model configurations: images/s of graph replays at each batch (inputs
     resident in HBM) and the synchronous batch-1 latency."""
@@ -399,11 +444,12 @@ def main():
     ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer (or config1) for --phase layer")
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
                     help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
-    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm"],
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm", "gemm"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
                          "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE; "
                          "sweep: the conv sweep only; layer: --steps passes of one sweep layer (--layer); "
-                         "hbm: the torch HBM stream probe alone (one JSON line)")
+                         "hbm: the torch HBM stream probe alone (one JSON line); "
+                         "gemm: the torch fp16 GEMM probe alone (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -412,6 +458,9 @@ def main():
 
     if args.phase == "hbm":  # before the library touches the GPU
         print(json.dumps(hbm_stream_rates()))
+        return
+    if args.phase == "gemm":
+        print(json.dumps(vendor_gemm_rate()))
         return
     import infvino_amd as ia
     from infvino_amd import planwriter as pw
@@ -521,28 +570,37 @@ def main():
 
     c1 = None if args.no_sweep else config1(ia, pw, max(args.profile_iters, 10))
     hbm_probe = hbm_stream_probe()
+
+    def practical(achieved, ref):
+        # a fraction of what a plain library kernel reaches on the box; a kernel that beats
+        # the probe shows the probe is no roof there, so no fraction is reported
+        f = achieved / ref
+        return round(f, 4) if f <= 1.0 else None
+
     if c1 and hbm_probe.get("broadcast_1r2w_gbs"):
-        c1["b64"]["roofline"]["frac_practical"] = round(
-            c1["b64"]["roofline"]["achieved"] / hbm_probe["broadcast_1r2w_gbs"], 4)
+        c1["b64"]["roofline"]["frac_practical"] = practical(c1["b64"]["roofline"]["achieved"],
+                                                            hbm_probe["broadcast_1r2w_gbs"])
     if roof["bound"] == "hbm" and hbm_probe.get("copy_large_gbs"):
         # against a plain copy of a footprint past the Infinity Cache, as the step's largest
         # node (367 MB) is
         roof["practical_peak"] = hbm_probe["copy_large_gbs"]
-        roof["frac_practical"] = round(roof["achieved"] / hbm_probe["copy_large_gbs"], 4)
+        roof["frac_practical"] = practical(roof["achieved"], hbm_probe["copy_large_gbs"])
     probe = mfma_roof_probe()
+    gemm = vendor_gemm_probe()
     sweep = None
     if not args.no_sweep:
         sweep = {f"b{b}": conv_sweep(ia, pw, b, max(args.profile_iters, 10)) for b in (B, 1)}
         sweep["dw_b256"] = conv_sweep(ia, pw, 256, max(args.profile_iters, 10), only="dw")
         for rows in sweep.values():
             for r in rows:
-                if r["bound"] == "mfma" and probe.get("random_tflops"):
-                    r["frac_practical"] = round(r["tflops"] / probe["random_tflops"], 4)
+                if r["bound"] == "mfma" and gemm.get("gemm_f16_tflops"):
+                    # against the vendor GEMM on random operands on this box
+                    r["frac_practical"] = practical(r["tflops"], gemm["gemm_f16_tflops"])
                 elif r["bound"] == "hbm" and hbm_probe.get("copy_gbs") and hbm_probe.get("copy_large_gbs"):
                     # a copy of the same side of the 256 MB Infinity Cache as the layer's bytes
                     nbytes = r["gbs"] * 1e9 * r["us"] * 1e-6
                     ref = hbm_probe["copy_large_gbs"] if nbytes > 256e6 else hbm_probe["copy_gbs"]
-                    r["frac_practical"] = round(r["gbs"] / ref, 4)
+                    r["frac_practical"] = practical(r["gbs"], ref)
     attn = None if args.no_sweep else attention(ia, pw, max(args.profile_iters, 10))
     others = None if args.no_models else model_lines(
         ia, pw, [("yolov8n-pose", 640, (16, 64)), ("mobilenetv3-small", 224, (1, 32, 256)),
@@ -593,6 +651,7 @@ def main():
         "roofline": roof,
         "roofline_step": roof_step,
         "mfma_roof_probe": probe,
+        "vendor_gemm_probe": gemm,
         "hbm_stream_probe": hbm_probe,
         "config1": c1,
         "conv_sweep": sweep,
