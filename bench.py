@@ -83,9 +83,12 @@ def calibrate(ia, pw):
 def sweep_plan(pw, d, name):
     """Plan of one conv sweep layer in the layout it has inside a model: the stem reads the
     NCHW graph input, every other conv sits between two ReLUs (channels-last tensors).
-    "config1": the plan's conv1x1 op on graph tensors (64->128 at 80x80, NCHW in and out)."""
+    "config1": the plan's conv1x1 op on graph tensors (64->128 at 80x80, NCHW in and out);
+    "attention": the C2PSA attention block (256 channels, 4 heads, 400 tokens)."""
     if name == "config1":
         return pw.conv1x1_config(d)[0]
+    if name == "attention":
+        return pw.c2psa_attention(d)[0]
     _, cin, cout, H, W, k, s, g, act = next(c for c in pw.CONV_SWEEP if c[0] == name)
     pb = pw.PlanBuilder(d, seed=0)
     x = pb.input("x", [1, cin, H, W])
@@ -444,12 +447,14 @@ def main():
     ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer (or config1) for --phase layer")
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
                     help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
-    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm", "gemm"],
+    ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm", "gemm",
+                                                       "attention"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
                          "128 MiB-in/128 MiB-out elementwise pass to scale FETCH_SIZE/WRITE_SIZE; "
                          "sweep: the conv sweep only; layer: --steps passes of one sweep layer (--layer); "
                          "hbm: the torch HBM stream probe alone (one JSON line); "
-                         "gemm: the torch fp16 GEMM probe alone (one JSON line)")
+                         "gemm: the torch fp16 GEMM probe alone (one JSON line); "
+                         "attention: the C2PSA attention measurement alone (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -465,6 +470,9 @@ def main():
     import infvino_amd as ia
     from infvino_amd import planwriter as pw
 
+    if args.phase == "attention":
+        print(json.dumps(attention(ia, pw, max(args.profile_iters, 10))))
+        return
     if args.phase == "calib":
         calibrate(ia, pw)
         return
