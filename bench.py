@@ -80,15 +80,41 @@ def calibrate(ia, pw):
     log("[bench] calibration pass: 5 x (128 MiB read + 128 MiB write)")
 
 
+# Other layers of the YOLOv8n-pose step whose kernels the planner picks (profiled one at a
+# time): name, cin, cout, H, W, k, s.  "pair<C>_<H>" is a C2f bottleneck (two 3x3 convs C -> C
+# with the block input added), which runs as one fused launch.
+MODEL_LAYERS = [
+    ("conv3x3s1_128to64_40", 128, 64, 40, 40, 3, 1),
+    ("conv3x3s2_64to128_80", 64, 128, 80, 80, 3, 2),
+    ("conv3x3s2_128to256_40", 128, 256, 40, 40, 3, 2),
+    ("conv1x1_32to32_160", 32, 32, 160, 160, 1, 1),
+    ("pair16_160", 16, 16, 160, 160, 3, 1),
+    ("pair32_80", 32, 32, 80, 80, 3, 1),
+]
+
+
 def sweep_plan(pw, d, name):
     """Plan of one conv sweep layer in the layout it has inside a model: the stem reads the
     NCHW graph input, every other conv sits between two ReLUs (channels-last tensors).
     "config1": the plan's conv1x1 op on graph tensors (64->128 at 80x80, NCHW in and out);
-    "attention": the C2PSA attention block (256 channels, 4 heads, 400 tokens)."""
+    "attention": the C2PSA attention block (256 channels, 4 heads, 400 tokens); the
+    MODEL_LAYERS names: those layers between two ReLUs."""
     if name == "config1":
         return pw.conv1x1_config(d)[0]
     if name == "attention":
         return pw.c2psa_attention(d)[0]
+    extra = next((c for c in MODEL_LAYERS if c[0] == name), None)
+    if extra:
+        _, cin, cout, H, W, k, s = extra
+        pb = pw.PlanBuilder(d, seed=0)
+        x = pb.unary(pb.input("x", [1, cin, H, W]), pw.UN_RELU)
+        if name.startswith("pair"):
+            t = pb.conv(x, cout, 3, 1)
+            y = pb.conv(t, cout, 3, 1, res=x)
+        else:
+            y = pb.conv(x, cout, k, s)
+        pb.output(pb.unary(y, pw.UN_RELU))
+        return pb.write()
     _, cin, cout, H, W, k, s, g, act = next(c for c in pw.CONV_SWEEP if c[0] == name)
     pb = pw.PlanBuilder(d, seed=0)
     x = pb.input("x", [1, cin, H, W])
