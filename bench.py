@@ -90,6 +90,13 @@ MODEL_LAYERS = [
     ("conv1x1_32to32_160", 32, 32, 160, 160, 1, 1),
     ("pair16_160", 16, 16, 160, 160, 3, 1),
     ("pair32_80", 32, 32, 80, 80, 3, 1),
+    ("conv3x3s1_64to64_40", 64, 64, 40, 40, 3, 1),
+    ("conv3x3s1_128to128_20", 128, 128, 20, 20, 3, 1),
+    ("conv3x3s1_256to64_20", 256, 64, 20, 20, 3, 1),
+    ("conv3x3s2_64to64_80", 64, 64, 80, 80, 3, 2),
+    ("conv3x3s2_128to128_40", 128, 128, 40, 40, 3, 2),
+    ("conv1x1_384to128_40", 384, 128, 40, 40, 1, 1),
+    ("conv1x1_128to64_80", 128, 64, 80, 80, 1, 1),
 ]
 
 

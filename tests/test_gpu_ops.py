@@ -441,6 +441,54 @@ def test_depthwise(tmp_path, c, hw, k, s, act, internal, post):
     _check_f32(path, 2, lo=-1.0)
 
 
+@pytest.mark.parametrize("c,h,w,k,s,p,act", [
+    (64, 80, 80, 3, 1, 1, 1), (128, 40, 40, 3, 1, 1, 1), (16, 112, 112, 3, 2, 1, 0), (96, 14, 14, 5, 2, 2, 0)])
+def test_depthwise_kernel_check_shapes(tmp_path, c, h, w, k, s, p, act):
+    """scripts/kernel_check.py:94-99's depthwise shapes on its own data (gen_depthwise,
+    :121-138: default_rng(0), x ~ N(0,1), w = 0.2 N(0,1), b ~ N(0,1), all fp16) as image 0 of
+    a batch of 2, checked against kernel_check's reference (fp32 taps, act(acc + b) -> fp16)
+    with its op contract; image 1 is uniform in [-1, 1).  Both images against the fp32 oracle
+    and the reference-rounding oracle.  Activation codes 0 and 1 (none, SiLU) mean the same in
+    the canonical and conv_general.cl numbering.  The conv reads the NCHW graph input, as
+    kernel_check's kernels do."""
+    rng = np.random.default_rng(0)
+    x0 = rng.standard_normal((c, h, w)).astype(np.float16)
+    wt = (rng.standard_normal((c, k, k)).astype(np.float16) * 0.2).astype(np.float16)
+    bt = rng.standard_normal(c).astype(np.float16)
+    pb = pw.PlanBuilder(str(tmp_path), seed=0)
+    y = pb.conv(pb.input("x", [1, c, h, w]), c, k, s, groups=c, act=act, pad=p,
+                weight=wt.astype(np.float32).reshape(c, 1, k, k), bias_val=bt.astype(np.float32))
+    pb.output(y)
+    path = pb.write()
+    assert _conv_kernel(path, 2) == "dwconv"
+    ho, wo = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    xp = np.pad(x0.astype(np.float32), ((0, 0), (p, p), (p, p)))
+    acc = np.zeros((c, ho, wo), np.float32)
+    for kh in range(k):
+        for kw in range(k):
+            acc += xp[:, kh:kh + ho * s:s, kw:kw + wo * s:s] * wt[:, kh, kw].astype(np.float32)[:, None, None]
+    acc += bt.astype(np.float32)[:, None, None]
+    kc = (acc / (1.0 + np.exp(-acc)) if act == 1 else acc).astype(np.float16).astype(np.float32).ravel()
+    x1 = O.f2h((2.0 * np.random.default_rng(7).random(c * h * w) - 1.0).astype(np.float32))
+    x = np.concatenate([x0.view(np.uint16).ravel(), x1])
+    print(f"depthwise {c}x{h}x{w} K{k} s{s} p{p} act{act} batch 2", flush=True)
+    m = ia.PlanModel(path, 0, 2)
+    m.setInput(x, 2)
+    m.run(2)
+    got = m.readOutput(0, 2).reshape(2, -1)
+    m.close()
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), kc)
+    print(f"   vs kernel_check reference mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < OP_MEAN and max_rel < OP_MAX
+    plan = O.Plan.load(path)
+    for mode, lim in ((O.F32, (F32_MEAN, F32_MAX)), (O.REF, (OP_MEAN, OP_MAX))):
+        ref = O.run_plan(plan, x, 2, mode=mode)[0]
+        for i in range(2):
+            mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[i]), O.h2f(ref[i].ravel()))
+            print(f"   image {i} vs oracle mode {mode} mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+            assert mean_rel < lim[0] and max_rel < lim[1]
+
+
 @pytest.mark.parametrize("c,hw,k,s,batches", [
     (16, 112, 3, 2, (1, 6)), (64, 80, 3, 1, (1, 3)), (240, 14, 5, 1, (1, 9)), (576, 7, 5, 1, (1, 5)),
     (88, 28, 3, 1, (2, 4)), (120, 33, 5, 2, (1, 3)), (8, 61, 5, 1, (1, 2)), (40, 45, 3, 2, (3, 1)),
