@@ -404,6 +404,8 @@ std::string igemm_launch_tag(const ConvParams & p)
     snprintf(b, sizeof b, "blocks=%ld lds=%zu planar-out%s", pw_blocks(p), pwt_lds_bytes(p), p.xt ? " planar-in" : "");
   else if (p.pw)
     snprintf(b, sizeof b, "blocks=%ld lds=%zu", pw_blocks(p), pw_lds_bytes(p));
+  else if (p.wide)
+    snprintf(b, sizeof b, "tm=%d ranges=%d wgs=%ld", p.th, p.tw, wide_grid(p));
   else if (p.pipe)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d items=%ld", p.pipe - 1, p.th, p.tw, pipe_items(p));
   else if (p.res)
@@ -429,6 +431,10 @@ void launch_conv_igemm(const ConvParams & p, hipStream_t s)
   }
   if (p.pw) {
     launch_conv_pw(p, s);
+    return;
+  }
+  if (p.wide) {
+    launch_conv_wide(p, s);
     return;
   }
   if (p.pipe) {

@@ -77,6 +77,10 @@ ConvPacking conv_packing(const ConvSpec & s)
         pk.kpad_halo[hi] = (cin_g + ck - 1) / ck * halo_taps(ck) * ck;
         pk.halo[hi] = seg((size_t)rows * pk.kpad_halo[hi] * 2);
       }
+      if (cin_g % 32 == 0 && cin_g >= 128 && s.Cout > 64 && s.Cout <= 256 && !(s.flags & IVH_FLAG_NO_WIDE)) {
+        pk.wide_bn = 128;
+        pk.wide = seg((size_t)rup(s.Cout, pk.wide_bn) * 9 * cin_g * 2);
+      }
       // 16 input channels: also one 32-channel chunk (zero past 16), the packing of the
       // second conv of a 32 -> 16 -> 32 bottleneck run as a fused pair of 32 channels
       if (cin_g == 16 && s.Cout == 32 && pk.halo[1] == kNoSeg) {
@@ -121,6 +125,20 @@ void conv_pack(const ConvSpec & s, const ConvPacking & pk, const uint16_t * W, c
       for (int co = 0; co < Cout; ++co)
         for (int ci = 0; ci < cin_g; ++ci)
           for (int t = 0; t < 9; ++t) Q[(size_t)co * kh + ((ci / ck) * taps + t) * ck + (ci % ck)] = at(co, ci, t);
+    }
+    if (pk.wide != kNoSeg) {
+      uint16_t * Q = reinterpret_cast<uint16_t *>(blob.data() + pk.wide);
+      const int bn = pk.wide_bn, ncb = bn / 32, nch = cin_g / 16, ncg = (Cout + bn - 1) / bn;
+      size_t o = 0;
+      for (int cg = 0; cg < ncg; ++cg)
+        for (int c16 = 0; c16 < nch; ++c16)
+          for (int t = 0; t < 9; ++t)
+            for (int cb = 0; cb < ncb; ++cb)
+              for (int l = 0; l < 64; ++l)
+                for (int e = 0; e < 8; ++e, ++o) {
+                  const int co = cg * bn + cb * 32 + (l & 31), ci = c16 * 16 + (l >> 5) * 8 + e;
+                  Q[o] = co < Cout ? at(co, ci, t) : 0;
+                }
     }
   } else if (pk.stem) {
     uint16_t * P = reinterpret_cast<uint16_t *>(blob.data() + pk.w);
@@ -227,6 +245,24 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   // 43.0 us, 128->51 / 128->64 at 40x40 28.2 / 27.6 -> 26.1 / 27.1 us; with Cin <= 64 the
   // resident-weight kernel below stays faster (64->64 at 80x80: 44 vs 51 us).
   int hc, th, tw;
+  // 3x3 stride 1 with Cin % 32 == 0, Cin >= 128, 64 < Cout <= 256 and SiLU: the wide-layer
+  // kernel (one persistent work-group per CU over an equal share of the pixels) on the
+  // fragment-ordered packing, when every work-group gets at least two 32-pixel blocks.
+  if (p.K == 3 && p.S == 1 && p.P == 1 && !(s.flags & IVH_FLAG_NO_WIDE) && pipe_views_ok(p) &&
+      wide_plan(p.Cin, p.Cout, p.H, p.W, batch, p.act, &th, &tw)) {
+    const long nblk = (((long)batch * (p.H + 1) - 1) * p.W + 31) / 32;
+    if (pk.wide != kNoSeg && pk.wide_bn == 128 && nblk >= 2L * tw) {
+      p.wide = 1;
+      p.th = th;
+      p.tw = tw;
+      p.ck = 16;
+      p.ksplit = 1;
+      p.ws = nullptr;
+      p.w = reinterpret_cast<const __half *>(base + pk.wide);
+      p.kpad = 9 * p.Cin;
+      return kLaunchIgemm;
+    }
+  }
   const bool pipe_any = (s.flags & IVH_FLAG_PIPE_ANY) != 0;
   if (p.K == 3 && p.S == 1 && p.P == 1 && !(s.flags & IVH_FLAG_NO_PIPE) && (p.Cin > 64 || pipe_any) && p.Cout <= 256 &&
       pipe_views_ok(p) &&

@@ -41,6 +41,12 @@ struct ConvPacking {
   int cin8 = 0, kpad = 0;            // implicit GEMM: fp16 [round_up(Cout,128)][kpad]
   size_t halo[3] = {kNoSeg, kNoSeg, kNoSeg};  // 3x3 s1 p1: fp16 [rows][chunk][tap][ck], ck 16/32/64
   int kpad_halo[3] = {0, 0, 0};
+  // 3x3 s1 p1 with Cin % 32 == 0, 64 <= Cin, Cout <= 256 (the wide-layer kernel): fp16
+  // [Cout / wide_bn groups][Cin / 16][tap][wide_bn / 32][64 lanes][8], every 32 x 16 MFMA A
+  // fragment (lane l: output channel l % 32 of its block, input channels 8 (l / 32) ..) as
+  // 1 KB in lane order, so the kernel's copies of a chunk read one contiguous range
+  size_t wide = kNoSeg;
+  int wide_bn = 0;
   bool stem = false;                 // Cin <= 3 3x3: fp16 [ceil(Cout/16)*16][32] ...
   size_t stem_w2 = kNoSeg;           // ... then (Cout <= 16) fp16 [16][64], k = tap*4 + ci
   size_t dw_w16 = kNoSeg;            // depthwise: the same [K][K][C] weights as fp16

@@ -1412,7 +1412,7 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   if (!pair_plan(C, b.H, b.W, batch, &th, &tw)) return false;
   b.th = th;
   b.tw = tw;
-  b.pipe = b.res = b.halo = b.s2 = 0;
+  b.pipe = b.wide = b.res = b.halo = b.s2 = 0;
   b.ksplit = 1;
   b.ws = nullptr;
   L.kind = Launch::kPair;
@@ -1997,7 +1997,7 @@ void Model::validate(const Launch & l) const
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
     // the resident-weight, pipelined and persistent stride-2 kernels write 4- or 8-channel
     // groups into the view's padding channels
-    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.s2 > 2 || p.pw == 1 ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
+    check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.wide || p.s2 > 2 || p.pw == 1 ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
           "conv y");
     if (p.r.ptr) check(p.r.ptr, 0, vlast(p.r, p.batch, p.Cout, HWo), 2, "conv residual");
     // the MFMA epilogues read the zero-padded bias of round_up(Cout, 128) channels
@@ -2049,8 +2049,21 @@ void Model::validate(const Launch & l) const
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 14)) throw std::runtime_error("pipelined conv geometry too large");
         check(p.w, 0, (long)(p.Cout + 127) / 128 * 128 * p.kpad - 1, 2, "pipelined conv w");
       }
+      if (p.wide) {
+        const long nslot = ((long)p.batch * (p.H + 1) - 1) * p.W;
+        const int bn = 128, pb = p.th;
+        if (p.wide != 1 || p.halo || p.res || p.pipe || p.s2 || p.pw || p.ck != 16 || p.K != 3 || p.S != 1 ||
+            p.P != 1 || p.ksplit != 1 || !wide_tm_ok(p.th) || p.tw < 1 || p.Ho != p.H || p.Wo != p.W ||
+            p.Cin < 128 || p.Cin % 32 || p.Cout <= 64 || p.Cout > 256 || !pipe_views_ok(p) || p.act != kActSiLU ||
+            nslot >= (1L << 22) - 64 || p.W >= (1 << 14) || p.tw > (nslot + 31) / 32 ||
+            (long)p.tw * ((p.Cout + bn - 1) / bn) > 65535 ||
+            (long)((p.W - 1 + 32 * pb - 1) / p.W + 3) * (3 * p.W + 16) > 2048)
+          throw std::runtime_error("wide-layer conv geometry");
+        if (p.kpad != 9 * p.Cin) throw std::runtime_error("wide-layer conv packing");
+        check(p.w, 0, (long)(p.Cout + bn - 1) / bn * bn * p.kpad - 1, 2, "wide-layer conv w");
+      }
       if (p.pw == 2) {
-        if (p.ksplit != 1 || p.halo || p.res || p.pipe || p.s2 || !pwt_plan(p) || pwt_lds_bytes(p) > 65536)
+        if (p.ksplit != 1 || p.halo || p.res || p.pipe || p.wide || p.s2 || !pwt_plan(p) || pwt_lds_bytes(p) > 65536)
           throw std::runtime_error("planar pointwise streaming geometry");
         check(p.w, 0, (long)(p.Cout - 1) * p.kpad + p.cin8 - 1, 2, "planar pointwise w");
         if (!p.xt) check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "planar pointwise x");
@@ -2085,8 +2098,8 @@ void Model::validate(const Launch & l) const
         check(p.ws, 0, (long)p.ksplit * rows * M - 1, 4, "igemm split-K workspace");
       }
       if (p.kpad % kIgemmBK && !p.res) throw std::runtime_error("kpad not a multiple of the K tile");
-      if (!p.halo && !p.res && !p.pipe && (p.bk != 32 && p.bk != 64)) throw std::runtime_error("kpad not a multiple of the K tile");
-      if (!p.halo && !p.res && !p.pipe && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
+      if (!p.halo && !p.res && !p.pipe && !p.wide && (p.bk != 32 && p.bk != 64)) throw std::runtime_error("kpad not a multiple of the K tile");
+      if (!p.halo && !p.res && !p.pipe && !p.wide && p.kpad % p.bk) throw std::runtime_error("kpad not a multiple of the K step");
     } else if (l.kind == Launch::kDirect && p.stem_mfma) {
       check(p.x.ptr, 0, vlast(p.x, p.batch, p.Cin, HW), 2, "stem x");
       check(p.w, 0, (long)(p.Cout + 15) / 16 * 16 * 32 - 1, 2, "stem w");
@@ -2482,7 +2495,7 @@ std::string Model::nodeKernel(int i)
   const Launch & l = P.L[P.begin[i]];
   switch (l.kind) {
   case Launch::kIgemm:
-    return l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.pw == 2 ? "conv_pw_planar" : l.cp.pw ? "conv_pw" : l.cp.s2 ? (l.cp.s2 > 2 ? "conv_s2p" : "conv_s2") : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
+    return l.cp.wide ? "conv_wide" : l.cp.pipe ? "conv_pipe" : l.cp.res ? "conv_res" : l.cp.halo ? "conv_halo" : (l.cp.pw == 2 ? "conv_pw_planar" : l.cp.pw ? "conv_pw" : l.cp.s2 ? (l.cp.s2 > 2 ? "conv_s2p" : "conv_s2") : (l.cp.ksplit > 1 ? "conv_igemm_sk" : "conv_igemm"));
   case Launch::kDirect: return l.cp.stem_mfma ? "conv_stem" : "conv_direct";
   case Launch::kDw: return "dwconv";
   case Launch::kDecode: return "pose_decode";

@@ -82,6 +82,10 @@ struct ConvParams {
   // 3x3 stride-1 pad-1 DMA-pipelined kernel (conv_pipe.hip, Cin % 8 == 0, Cin >= 32): config
   // + 1 (0: not used); th x tw as for the halo kernel, w the 32-channel-chunk halo packing
   int pipe = 0;
+  // 3x3 stride-1 pad-1 wide-layer kernel (conv_wide.hip, Cin % 32 == 0, Cin >= 128): 1 when
+  // used; th = 32-pixel blocks per wave and pass, tw = pixel ranges (work-groups per
+  // 128-channel group); w the fragment-ordered packing (ConvPacking::wide)
+  int wide = 0;
   // channels after the output view's last one that belong to no tensor (the padding of a
   // channels-last root whose last channel range this view is); a kernel may write there
   int ypad = 0;

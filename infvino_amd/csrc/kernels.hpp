@@ -51,6 +51,13 @@ constexpr int kResMaxRows = 34;  // patch rows (TH + 2) of the resident-weight k
 constexpr int kHaloMaxRows = 34;  // patch rows (TH + 2) of the LDS-patch kernel's tiles
 void launch_conv_res(const ConvParams & p, hipStream_t s);
 
+// conv_wide.hip: 3x3 stride-1 pad-1 convs with Cin % 32 == 0, Cin >= 128, 64 < Cout <= 256,
+// one persistent work-group per CU over an equal share of the output pixels
+bool wide_plan(int cin, int cout, int H, int W, int batch, int act, int * tm, int * gx);
+bool wide_tm_ok(int tm);
+long wide_grid(const ConvParams & p);
+void launch_conv_wide(const ConvParams & p, hipStream_t s);
+
 // conv_pipe.hip: 3x3 stride-1 pad-1 convs with Cin % 8 == 0, Cin >= 32, fed through LDS by
 // DMA (buffer loads into LDS), persistent over (tile, channel block) items
 // config and output tile th x tw for a layer at a batch size; false: not eligible

@@ -211,6 +211,67 @@ def test_pipe_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
+@pytest.mark.parametrize("cin,cout,H,W,batch,want", [
+    (128, 128, 40, 40, 64, "tm=13"),   # the 128->128 sweep layer: one pass of 13 blocks per work-group
+    (256, 256, 20, 20, 64, "tm=7"),    # the 256->256 sweep layer: two channel groups, 16 chunks
+    (128, 96, 40, 40, 39, "tm=10"),    # a channel block past Cout (96 of 128)
+    (128, 256, 40, 40, 24, "tm=10"),
+    (128, 96, 20, 20, 49, "tm=4"),     # 20x20: passes across image boundaries
+    (128, 96, 20, 20, 39, "tm=2"),
+    (128, 256, 20, 20, 49, "tm=7"),
+    (256, 128, 20, 20, 64, ""),        # sixteen chunks, one channel group
+    (128, 128, 33, 35, 40, ""),        # odd map: rows of 35, passes starting mid-row
+    (192, 96, 40, 40, 16, ""),         # twelve chunks
+])
+def test_wide_conv3x3(tmp_path, cin, cout, H, W, batch, want):
+    """3x3 stride-1 convs through the wide-layer kernel (one work-group per CU over an equal
+    share of the pixels) vs the oracle and vs the kernel the planner picks without it."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=pw.ACT_SILU, pre_relu=True, post_relu=True)
+    print(f"wide conv {cin}->{cout} {H}x{W} batch {batch}", flush=True)
+    tags = _conv_tags(path, batch)
+    assert tags[0].startswith("conv_wide " + want), tags
+    assert _conv_kernel(path, batch, ia.IVH_FLAG_NO_WIDE) != "conv_wide"
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_WIDE)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    print(f"   vs other kernel mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
+def _conv_tags(path, batch, flags=0):
+    m = ia.PlanModel(path, 0, batch, flags | ia.IVH_FLAG_DRY_RUN)
+    m.run(batch)
+    tags = [m.nodeTag(i) for i in range(m.nodeCount()) if m.nodeInfo(i)["kernel"].startswith("conv")]
+    m.close()
+    return tags
+
+
+@pytest.mark.parametrize("C,H,W,batch,want", [
+    (128, 40, 40, 64, "tm=13"), (128, 40, 40, 39, "tm=10"), (128, 40, 40, 24, "tm=7"),
+    (128, 20, 20, 49, "tm=4"), (128, 20, 20, 39, "tm=2"), (256, 20, 20, 49, "tm=7"),
+])
+def test_wide_residual_chain(tmp_path, C, H, W, batch, want):
+    """Bottleneck chain (3x3 SiLU, 3x3 SiLU + residual, 3x3 SiLU + residual) through the
+    wide-layer kernel with the fused residual add."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, C, H, W]), pw.UN_RELU)
+        t = pb.conv(x, C, 3)
+        t = pb.conv(t, C, 3)
+        y = pb.binary(x, t, 0)
+        u = pb.conv(y, C, 3)
+        z = pb.binary(y, u, 0)
+        return pb.unary(z, pw.UN_RELU)
+    path = _small_plan(tmp_path, build)
+    print(f"wide residual chain C {C} {H}x{W} batch {batch}", flush=True)
+    tags = _conv_tags(path, batch)
+    assert len(tags) == 3 and all(t.startswith("conv_wide") for t in tags), tags
+    assert tags[1].startswith("conv_wide " + want) and tags[2].startswith("conv_wide " + want), tags
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_WIDE)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
+
+
 @pytest.mark.parametrize("C,H,W,batch,res,act1,act2", [
     (32, 80, 80, 2, True, pw.ACT_SILU, pw.ACT_SILU),     # the YOLOv8 C2f bottleneck at 80x80
     (32, 80, 80, 3, False, pw.ACT_SILU, pw.ACT_SILU),    # no shortcut (the neck's C2f)

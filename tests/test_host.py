@@ -56,8 +56,9 @@ def test_kernel_choice_yolov8(plans):
     stride-2 kernel for the 16->32, 32->64 and 64->128 downsamples, the implicit GEMM for the
     wider ones (128->256), the
     resident-weight kernel for the stride-1 3x3 convs with 16 < Cin <= 64 (but not the
-    Cin <= 32 ones with a fused residual), the DMA-pipelined kernel for Cin > 64 on the
-    40x40 maps (enough items for its persistent grid), the fused pair kernel for the three
+    Cin <= 32 ones with a fused residual), the wide-layer kernel for Cin >= 128 with
+    64 < Cout <= 256, the DMA-pipelined kernel for the other Cin > 64 convs on the 40x40 maps
+    (enough items for its persistent grid), the fused pair kernel for the three
     32-channel bottlenecks at 80x80 and the 16-channel one at 160x160 (their second conv then
     launches nothing) and the stride-1 LDS-patch kernel for the rest."""
     m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
@@ -70,23 +71,29 @@ def test_kernel_choice_yolov8(plans):
     assert by["conv3x3 64x80x80->128x40x40 k3 s2 g1 act1"] == "conv_s2p"
     assert by["conv3x3 128x40x40->256x20x20 k3 s2 g1 act1"] == "conv_igemm"
     s1 = [(i["kernel"], int(i["desc"].split()[1].split("x")[0]), int(i["desc"].split()[1].split("x")[1]),
-           "+res" in i["desc"]) for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
+           "+res" in i["desc"], int(i["desc"].split("->")[1].split("x")[0]))
+          for i in info if i["op"] == "conv3x3" and " s1 " in i["desc"]]
 
-    def want(k, cin, hw, res):
+    def want(k, cin, hw, res, cout):
         if (cin, hw) in ((32, 80), (16, 160)) and k in ("conv_pair", "(fused)"):  # bottleneck pairs, one launch
             return True
         if 16 < cin <= 64 and not (res and cin <= 32):
             return k == "conv_res"
+        if cin >= 128 and cin % 32 == 0 and 64 < cout <= 256:
+            return k == "conv_wide"
         return k == ("conv_pipe" if cin > 64 and hw >= 40 else "conv_halo")
-    assert s1 and all(want(k, cin, hw, res) for k, cin, hw, res in s1)
-    assert sum(k == "conv_res" for k, _, _, _ in s1) >= 16
+    assert s1 and all(want(k, cin, hw, res, cout) for k, cin, hw, res, cout in s1)
+    assert sum(k == "conv_res" for k, *_ in s1) >= 16
+    # the P5 C2f bottlenecks of the backbone (with its shortcut) and of the neck: 128 -> 128
+    # at 20x20, on the wide-layer kernel
+    assert sum(k == "conv_wide" for k, *_ in s1) == 4
     # the heads' last 1x1 convs (box 64 and keypoint 51 planes at three scales) write the NCHW
     # head tensors through the planar-output streaming kernel; the single class plane stays on
     # the implicit GEMM
     planar = sorted(i["desc"].split()[1] for i in info if i["kernel"] == "conv_pw_planar")
     assert planar == sorted(f"{c}x{hw}x{hw}->{o}x{hw}x{hw}" for hw in (80, 40, 20) for c, o in ((51, 51), (64, 64)))
-    assert sum(k == "conv_pipe" for k, _, _, _ in s1) >= 3
-    assert sum(k == "conv_pair" for k, _, _, _ in s1) == 4 and sum(k == "(fused)" for k, _, _, _ in s1) == 4
+    assert sum(k == "conv_pipe" for k, *_ in s1) >= 3
+    assert sum(k == "conv_pair" for k, *_ in s1) == 4 and sum(k == "(fused)" for k, *_ in s1) == 4
     m.close()
 
 
@@ -149,7 +156,7 @@ def test_kernel_choice_conv1x1_config(tmp_path):
 def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
     """Each conv sweep layer at batch 64, as it runs inside a model, gets its kernel family."""
     want = {"stem": "conv_stem", "conv3x3s2_16": "conv_s2p", "conv3x3s2_32": "conv_s2p", "conv3x3s2": "conv_igemm",
-            "conv3x3s1_64": "conv_res", "conv3x3s1_128": "conv_pipe", "conv3x3s1": "conv_halo", "dw": "dwconv"}
+            "conv3x3s1_64": "conv_res", "conv3x3s1_128": "conv_wide", "conv3x3s1_256": "conv_wide", "dw": "dwconv"}
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=k, s=s, groups=g, act=act,
                              pre_relu=not name.startswith("stem"), post_relu=True)
     m = ia.PlanModel(path, 0, 64, DRY)
@@ -163,16 +170,20 @@ def test_kernel_choice_sweep(tmp_path, name, cin, cout, H, W, k, s, g, act):
 # 3x3 layers on LDS-patch configs 3 (32-channel chunks) and 7 (64-channel chunks); these
 # small-batch shapes reach the same configs, and the 1x1 shape reaches 769..1024 output tiles
 # of the 128-wide im2col tile, the case of its 128-VGPR build.
+NW = ia.IVH_FLAG_NO_WIDE
 TAGGED = [
-    ((128, 128, 160, 3, 2), "conv_halo cfg=7", "ck=64", 0),
+    ((128, 128, 160, 3, 2), "conv_halo cfg=7", "ck=64", NW),
     ((96, 136, 96, 3, 2), "conv_halo cfg=7", "ck=64", 0),
-    ((128, 128, 224, 3, 2), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE),
-    ((128, 128, 40, 3, 64), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE),
-    ((256, 256, 20, 3, 64), "conv_halo cfg=7", "ck=64", 0),
+    ((128, 128, 224, 3, 2), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE | NW),
+    ((128, 128, 40, 3, 64), "conv_halo cfg=3", "ck=32", ia.IVH_FLAG_NO_PIPE | NW),
+    ((256, 256, 20, 3, 64), "conv_halo cfg=7", "ck=64", NW),
     ((128, 128, 160, 1, 4), "conv_igemm bn=128 bk=32 ksplit=1", "vgpr128", 0),
-    ((128, 128, 40, 3, 64), "conv_pipe cfg=0", "items=438", 0),
+    ((128, 128, 40, 3, 64), "conv_pipe cfg=0", "items=438", NW),
     ((128, 64, 40, 3, 64), "conv_pipe cfg=1", "items=410", 0),
     ((64, 64, 80, 3, 2), "conv_pipe cfg=1", "items=54", ia.IVH_FLAG_PIPE_ANY),
+    ((128, 128, 40, 3, 64), "conv_wide tm=13", "ranges=256", 0),
+    ((256, 256, 20, 3, 64), "conv_wide tm=7", "ranges=128", 0),
+    ((128, 128, 160, 3, 2), "conv_wide tm=4", "wgs=256", 0),
 ]
 
 
