@@ -2,9 +2,23 @@
 // fp16 MFMA shapes behind one interface, the activation formulas and the fused epilogue.
 #pragma once
 
+#include <type_traits>
+
 #include "ivh_internal.hpp"
 
 namespace ivh {
+
+// fn(integral_constant<int, i>) for i = B .. E - 1: a loop the compiler cannot leave rolled
+template <int B, int E, class Fn> __device__ __forceinline__ void static_for(Fn && fn)
+{
+  if constexpr (B < E) {
+    fn(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(fn);
+  }
+}
+
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding)
+constexpr int kVmWait0 = (0x7 << 4) | (0xf << 8);
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));

@@ -292,7 +292,7 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
   // 35 vs 30 us); with Cin <= 16 the two are even (16->16 at 160x160: 49 vs 51 us).
   if (p.K == 3 && p.S == 1 && p.P == 1 && !(s.flags & IVH_FLAG_NO_RESIDENT) && p.Cin > 16 &&
       !(p.r.ptr && p.Cin <= 32) && res_views_ok(p) &&
-      res_plan(p.Cin, p.Cout, p.H, p.W, batch, p.act, &hc, &th, &tw)) {
+      res_plan(p.Cin, p.Cout, p.H, p.W, batch, p.act, !(s.flags & IVH_FLAG_NO_PINGPONG), &hc, &th, &tw)) {
     const int ck = res_ck(p.Cin), hi = halo_index(ck);
     if (pk.halo[hi] != kNoSeg && pk.kpad_halo[hi] == halo_taps(ck) * ck) {
       ConvParams q = p;

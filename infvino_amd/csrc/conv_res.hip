@@ -380,6 +380,328 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
   }
 }
 
+// ---------------------------------------------------------------- ping-pong variant
+//
+// 32 < Cin <= 64 with Cin % 8 == 0 and Cout > 32: the same convolution, tiles (BN = 64
+// output channels per work-group) and epilogue, with the two waves of every SIMD taking
+// turns instead of each interleaving its own epilogue with its own MFMAs (measured on
+// gfx950: a wave's VALU work and its MFMAs
+// barely overlap, while one wave's VALU work runs under another wave's MFMAs at almost full
+// speed for both).  The eight waves form two groups of four (waves 0-3 and 4-7, one wave of
+// each per SIMD) and a work-group's tiles alternate between the groups.  In phase k the
+// group owning tile k runs all of its MFMAs -- each wave 64 pixels x 64 channels, 2 x 2
+// blocks of 32 x 32, so every fragment read from LDS feeds two MFMAs -- while the other
+// group stores tile k - 1 from its accumulators (bias, activation, one fp16 rounding,
+// residual) and copies the input patch of its next tile, k + 1, into its own LDS buffer by
+// buffer loads with the LDS flag (no VGPR round trip); one barrier ends the phase.
+// LDS: the resident weights (64 rows of 9 x 64 fp16, pitch 584: conflict-free A reads), two
+// patch buffers and the bias.  A patch buffer holds up to 324 pixels as dense 128-byte rows
+// of eight 16-byte pieces (8 channels each); piece q of patch pixel (py, px) sits at
+// position q ^ (bits 1..3 of py * TW + px), so the 16 lanes of a B-fragment read quarter --
+// 16 consecutive tile pixels, whose py * TW + px are 16 consecutive integers -- hit 16
+// distinct 16-byte bank groups with no padding (two buffers and the weights fill 158 KB).
+namespace {
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kPpLdk = 9 * 64 + 8;   // weight row pitch (halves)
+constexpr int kPpPix = 324;          // patch pixels per buffer
+constexpr int kPpSlots = 2624;       // patch buffer slots: 41 DMA instructions of 64 >= 8 * 324
+constexpr int kPpDmaPerWave = 11;    // patch DMA instructions per wave (4 waves x 11 >= 41)
+constexpr int kPpWDma = 73;          // weight DMA instructions: 64 rows x 73 slots (72 + pad)
+
+__device__ __forceinline__ void pp_dma16(__amdgpu_buffer_rsrc_t r, void * lds, unsigned voff)
+{
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, (int)voff, 0, 0, 0);
+}
+}  // namespace
+
+template <int ACT, bool RES, int SM>
+__global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p)
+{
+  using F = Mf<32>;
+  typedef F::acc_t acc_t;
+  constexpr int BN = 64, TM = 2, TN = 2, NSL = 36, LDK = kPpLdk;
+  constexpr int NG = TN * TM * 4;            // epilogue groups (4 accumulator values) per lane
+  constexpr int NE = SM == 2 ? NG / 2 : NG;  // epilogue steps
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[64 * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 P0[kPpSlots * 8];
+  __shared__ __attribute__((aligned(16))) _Float16 P1[kPpSlots * 8];
+  __shared__ __attribute__((aligned(16))) float bias_s[BN];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = wave & 3;  // position in the group (the SIMD it shares with its partner)
+  const int TH = p.th, TW = p.tw, PW = TW + 2, PP = (TH + 2) * PW;
+  const int Hs = p.H + 1;
+  const int tiles_x = (p.W + TW - 1) / TW;
+  const int ntiles = ((p.batch * Hs - 1 + TH - 1) / TH) * tiles_x;
+  const int G = gridDim.x;
+  const int r = xcd_tile(blockIdx.x, G);
+  const int t_lo = (int)((long)r * ntiles / G), t_hi = (int)((long)(r + 1) * ntiles / G);
+  const int ntl = t_hi - t_lo;
+  if (ntl <= 0) return;
+  const int n0 = blockIdx.y * BN;
+  const float inv_tw = __builtin_amdgcn_rcpf((float)TW), inv_pw = __builtin_amdgcn_rcpf((float)PW);
+
+  const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
+
+  // ---- prologue: weights into LDS by DMA (slot s = row s / 73, piece s % 73; piece 72 is
+  // the row's pad), bias
+#pragma unroll
+  for (int u = 0; u < (kPpWDma + 7) / 8; ++u) {
+    const int ins = u * 8 + wave;
+    if (ins < kPpWDma) {
+      const unsigned s = (unsigned)(ins * 64 + lane), row = s / 73u, c = s - row * 73u;
+      pp_dma16(wr, Ws + ins * 512, c < 72u ? (row * (unsigned)p.kpad + c * 8u) * 2u : kBufOOB);
+    }
+  }
+  if (tid < BN) bias_s[tid] = p.bias ? p.bias[n0 + tid] : 0.0f;
+
+  // patch slots of this lane's DMA instructions (instruction u * 4 + wg of its group covers
+  // slots 64 (u * 4 + wg) ..): patch row << 16 | column << 3 | channel piece, bit 12 = no
+  // input (slots past the patch)
+  const int ninst = (PP * 8 + 63) / 64;
+  unsigned pdesc[kPpDmaPerWave];
+#pragma unroll
+  for (int u = 0; u < kPpDmaPerWave; ++u) {
+    const int s = (u * 4 + wg) * 64 + lane, pp = s >> 3;
+    const int py = idiv_small(pp, PW, inv_pw), px = pp - py * PW;
+    const int q = (s & 7) ^ (((py * TW + px) >> 1) & 7);
+    pdesc[u] = pp < PP ? ((unsigned)py << 16) | ((unsigned)px << 3) | (unsigned)q : 1u << 12;
+  }
+  // tile t -> first output row (image b0, row r0 of it) and column of the tall image
+  auto tile_origin = [&](int t, int & b0, int & r0, int & ox0) __attribute__((always_inline)) {
+    const int ty = t / tiles_x;
+    const int oy0 = ty * TH;
+    b0 = oy0 / Hs;
+    r0 = oy0 - b0 * Hs;
+    ox0 = (t - ty * tiles_x) * TW;
+  };
+  const int xcs = p.x.cs, xwcs = p.W * p.x.cs;
+  const int xdelta = (int)p.x.img - Hs * xwcs;  // (b0 + 1, r - Hs) is at (b0, r) + xdelta
+  // patch of tile t into buffer P by this wave's DMA instructions; pixels outside the image,
+  // separator rows and pieces at or past Cin read zeros from past the buffer range
+  auto dma_patch = [&](int t, _Float16 * P) __attribute__((always_inline)) {
+    int b0, r0, ox0;
+    tile_origin(t, b0, r0, ox0);
+    int rb = r0 - 1, bb = b0;  // patch row 0 is output row - 1
+    if (rb < 0 && bb > 0) {
+      rb += Hs;
+      --bb;
+    }
+    const bool next_ok = bb + 1 < p.batch;
+    const int base = bb * (int)p.x.img + (rb * p.W + ox0 - 1) * xcs;
+#pragma unroll
+    for (int u = 0; u < kPpDmaPerWave; ++u) {
+      if (u * 4 + wg < ninst) {
+        unsigned d = pdesc[u];
+        __asm__ volatile("" : "+v"(d));  // decoded here, not hoisted out of the phase loop
+        const int py = (int)(d >> 16), px = (int)((d >> 3) & 511u), q = (int)(d & 7u);
+        const int rr = rb + py;
+        const bool wrap = rr >= Hs;
+        const int rw = wrap ? rr - Hs : rr;
+        const int ix = ox0 - 1 + px;
+        const bool ok = !(d & (1u << 12)) && (unsigned)rw < (unsigned)p.H && (unsigned)ix < (unsigned)p.W &&
+                        (!wrap || next_ok) && q * 8 < p.Cin;
+        const int off = base + __umul24(py, xwcs) + __umul24(px, xcs) + q * 8 + (wrap ? xdelta : 0);
+        pp_dma16(xr, P + (u * 4 + wg) * 512, ok ? (unsigned)off * 2u : kBufOOB);
+      }
+    }
+  };
+
+  // ---- per-lane fragment geometry (tile-independent): the wave's pixels are
+  // wg * 64 + tm * 32 + lane % 32 of the tile; a slot past the tile computes pixel 0
+  const int h16 = (lane >> 5) << 4;  // the lane's half of a 16-channel slice: piece 2 j + h
+  unsigned pb[TM], pv[TM];           // patch byte offset and tile-linear index at tap (0, 0)
+  int syx[TM];                       // output (row << 16 | column) in the tile
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int pl = wg * 64 + tm * 32 + F::col(lane);
+    const int pc = pl < TH * TW ? pl : 0;
+    const int ty = idiv_small(pc, TW, inv_tw), tx = pc - ty * TW;
+    pb[tm] = (unsigned)(ty * PW + tx) * 128u;
+    pv[tm] = (unsigned)(ty * TW + tx);
+    const int oy = idiv_small(pl, TW, inv_tw);
+    syx[tm] = pl < TH * TW ? (oy << 16) | (pl - oy * TW) : 0x7fff0000;
+  }
+  const int arow = ((lane & 31) * LDK + F::kq(lane)) * 2;  // A fragment byte offset at slice 0
+
+  // ---- output side (as in the resident-weight kernel)
+  const int cl0 = F::row(lane, 0);
+  const long y_last = (long)(p.batch - 1) * p.y.img + ((long)p.H * p.W - 1) * p.y.cs +
+                      (SM == 2 ? (p.Cout + 7) & ~7 : SM == 1 ? (p.Cout + 3) & ~3 : p.Cout);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(p.y.ptr, (short)0, (int)(y_last * 2), kBufDword3);
+  const long r_last = RES ? (long)(p.batch - 1) * p.r.img + ((long)p.H * p.W - 1) * p.r.cs + p.Cout : 0;
+  const __amdgpu_buffer_rsrc_t rr_ = __builtin_amdgcn_make_buffer_rsrc(RES ? p.r.ptr : p.y.ptr, (short)0,
+                                                                       (int)(r_last * 2), kBufDword3);
+  auto out_offsets = [&](int t, unsigned (&yo)[TM], unsigned (&ro)[TM]) __attribute__((always_inline)) {
+    int b0, r0, ox0;
+    tile_origin(t, b0, r0, ox0);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      int rr = r0 + (syx[tm] >> 16), b = b0;
+      if (rr >= Hs) {  // TH + 2 <= Hs: at most one image boundary inside a tile
+        rr -= Hs;
+        ++b;
+      }
+      const int ox = ox0 + (syx[tm] & 0xffff);
+      const bool ok = rr < p.H && b < p.batch && ox < p.W;
+      const unsigned hw = (unsigned)(rr * p.W + ox);
+      yo[tm] = ok ? ((unsigned)b * (unsigned)p.y.img + hw * (unsigned)p.y.cs + (unsigned)n0) * 2u : kBufOOB;
+      if (RES) ro[tm] = ok ? ((unsigned)b * (unsigned)p.r.img + hw * (unsigned)p.r.cs + (unsigned)n0) * 2u : kBufOOB;
+    }
+  };
+  auto chan_off = [&](unsigned base, int cl) __attribute__((always_inline)) {
+    return n0 + cl < p.Cout ? base + (unsigned)cl * 2u : kBufOOB;
+  };
+  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
+      rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
+    }
+  };
+  // bias + activation in fp32, one rounding, then + residual (rounded again); the empty asm
+  // keeps every copy of this code on the same fp32 -> fp16 path
+  auto epi_vals = [&](const acc_t (&ac)[TN][TM], const h4 (&rv)[NG], int g) __attribute__((always_inline)) {
+    const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
+    const int cl = tn * 32 + cl0 + 2 * v4;
+    const float4 b4 = *reinterpret_cast<const float4 *>(bias_s + cl);
+    float o[4] = {act_fast<ACT>(ac[tn][tm][v4 + 0] + b4.x), act_fast<ACT>(ac[tn][tm][v4 + 1] + b4.y),
+                  act_fast<ACT>(ac[tn][tm][v4 + 2] + b4.z), act_fast<ACT>(ac[tn][tm][v4 + 3] + b4.w)};
+    h4 hv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      __asm__("" : "+v"(o[k]));
+      hv[k] = (_Float16)o[k];
+    }
+    if (RES) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = (_Float16)((float)hv[k] + (float)rv[g][k]);
+    }
+    return hv;
+  };
+  auto epi_step = [&](const acc_t (&ac)[TN][TM], const unsigned (&yo)[TM], const h4 (&rv)[NG], int e)
+      __attribute__((always_inline)) {
+    if (SM == 2) {
+      const int g = 2 * e;
+      const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
+      const u2 a = __builtin_bit_cast(u2, epi_vals(ac, rv, g));
+      const u2 b = __builtin_bit_cast(u2, epi_vals(ac, rv, g + 1));
+      const auto s0 = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+      const u4 q = {s0[0], s1[0], s0[1], s1[1]};
+      const int cl = tn * 32 + cl0 + 2 * v4 + 4 * (lane >> 5);
+      __builtin_amdgcn_raw_buffer_store_b128(q, yr, chan_off(yo[tm], cl), 0, 0);
+    } else {
+      const int tn = e / (TM * 4), tm = (e / 4) % TM, v4 = (e % 4) * 4;
+      const int cl = tn * 32 + cl0 + 2 * v4;
+      const h4 hv = epi_vals(ac, rv, e);
+      if (SM == 1) {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, hv), yr, chan_off(yo[tm], cl), 0, 0);
+      } else {
+        const u16x4 hu = __builtin_bit_cast(u16x4, hv);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) __builtin_amdgcn_raw_buffer_store_b16(hu[k], yr, chan_off(yo[tm], cl + k), 0, 0);
+      }
+    }
+  };
+
+  // ---- MFMA phase: the 36 K slices of one tile from buffer P, fragments read two slices
+  // ahead into a three-set register ring
+  auto mfma_tile = [&](const _Float16 * P, acc_t (&acc)[TN][TM]) __attribute__((always_inline)) {
+    const char * const Pb = reinterpret_cast<const char *>(P);
+    const char * const Wb = reinterpret_cast<const char *>(Ws) + arow;
+    // the per-tap offsets below are the same in every phase; computed afresh (a few VALU
+    // operations per tap) rather than hoisted out of the phase loop into 36+ live registers
+    unsigned pbt[TM], pvt[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      pbt[tm] = pb[tm];
+      pvt[tm] = pv[tm];
+      __asm__ volatile("" : "+v"(pbt[tm]), "+v"(pvt[tm]));
+    }
+    unsigned tb[TM], tk[TM];  // B byte offset and swizzled piece offset of the prefetch tap
+    auto set_tap = [&](int tap) __attribute__((always_inline)) {
+      const int dy = tap / 3, dx = tap % 3;
+      const unsigned boff = (unsigned)((dy * PW + dx) * 128), voff = (unsigned)(dy * TW + dx);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        tb[tm] = pbt[tm] + boff;
+        tk[tm] = ((((pvt[tm] + voff) >> 1) & 7u) << 4) ^ (unsigned)h16;
+      }
+    };
+    h8 fa[3][TN], fb[3][TM];
+    auto frags = [&](auto S) __attribute__((always_inline)) {
+      constexpr int s = decltype(S)::value, tap = s / 4, j = s % 4, k = s % 3;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        fa[k][tn] = *reinterpret_cast<const h8 *>(Wb + (tn * 32 * LDK + tap * 64 + j * 16) * 2);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        fb[k][tm] = *reinterpret_cast<const h8 *>(Pb + tb[tm] + (tk[tm] ^ (unsigned)(j << 5)));
+    };
+    set_tap(0);
+    frags(std::integral_constant<int, 0>{});
+    frags(std::integral_constant<int, 1>{});
+    static_for<0, NSL>([&](auto S) __attribute__((always_inline)) {
+      constexpr int s = decltype(S)::value, k = s % 3;
+      if constexpr (s + 2 < NSL) {
+        if constexpr ((s + 2) % 4 == 0) set_tap((s + 2) / 4);
+        frags(std::integral_constant<int, s + 2>{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+          acc[tn][tm] = F::mma(fa[k][tn], fb[k][tm], s == 0 ? acc_t{} : acc[tn][tm]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // the first tile's patch (group 0's buffer), then everything in LDS
+  if (wave < 4) dma_patch(t_lo, P0);
+  __builtin_amdgcn_s_waitcnt(kVmWait0);
+  __syncthreads();
+
+  // phase k = 0 .. ntl: the group of tile k (k % 2) runs its MFMAs; the other group stores
+  // tile k - 1 and copies the patch of tile k + 1 into its own buffer
+  auto run = [&](auto GRP) __attribute__((always_inline)) {
+    constexpr int g = decltype(GRP)::value;
+    _Float16 * const myP = g == 0 ? P0 : P1;
+    acc_t acc[TN][TM];
+    for (int k = 0; k <= ntl; ++k) {
+      if ((k & 1) == g) {
+        if (k < ntl) {
+          __builtin_amdgcn_s_setprio(1);
+          mfma_tile(myP, acc);
+          __builtin_amdgcn_s_setprio(0);
+        }
+      } else {
+        unsigned yo[TM], ro[TM];
+        h4 rv[NG];
+        if (k >= 1) {
+          out_offsets(t_lo + k - 1, yo, ro);
+          if (RES) load_res(ro, rv);
+        }
+        if (k + 1 < ntl) dma_patch(t_lo + k + 1, myP);
+        if (k >= 1) {
+#pragma unroll
+          for (int e = 0; e < NE; ++e) epi_step(acc, yo, rv, e);
+        }
+        __builtin_amdgcn_s_waitcnt(kVmWait0);
+      }
+      __syncthreads();
+    }
+  };
+  if (wave < 4) run(std::integral_constant<int, 0>{});
+  else run(std::integral_constant<int, 1>{});
+}
+
 // ---------------------------------------------------------------- host side
 
 namespace {
@@ -390,9 +712,11 @@ struct ResCfgDesc {
 //   0: 4 x 2 waves of 2 x 1 blocks (BM 256, BN 64; Cout > 32)
 //   1: 8 x 1 waves of 2 x 1 blocks (BM 512, BN 32; Cout <= 32, Cin <= 32)
 //   2: 8 x 1 waves of 1 x 1 blocks (BM 256, BN 32; Cout <= 32, Cin > 32)
-// Patch sizes keep resident weights + patch within the 160 KB of LDS at Cin 64.
+//   3: the ping-pong kernel, two groups of 4 waves of 2 x 2 blocks (BM 256, BN 64; Cout > 32,
+//      32 < Cin <= 64, Cin % 8 == 0)
+// Patch sizes keep resident weights + patch(es) within the 160 KB of LDS at Cin 64.
 constexpr int kResP0 = 352, kResP1 = 720, kResP2 = 352;
-constexpr ResCfgDesc kResCfg[3] = {{256, 64, kResP0}, {512, 32, kResP1}, {256, 32, kResP2}};
+constexpr ResCfgDesc kResCfg[4] = {{256, 64, kResP0}, {512, 32, kResP1}, {256, 32, kResP2}, {256, 64, kPpPix}};
 constexpr int kResCUs = 256;  // one work-group per CU
 }  // namespace
 
@@ -439,12 +763,12 @@ bool res_views_ok(const ConvParams & p)
   return p.H == p.Ho && p.W == p.Wo && (long)p.W * p.x.cs < (1L << 23);
 }
 
-bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw)
+bool res_plan(int cin, int cout, int H, int W, int batch, int act, bool pingpong, int * cfg, int * th, int * tw)
 {
   if (cin > 64 || cin <= 16 || H < 3 || W < 2 || (long)batch * (H + 1) >= (1L << 22) || W >= (1 << 22)) return false;
   if (act != kActNone && act != kActSiLU && act != kActReLU && act != kActHSwish) return false;
   const int ck = res_ck(cin);
-  const int c = cout > 32 ? 0 : (ck == 64 ? 2 : 1);
+  const int c = cout > 32 ? (pingpong && ck == 64 && cin % 8 == 0 ? 3 : 0) : (ck == 64 ? 2 : 1);
   const ResCfgDesc & d = kResCfg[c];
   const int nblk = (cout + d.bn - 1) / d.bn;
   long g = std::max(1, kResCUs / nblk);
@@ -507,6 +831,33 @@ static void launch_res_cfg(const ConvParams & p, int cfg, hipStream_t s)
   }
 }
 
+template <bool RES, int SM>
+static void launch_pp_act(const ConvParams & p, hipStream_t s)
+{
+  dim3 grid((unsigned)res_grid_x(p, 3), (unsigned)((p.Cout + 63) / 64), 1), block(512);
+  switch (p.act) {
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActSiLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActReLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActHSwish, RES, SM>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActNone, RES, SM>), grid, block, 0, s, p); break;
+  }
+}
+
+static void launch_pp(const ConvParams & p, hipStream_t s)
+{
+  const int sm = res_store_mode(p);
+  if (p.r.ptr) {
+    if (sm == 2) launch_pp_act<true, 2>(p, s);
+    else launch_pp_act<true, 1>(p, s);
+  } else if (sm == 2) {
+    launch_pp_act<false, 2>(p, s);
+  } else if (sm == 1) {
+    launch_pp_act<false, 1>(p, s);
+  } else {
+    launch_pp_act<false, 0>(p, s);
+  }
+}
+
 void launch_conv_res(const ConvParams & p, hipStream_t s)
 {
   const int bc = conv_batch_chunk(p);
@@ -520,6 +871,8 @@ void launch_conv_res(const ConvParams & p, hipStream_t s)
     else launch_res_cfg<4, 2, 2, 1, 64, kResP0>(p, cfg, s);
   } else if (cfg == 1) {
     launch_res_cfg<8, 1, 2, 1, 32, kResP1>(p, cfg, s);
+  } else if (cfg == 3) {
+    launch_pp(p, s);
   } else {
     launch_res_cfg<8, 1, 1, 1, 64, kResP2>(p, cfg, s);
   }

@@ -44,18 +44,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned u2w __attribute__((ext_vector_type(2)));
 typedef unsigned u4w __attribute__((ext_vector_type(4)));
 
-// fn(integral_constant<int, i>) for i = B .. E - 1: a loop the compiler cannot leave rolled
-template <int B, int E, class Fn> __device__ __forceinline__ void static_for(Fn && fn)
-{
-  if constexpr (B < E) {
-    fn(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(fn);
-  }
-}
-
-// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding)
-constexpr int kVmWait0 = (0x7 << 4) | (0xf << 8);
-
 // 16 bytes per lane from byte offset voff + soff (soff wave-uniform) into 64 consecutive
 // 16-byte LDS slots from lds
 __device__ __forceinline__ void dma16w(__amdgpu_buffer_rsrc_t r, _Float16 * lds, unsigned voff, int soff)

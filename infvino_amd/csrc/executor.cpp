@@ -2026,11 +2026,12 @@ void Model::validate(const Launch & l) const
       }
       if (p.res) {
         const int cfg = p.res - 1, ck = p.ck;
-        if (cfg < 0 || cfg > 2 || p.halo || p.s2 || ck != res_ck(p.Cin) || p.Cin > ck || p.K != 3 || p.S != 1 ||
+        if (cfg < 0 || cfg > 3 || p.halo || p.s2 || ck != res_ck(p.Cin) || p.Cin > ck || p.K != 3 || p.S != 1 ||
             p.P != 1 || p.ksplit != 1 || p.th < 1 || p.tw < 1 || p.Ho != p.H || p.Wo != p.W ||
             p.th * p.tw > res_bm(cfg) || (p.th + 2) * (p.tw + 2) > res_pmax(cfg) || p.th + 2 > p.H + 1 ||
             p.th + 2 > kResMaxRows ||
-            (cfg == 0) != (p.Cout > 32) || (cfg == 2) != (p.Cout <= 32 && ck == 64) || !res_views_ok(p))
+            (cfg == 0 || cfg == 3) != (p.Cout > 32) || (cfg == 2) != (p.Cout <= 32 && ck == 64) ||
+            (cfg == 3 && (ck != 64 || p.Cin % 8 || p.Cin != p.cin8)) || !res_views_ok(p))
           throw std::runtime_error("resident-weight conv geometry");
         if (p.kpad != halo_taps(ck) * ck) throw std::runtime_error("resident-weight packing");
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("resident-weight geometry too large");

@@ -42,7 +42,7 @@ int res_pmax(int cfg);
 long res_tiles(const ConvParams & p);
 int res_grid_x(const ConvParams & p, int cfg);
 // config and output tile th x tw for a layer at a batch size; false: not eligible
-bool res_plan(int cin, int cout, int H, int W, int batch, int act, int * cfg, int * th, int * tw);
+bool res_plan(int cin, int cout, int H, int W, int batch, int act, bool pingpong, int * cfg, int * th, int * tw);
 // the output (and residual) views suit the kernel's 8-byte channels-last buffer stores
 bool res_views_ok(const ConvParams & p);
 int res_store_width(const ConvParams & p);  // channels per output store: 8, 4 or 1 (padding absorbs the rounding up)

@@ -190,6 +190,49 @@ def test_res_residual_chain(tmp_path):
 
 
 @pytest.mark.parametrize("cin,cout,H,W,batch,act", [
+    (64, 64, 80, 80, 64, pw.ACT_SILU),    # the 64->64 @80 layer of the YOLO heads: 6-7 tiles per work-group
+    (64, 51, 80, 80, 16, pw.ACT_SILU),    # Cout 51 (the pose head): stores reach the view's padding
+    (48, 64, 33, 35, 6, pw.ACT_HSWISH),   # Cin 48: two 8-channel pieces read as zeros; odd map
+    (64, 96, 24, 24, 8, pw.ACT_SILU),     # two channel blocks, the second 32 channels wide
+    (40, 40, 20, 20, 3, pw.ACT_RELU),     # small maps: tiles across image boundaries
+    (64, 64, 40, 40, 1, pw.ACT_SILU),     # batch 1: eight work-groups of one tile each
+    (56, 128, 16, 16, 2, pw.ACT_SILU),    # 16x16: one tile column, two full channel blocks
+])
+def test_pingpong_conv3x3(tmp_path, cin, cout, H, W, batch, act):
+    """3x3 stride-1 convs with 32 < Cin <= 64, Cin % 8 == 0 and Cout > 32 through the
+    ping-pong resident-weight kernel (config 3) vs the oracle, and bit for bit vs the
+    single-group kernel (config 0): both accumulate every 32 x 32 block over the same K slices
+    in the same order and share the epilogue."""
+    path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=act, pre_relu=True, post_relu=True)
+    print(f"ping-pong conv {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
+    tags = _conv_tags(path, batch)
+    assert tags[0].startswith("conv_res cfg=3"), tags
+    assert _conv_tags(path, batch, ia.IVH_FLAG_NO_PINGPONG)[0].startswith("conv_res cfg=0")
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PINGPONG)
+    assert np.array_equal(got[0], other[0])
+
+
+def test_pingpong_residual_chain(tmp_path):
+    """Bottleneck chain of 64 channels at batch 24 (3x3 SiLU, 3x3 + residual, 3x3 without
+    activation + residual) through the ping-pong kernel's fused residual add."""
+    def build(pb):
+        x = pb.unary(pb.input("x", [1, 64, 40, 40]), pw.UN_RELU)
+        t = pb.conv(x, 64, 3)
+        t = pb.conv(t, 64, 3)
+        y = pb.binary(x, t, 0)
+        u = pb.conv(y, 64, 3, act=pw.ACT_NONE)
+        z = pb.binary(y, u, 0)
+        return pb.unary(z, pw.UN_RELU)
+    path = _small_plan(tmp_path, build)
+    tags = _conv_tags(path, 24)
+    assert len(tags) == 3 and all(t.startswith("conv_res cfg=3") for t in tags), tags
+    got = _check_f32(path, 24, lo=-1.0, ref_mode=False)
+    _, _, other = _run(path, 24, lo=-1.0, flags=ia.IVH_FLAG_NO_PINGPONG)
+    assert np.array_equal(got[0], other[0])
+
+
+@pytest.mark.parametrize("cin,cout,H,W,batch,act", [
     (128, 128, 40, 40, 2, pw.ACT_SILU),    # BN 128 (config 0), four 32-channel chunks
     (72, 64, 33, 35, 2, pw.ACT_SILU),      # BN 64, a last chunk of 8 channels, odd H and W
     (96, 136, 24, 40, 2, pw.ACT_SILU),     # two channel blocks, the second 8 channels wide
