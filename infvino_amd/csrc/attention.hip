@@ -44,8 +44,6 @@ namespace {
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 constexpr int kAttnWaves = 12;  // waves per work-group (three per SIMD)
-// s_waitcnt immediate for vmcnt(n) with the other counters left alone (gfx9 encoding)
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 }  // namespace
 
 // fp16 pair {a * s, b * s}, each product rounded once to fp16 (v_fma_mixlo / mixhi_f16 on

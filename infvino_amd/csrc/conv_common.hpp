@@ -19,6 +19,8 @@ template <int B, int E, class Fn> __device__ __forceinline__ void static_for(Fn 
 
 // s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding)
 constexpr int kVmWait0 = (0x7 << 4) | (0xf << 8);
+// s_waitcnt vmcnt(n), 0 <= n < 64, the other counters left alone
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));

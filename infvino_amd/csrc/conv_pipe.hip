@@ -51,9 +51,6 @@ constexpr int kPipeNW = 3;        // weight ring slots: a step's weights are cop
 constexpr int kPipePS = 10 - kPipeNW;  // steps of a chunk that copy the next chunk's patch
 constexpr int kPipeWGs = 512;     // persistent grid: two work-groups on each of 256 CUs
 
-// s_waitcnt immediate for vmcnt(n) with the other counters left alone (gfx9 encoding)
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
-
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, _Float16 * lds, unsigned voff, int soff)
 {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, soff, 0, 0);

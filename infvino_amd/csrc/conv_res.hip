@@ -383,17 +383,20 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1) conv3x3s1_res_kernel(const 
 // ---------------------------------------------------------------- ping-pong variant
 //
 // 32 < Cin <= 64 with Cin % 8 == 0 and Cout > 32: the same convolution, tiles (BN = 64
-// output channels per work-group) and epilogue, with the two waves of every SIMD taking
-// turns instead of each interleaving its own epilogue with its own MFMAs (measured on
-// gfx950: a wave's VALU work and its MFMAs
-// barely overlap, while one wave's VALU work runs under another wave's MFMAs at almost full
-// speed for both).  The eight waves form two groups of four (waves 0-3 and 4-7, one wave of
-// each per SIMD) and a work-group's tiles alternate between the groups.  In phase k the
-// group owning tile k runs all of its MFMAs -- each wave 64 pixels x 64 channels, 2 x 2
-// blocks of 32 x 32, so every fragment read from LDS feeds two MFMAs -- while the other
-// group stores tile k - 1 from its accumulators (bias, activation, one fp16 rounding,
-// residual) and copies the input patch of its next tile, k + 1, into its own LDS buffer by
-// buffer loads with the LDS flag (no VGPR round trip); one barrier ends the phase.
+// output channels per work-group) and epilogue, with the waves of every SIMD taking turns
+// instead of each interleaving its own epilogue with its own MFMAs (measured on gfx950: a
+// wave's VALU work and its own MFMAs barely overlap, while one wave's VALU work runs under
+// another wave's MFMAs at almost full speed for both).  Twelve waves form three groups of
+// four (waves 0-3, 4-7, 8-11: one wave of each per SIMD) and a work-group's tiles rotate
+// over the groups.  In phase k the group owning tile k runs all of its MFMAs -- each wave
+// 64 pixels x 64 channels, 2 x 2 blocks of 32 x 32, so every fragment read from LDS feeds
+// two MFMAs, with one fragment read issued behind each MFMA -- while the group that ran
+// tile k - 1 stores the first half of its outputs (activation, one fp16 rounding, residual;
+// the accumulators start from the bias) and the group of tiles k - 2 and k + 1 stores the
+// second half of tile k - 2 and copies the input patch of tile k + 1 into the buffer tile
+// k - 1 used, by buffer loads with the LDS flag (no VGPR round trip); one barrier ends the
+// phase.  So a tile's epilogue VALU work -- two transcendentals per SiLU output -- runs on
+// two waves per SIMD under the third wave's MFMAs, and output stores are never waited for.
 // LDS: the resident weights (64 rows of 9 x 64 fp16, pitch 584: conflict-free A reads), two
 // patch buffers and the bias.  A patch buffer holds up to 324 pixels as dense 128-byte rows
 // of eight 16-byte pieces (8 channels each); piece q of patch pixel (py, px) sits at
@@ -407,16 +410,32 @@ constexpr int kPpPix = 324;          // patch pixels per buffer
 constexpr int kPpSlots = 2624;       // patch buffer slots: 41 DMA instructions of 64 >= 8 * 324
 constexpr int kPpDmaPerWave = 11;    // patch DMA instructions per wave (4 waves x 11 >= 41)
 constexpr int kPpWDma = 73;          // weight DMA instructions: 64 rows x 73 slots (72 + pad)
+constexpr int kPpGroups = 3;         // wave groups (one wave of each per SIMD)
 
 __device__ __forceinline__ void pp_dma16(__amdgpu_buffer_rsrc_t r, void * lds, unsigned voff)
 {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, (int)voff, 0, 0, 0);
 }
+
+typedef unsigned pp_u4 __attribute__((ext_vector_type(4)));
+// The same copy issued as inline assembly, so the compiler does not track it: its waitcnt
+// pass would otherwise make the next LDS read of any patch buffer wait for every vector
+// memory operation still in flight (the epilogue's output stores included).  The caller
+// waits for these copies itself (s_waitcnt vmcnt) before the barrier that publishes them.
+// rs: the buffer descriptor; lds: the LDS byte address of the 64 destination slots.
+__device__ __forceinline__ void pp_dma16_untracked(pp_u4 rs, unsigned lds, unsigned voff)
+{
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                   :
+                   : "v"(voff), "s"(rs), "s"(lds)
+                   : "memory", "m0");
+}
 }  // namespace
 
-template <int ACT, bool RES, int SM>
-__global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p)
+template <int NGRP, int ACT, bool RES, int SM>
+__global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvParams p)
 {
+  static_assert(NGRP == 3, "three wave groups");
   using F = Mf<32>;
   typedef F::acc_t acc_t;
   constexpr int BN = 64, TM = 2, TN = 2, NSL = 36, LDK = kPpLdk;
@@ -447,13 +466,19 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
       const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
+  const unsigned long long xaddr = reinterpret_cast<unsigned long long>(p.x.ptr);
+  const pp_u4 xrs = {(unsigned)xaddr, (unsigned)(xaddr >> 32) & 0xffffu, (unsigned)(x_last * 2), (unsigned)kBufDword3};
 
   // ---- prologue: weights into LDS by DMA (slot s = row s / 73, piece s % 73; piece 72 is
   // the row's pad), bias
+  constexpr int NW = 4 * NGRP;  // waves
 #pragma unroll
-  for (int u = 0; u < (kPpWDma + 7) / 8; ++u) {
-    const int ins = u * 8 + wave;
-    if (ins < kPpWDma) {
+  for (int u = 0; u < (kPpWDma + NW - 1) / NW; ++u) {
+    const int i0 = u * NW + wave;
+    if (i0 < kPpWDma) {
+      // work-groups sharing an XCD (and its L2) start at different instructions, so their
+      // first requests spread over the whole weight block
+      const int ins = (i0 + (int)(blockIdx.x / kXcds) * 7) % kPpWDma;
       const unsigned s = (unsigned)(ins * 64 + lane), row = s / 73u, c = s - row * 73u;
       pp_dma16(wr, Ws + ins * 512, c < 72u ? (row * (unsigned)p.kpad + c * 8u) * 2u : kBufOOB);
     }
@@ -482,9 +507,10 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
   };
   const int xcs = p.x.cs, xwcs = p.W * p.x.cs;
   const int xdelta = (int)p.x.img - Hs * xwcs;  // (b0 + 1, r - Hs) is at (b0, r) + xdelta
-  // patch of tile t into buffer P by this wave's DMA instructions; pixels outside the image,
-  // separator rows and pieces at or past Cin read zeros from past the buffer range
-  auto dma_patch = [&](int t, _Float16 * P) __attribute__((always_inline)) {
+  // Source byte offsets of this wave's patch slots for tile t (fn(u, offset) for each of its
+  // instructions u): pixels outside the image, separator rows and pieces at or past Cin read
+  // zeros from past the buffer range.
+  auto patch_src = [&](int t, auto && fn) __attribute__((always_inline)) {
     int b0, r0, ox0;
     tile_origin(t, b0, r0, ox0);
     int rb = r0 - 1, bb = b0;  // patch row 0 is output row - 1
@@ -507,9 +533,19 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
         const bool ok = !(d & (1u << 12)) && (unsigned)rw < (unsigned)p.H && (unsigned)ix < (unsigned)p.W &&
                         (!wrap || next_ok) && q * 8 < p.Cin;
         const int off = base + __umul24(py, xwcs) + __umul24(px, xcs) + q * 8 + (wrap ? xdelta : 0);
-        pp_dma16(xr, P + (u * 4 + wg) * 512, ok ? (unsigned)off * 2u : kBufOOB);
+        fn(u, ok ? (unsigned)off * 2u : kBufOOB);
       }
     }
+  };
+  // patch of tile t into buffer P by DMA: tracked (the first tile) or not (in the phase loop)
+  auto dma_patch = [&](int t, _Float16 * P) __attribute__((always_inline)) {
+    patch_src(t, [&](int u, unsigned src) __attribute__((always_inline)) { pp_dma16(xr, P + (u * 4 + wg) * 512, src); });
+  };
+  auto dma_patch_untracked = [&](int t, _Float16 * P) __attribute__((always_inline)) {
+    const unsigned lds = (unsigned)reinterpret_cast<unsigned long>((__attribute__((address_space(3))) _Float16 *)P);
+    patch_src(t, [&](int u, unsigned src) __attribute__((always_inline)) {
+      pp_dma16_untracked(xrs, lds + (unsigned)((u * 4 + wg) * 1024), src);
+    });
   };
 
   // ---- per-lane fragment geometry (tile-independent): the wave's pixels are
@@ -557,9 +593,9 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
   auto chan_off = [&](unsigned base, int cl) __attribute__((always_inline)) {
     return n0 + cl < p.Cout ? base + (unsigned)cl * 2u : kBufOOB;
   };
-  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG]) __attribute__((always_inline)) {
+  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG], int g0, int g1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
+    for (int g = g0; g < g1; ++g) {
       const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
       rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
     }
@@ -568,10 +604,8 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
   // keeps every copy of this code on the same fp32 -> fp16 path
   auto epi_vals = [&](const acc_t (&ac)[TN][TM], const h4 (&rv)[NG], int g) __attribute__((always_inline)) {
     const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
-    const int cl = tn * 32 + cl0 + 2 * v4;
-    const float4 b4 = *reinterpret_cast<const float4 *>(bias_s + cl);
-    float o[4] = {act_fast<ACT>(ac[tn][tm][v4 + 0] + b4.x), act_fast<ACT>(ac[tn][tm][v4 + 1] + b4.y),
-                  act_fast<ACT>(ac[tn][tm][v4 + 2] + b4.z), act_fast<ACT>(ac[tn][tm][v4 + 3] + b4.w)};
+    float o[4] = {act_fast<ACT>(ac[tn][tm][v4 + 0]), act_fast<ACT>(ac[tn][tm][v4 + 1]),
+                  act_fast<ACT>(ac[tn][tm][v4 + 2]), act_fast<ACT>(ac[tn][tm][v4 + 3])};
     h4 hv;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -612,7 +646,7 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
 
   // ---- MFMA phase: the 36 K slices of one tile from buffer P, fragments read two slices
   // ahead into a three-set register ring
-  auto mfma_tile = [&](const _Float16 * P, acc_t (&acc)[TN][TM]) __attribute__((always_inline)) {
+  auto mfma_tile = [&](const _Float16 * P, unsigned poff, acc_t (&acc)[TN][TM]) __attribute__((always_inline)) {
     const char * const Pb = reinterpret_cast<const char *>(P);
     const char * const Wb = reinterpret_cast<const char *>(Ws) + arow;
     // the per-tap offsets below are the same in every phase; computed afresh (a few VALU
@@ -620,7 +654,7 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
     unsigned pbt[TM], pvt[TM];
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
-      pbt[tm] = pb[tm];
+      pbt[tm] = pb[tm] + poff;
       pvt[tm] = pv[tm];
       __asm__ volatile("" : "+v"(pbt[tm]), "+v"(pvt[tm]));
     }
@@ -647,59 +681,110 @@ __global__ void __launch_bounds__(512, 1) conv3x3s1_pp_kernel(const ConvParams p
     set_tap(0);
     frags(std::integral_constant<int, 0>{});
     frags(std::integral_constant<int, 1>{});
+    // the accumulators start from the bias: lane rows 8 i + 4 (lane / 32) + 0..3 of block tn
+    // are four consecutive channels
+    acc_t bias_v[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 b4 = *reinterpret_cast<const float4 *>(bias_s + tn * 32 + F::row(lane, 4 * i));
+        bias_v[tn][4 * i] = b4.x;
+        bias_v[tn][4 * i + 1] = b4.y;
+        bias_v[tn][4 * i + 2] = b4.z;
+        bias_v[tn][4 * i + 3] = b4.w;
+      }
     static_for<0, NSL>([&](auto S) __attribute__((always_inline)) {
       constexpr int s = decltype(S)::value, k = s % 3;
       if constexpr (s + 2 < NSL) {
         if constexpr ((s + 2) % 4 == 0) set_tap((s + 2) / 4);
         frags(std::integral_constant<int, s + 2>{});
       }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
-          acc[tn][tm] = F::mma(fa[k][tn], fb[k][tm], s == 0 ? acc_t{} : acc[tn][tm]);
+          acc[tn][tm] = F::mma(fa[k][tn], fb[k][tm], s == 0 ? bias_v[tn] : acc[tn][tm]);
+      // one fragment read and a VALU operation behind each MFMA: a lone wave issues them
+      // while the matrix pipe is busy instead of between MFMA groups
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
     });
   };
 
-  // the first tile's patch (group 0's buffer), then everything in LDS
-  if (wave < 4) dma_patch(t_lo, P0);
+  // the first tile's patch into buffer 0
+  const int grp = wave >> 2;
+  if (grp == 0) dma_patch(t_lo, P0);
   __builtin_amdgcn_s_waitcnt(kVmWait0);
   __syncthreads();
 
-  // phase k = 0 .. ntl: the group of tile k (k % 2) runs its MFMAs; the other group stores
-  // tile k - 1 and copies the patch of tile k + 1 into its own buffer
-  auto run = [&](auto GRP) __attribute__((always_inline)) {
-    constexpr int g = decltype(GRP)::value;
-    _Float16 * const myP = g == 0 ? P0 : P1;
-    acc_t acc[TN][TM];
-    for (int k = 0; k <= ntl; ++k) {
-      if ((k & 1) == g) {
-        if (k < ntl) {
-          __builtin_amdgcn_s_setprio(1);
-          mfma_tile(myP, acc);
-          __builtin_amdgcn_s_setprio(0);
-        }
-      } else {
-        unsigned yo[TM], ro[TM];
-        h4 rv[NG];
-        if (k >= 1) {
-          out_offsets(t_lo + k - 1, yo, ro);
-          if (RES) load_res(ro, rv);
-        }
-        if (k + 1 < ntl) dma_patch(t_lo + k + 1, myP);
-        if (k >= 1) {
-#pragma unroll
-          for (int e = 0; e < NE; ++e) epi_step(acc, yo, rv, e);
-        }
-        __builtin_amdgcn_s_waitcnt(kVmWait0);
-      }
-      __syncthreads();
-    }
+  // Phase k = 0 .. ntl + 1; group g has role (k - g) mod 3 in it:
+  //   0: the MFMAs of tile k (patch in buffer k % 2);
+  //   1: the first half of the epilogue of tile k - 1;
+  //   2: the patch of tile k + 1 -- the group's next tile -- into buffer (k + 1) % 2, which
+  //      tile k - 1 read in the phase before, and the second half of the epilogue of tile
+  //      k - 2.
+  // A tile's epilogue is spread over two phases and two waves per SIMD; output stores are
+  // never waited for.  Each group walks its roles in order (code per role, so registers live
+  // only where they are used).
+  const int nph = ntl + 2;
+  acc_t acc[TN][TM];
+  int k = 0;
+  auto epi_part = [&](int te, auto E0, auto E1) __attribute__((always_inline)) {
+    constexpr int e0 = decltype(E0)::value, e1 = decltype(E1)::value;
+    constexpr int g0 = SM == 2 ? 2 * e0 : e0, g1 = SM == 2 ? 2 * e1 : e1;  // groups of the steps
+    unsigned yo[TM], ro[TM];
+    h4 rv[NG];
+    out_offsets(t_lo + te, yo, ro);
+    if (RES) load_res(ro, rv, g0, g1);
+    static_for<e0, e1>([&](auto E) __attribute__((always_inline)) { epi_step(acc, yo, rv, E); });
   };
-  if (wave < 4) run(std::integral_constant<int, 0>{});
-  else run(std::integral_constant<int, 1>{});
+  // LDS hand-over only: no fence, so outstanding output stores do not hold the barrier
+  auto end_phase = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_barrier();
+    ++k;
+  };
+  auto role1 = [&]() __attribute__((always_inline)) {
+    if (k >= 1 && k - 1 < ntl) epi_part(k - 1, std::integral_constant<int, 0>{}, std::integral_constant<int, NE / 2>{});
+    end_phase();
+  };
+  auto role2 = [&]() __attribute__((always_inline)) {
+    const bool copy = k + 1 < ntl;
+    if (copy) {
+      if ((k + 1) & 1) dma_patch_untracked(t_lo + k + 1, P1);
+      else dma_patch_untracked(t_lo + k + 1, P0);
+    }
+    if (k >= 2 && k - 2 < ntl) {
+      epi_part(k - 2, std::integral_constant<int, NE / 2>{}, std::integral_constant<int, NE>{});
+      // the copies were issued before this part's stores, and vector memory operations
+      // complete in order: wait for all but the stores
+      constexpr int nst = (SM == 0 ? 4 : 1) * (NE - NE / 2);
+      __builtin_amdgcn_s_waitcnt(vm_wait(nst < 63 ? nst : 63));
+    } else {
+      __builtin_amdgcn_s_waitcnt(kVmWait0);
+    }
+    end_phase();
+  };
+  if (grp == 2) role1();
+  if (grp >= 1) role2();
+  while (k < nph) {
+    if (k < ntl) {
+      __builtin_amdgcn_s_setprio(1);
+      // one copy of the MFMA code for both buffers: buffer 1 as a byte offset from buffer 0
+      mfma_tile(P0, (k & 1) ? (unsigned)(reinterpret_cast<char *>(P1) - reinterpret_cast<char *>(P0)) : 0u, acc);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    end_phase();
+    if (k >= nph) break;
+    role1();
+    if (k >= nph) break;
+    role2();
+  }
 }
 
 // ---------------------------------------------------------------- host side
@@ -834,12 +919,13 @@ static void launch_res_cfg(const ConvParams & p, int cfg, hipStream_t s)
 template <bool RES, int SM>
 static void launch_pp_act(const ConvParams & p, hipStream_t s)
 {
-  dim3 grid((unsigned)res_grid_x(p, 3), (unsigned)((p.Cout + 63) / 64), 1), block(512);
+  constexpr int NGRP = kPpGroups;
+  dim3 grid((unsigned)res_grid_x(p, 3), (unsigned)((p.Cout + 63) / 64), 1), block(256 * NGRP);
   switch (p.act) {
-  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActSiLU, RES, SM>), grid, block, 0, s, p); break;
-  case kActReLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActReLU, RES, SM>), grid, block, 0, s, p); break;
-  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActHSwish, RES, SM>), grid, block, 0, s, p); break;
-  default: hipLaunchKernelGGL((conv3x3s1_pp_kernel<kActNone, RES, SM>), grid, block, 0, s, p); break;
+  case kActSiLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<NGRP, kActSiLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActReLU: hipLaunchKernelGGL((conv3x3s1_pp_kernel<NGRP, kActReLU, RES, SM>), grid, block, 0, s, p); break;
+  case kActHSwish: hipLaunchKernelGGL((conv3x3s1_pp_kernel<NGRP, kActHSwish, RES, SM>), grid, block, 0, s, p); break;
+  default: hipLaunchKernelGGL((conv3x3s1_pp_kernel<NGRP, kActNone, RES, SM>), grid, block, 0, s, p); break;
   }
 }
 

@@ -200,9 +200,11 @@ def test_res_residual_chain(tmp_path):
 ])
 def test_pingpong_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     """3x3 stride-1 convs with 32 < Cin <= 64, Cin % 8 == 0 and Cout > 32 through the
-    ping-pong resident-weight kernel (config 3) vs the oracle, and bit for bit vs the
-    single-group kernel (config 0): both accumulate every 32 x 32 block over the same K slices
-    in the same order and share the epilogue."""
+    ping-pong resident-weight kernel (config 3) vs the oracle, and vs the single-group kernel
+    (config 0): both accumulate every 32 x 32 block over the same K slices in the same order,
+    config 3 from the bias instead of zero, so the fp32 sums differ only in rounding and the
+    fp16 outputs by at most two units in the last place (two where the fp32 values straddle
+    a power of two)."""
     path, _ = pw.single_conv(str(tmp_path), cin, cout, H, W, k=3, s=1, act=act, pre_relu=True, post_relu=True)
     print(f"ping-pong conv {cin}->{cout} {H}x{W} batch {batch} act {act}", flush=True)
     tags = _conv_tags(path, batch)
@@ -210,7 +212,14 @@ def test_pingpong_conv3x3(tmp_path, cin, cout, H, W, batch, act):
     assert _conv_tags(path, batch, ia.IVH_FLAG_NO_PINGPONG)[0].startswith("conv_res cfg=0")
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
     _, _, other = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_PINGPONG)
-    assert np.array_equal(got[0], other[0])
+    _assert_ulp2(got[0], other[0])
+
+
+def _assert_ulp2(a, b):
+    """fp16 bit patterns of non-negative outputs (the plans end in a ReLU) at most 2 apart."""
+    d = np.abs(np.asarray(a).view(np.uint16).astype(np.int32) - np.asarray(b).view(np.uint16).astype(np.int32))
+    print(f"   vs config 0: {int((d > 0).sum())} of {d.size} outputs differ, max {int(d.max())} ulp")
+    assert d.max() <= 2 and (d > 0).mean() < 1e-2
 
 
 def test_pingpong_residual_chain(tmp_path):
@@ -229,7 +238,8 @@ def test_pingpong_residual_chain(tmp_path):
     assert len(tags) == 3 and all(t.startswith("conv_res cfg=3") for t in tags), tags
     got = _check_f32(path, 24, lo=-1.0, ref_mode=False)
     _, _, other = _run(path, 24, lo=-1.0, flags=ia.IVH_FLAG_NO_PINGPONG)
-    assert np.array_equal(got[0], other[0])
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(other[0]))
+    assert mean_rel < 1e-3 and max_rel < 5e-3
 
 
 @pytest.mark.parametrize("cin,cout,H,W,batch,act", [
