@@ -435,10 +435,10 @@ __device__ __forceinline__ void pp_dma16_untracked(pp_u4 rs, unsigned lds, unsig
 template <int NGRP, int ACT, bool RES, int SM>
 __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvParams p)
 {
-  static_assert(NGRP == 3, "three wave groups");
   using F = Mf<32>;
   typedef F::acc_t acc_t;
   constexpr int BN = 64, TM = 2, TN = 2, NSL = 36, LDK = kPpLdk;
+  static_assert(NGRP == 3 && TM == 2, "three wave groups, an epilogue part per pixel block");
   constexpr int NG = TN * TM * 4;            // epilogue groups (4 accumulator values) per lane
   constexpr int NE = SM == 2 ? NG / 2 : NG;  // epilogue steps
   __shared__ __attribute__((aligned(16))) _Float16 Ws[64 * LDK];
@@ -593,11 +593,13 @@ __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvP
   auto chan_off = [&](unsigned base, int cl) __attribute__((always_inline)) {
     return n0 + cl < p.Cout ? base + (unsigned)cl * 2u : kBufOOB;
   };
-  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG], int g0, int g1) __attribute__((always_inline)) {
+  // residual values of the groups of pixel block h (all channels)
+  auto load_res = [&](const unsigned (&ro)[TM], h4 (&rv)[NG], int h) __attribute__((always_inline)) {
 #pragma unroll
-    for (int g = g0; g < g1; ++g) {
+    for (int g = 0; g < NG; ++g) {
       const int tn = g / (TM * 4), tm = (g / 4) % TM, v4 = (g % 4) * 4;
-      rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
+      if (tm == h)
+        rv[g] = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr_, chan_off(ro[tm], tn * 32 + cl0 + 2 * v4), 0, 0));
     }
   };
   // bias + activation in fp32, one rounding, then + residual (rounded again); the empty asm
@@ -735,14 +737,18 @@ __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvP
   const int nph = ntl + 2;
   acc_t acc[TN][TM];
   int k = 0;
-  auto epi_part = [&](int te, auto E0, auto E1) __attribute__((always_inline)) {
-    constexpr int e0 = decltype(E0)::value, e1 = decltype(E1)::value;
-    constexpr int g0 = SM == 2 ? 2 * e0 : e0, g1 = SM == 2 ? 2 * e1 : e1;  // groups of the steps
+  // epilogue part H: the steps of pixel block H (all 64 channels, so every 128-byte output
+  // pixel is written within one phase and leaves L2 whole)
+  auto epi_part = [&](int te, auto H) __attribute__((always_inline)) {
+    constexpr int h = decltype(H)::value;
     unsigned yo[TM], ro[TM];
     h4 rv[NG];
     out_offsets(t_lo + te, yo, ro);
-    if (RES) load_res(ro, rv, g0, g1);
-    static_for<e0, e1>([&](auto E) __attribute__((always_inline)) { epi_step(acc, yo, rv, E); });
+    if (RES) load_res(ro, rv, h);
+    static_for<0, NE>([&](auto E) __attribute__((always_inline)) {
+      constexpr int e = decltype(E)::value, g = SM == 2 ? 2 * e : e;
+      if constexpr ((g / 4) % TM == h) epi_step(acc, yo, rv, e);
+    });
   };
   // LDS hand-over only: no fence, so outstanding output stores do not hold the barrier
   auto end_phase = [&]() __attribute__((always_inline)) {
@@ -750,7 +756,7 @@ __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvP
     ++k;
   };
   auto role1 = [&]() __attribute__((always_inline)) {
-    if (k >= 1 && k - 1 < ntl) epi_part(k - 1, std::integral_constant<int, 0>{}, std::integral_constant<int, NE / 2>{});
+    if (k >= 1 && k - 1 < ntl) epi_part(k - 1, std::integral_constant<int, 0>{});
     end_phase();
   };
   auto role2 = [&]() __attribute__((always_inline)) {
@@ -760,10 +766,10 @@ __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvP
       else dma_patch_untracked(t_lo + k + 1, P0);
     }
     if (k >= 2 && k - 2 < ntl) {
-      epi_part(k - 2, std::integral_constant<int, NE / 2>{}, std::integral_constant<int, NE>{});
+      epi_part(k - 2, std::integral_constant<int, 1>{});
       // the copies were issued before this part's stores, and vector memory operations
       // complete in order: wait for all but the stores
-      constexpr int nst = (SM == 0 ? 4 : 1) * (NE - NE / 2);
+      constexpr int nst = (SM == 0 ? 4 : 1) * (NE / 2);
       __builtin_amdgcn_s_waitcnt(vm_wait(nst < 63 ? nst : 63));
     } else {
       __builtin_amdgcn_s_waitcnt(kVmWait0);
