@@ -73,6 +73,9 @@ extern "C" {
 #define IVH_FLAG_NO_WIDE 0x40000u /* 3x3 stride-1 convs never use the wide-layer kernel */
 #define IVH_FLAG_NO_PINGPONG 0x80000u /* 3x3 stride-1 convs with Cin <= 64 never use the
                                          ping-pong resident-weight kernel */
+#define IVH_FLAG_NO_FUSE_UPSAMPLE 0x100000u /* run a 2x resize_nn whose output only feeds a
+                                               concat read by one 1x1 conv, instead of that
+                                               conv reading the resize's input directly */
 #define IVH_FLAG_NO_PW 0x20000u   /* 1x1 convs never use the streaming pointwise kernels */
 #define IVH_FLAG_PIPE_ANY 0x4000u /* 3x3 stride-1 convs use the DMA-pipelined kernel wherever it
                                      applies (Cin >= 32, any grid size), not only where it is

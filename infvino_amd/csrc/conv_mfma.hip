@@ -39,8 +39,12 @@ namespace ivh {
 // (the compile-time switch keeps the masking out of the common case).  XT: a 1x1 conv on
 // NCHW channel planes (p.xt): a thread's A piece is 8 consecutive pixels of one channel (one
 // 16-byte load along the plane), written transposed into the pixel rows of the LDS tile, so
-// the MFMA loop and the epilogue are those of the channels-last case.
-template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG, int OCC = 1, bool XT = false>
+// the MFMA loop and the epilogue are those of the channels-last case.  UP: a 1x1 conv over a
+// channel concat whose first p.cu channels are a 2x nearest upsample of p.xu (p.cu a multiple
+// of BK): the K steps below p.cu read pixel (oy / 2, ox / 2) of xu instead of x, so the
+// upsampled tensor is never written (the same values reach the same LDS rows as when the
+// concat is materialised, hence the same results bit for bit).
+template <int WGM, int WGN, int TM, int TN, int BK, int PF, bool RAG, int OCC = 1, bool XT = false, bool UP = false>
 __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p)
 {
   using F = Mf<32>;
@@ -81,8 +85,9 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
 
-  // A rows of this thread: image base offset and the input corner of the output pixel
-  int abase[A_IT], aiy[A_IT], aix[A_IT];
+  // A rows of this thread: image base offset and the input corner of the output pixel; UP:
+  // the element offset of the row's source pixel in xu (-1 past the batch)
+  int abase[A_IT], aiy[A_IT], aix[A_IT], uoff[UP ? A_IT : 1];
 #pragma unroll
   for (int i = 0; i < A_IT; ++i) {
     const unsigned pm = m0 + r0 + i * RPI;
@@ -92,12 +97,18 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
       abase[i] = b * (int)p.x.img;
       aiy[i] = oy * p.S - p.P;
       aix[i] = ox * p.S - p.P;
+      if constexpr (UP) uoff[i] = b * (int)p.xu.img + ((oy >> 1) * (p.W >> 1) + (ox >> 1)) * p.xu.cs;
     } else {
       abase[i] = 0;
       aiy[i] = -0x4000000;  // never inside the image
       aix[i] = 0;
+      if constexpr (UP) uoff[i] = -1;
     }
   }
+  // UP: the upsample source's range, its last pixel's first p.cu channels
+  const long u_last = UP ? (long)(p.batch - 1) * p.xu.img + ((long)(p.H >> 1) * (p.W >> 1) - 1) * p.xu.cs + p.cu : 0;
+  const __amdgpu_buffer_rsrc_t ur = __builtin_amdgcn_make_buffer_rsrc(
+      UP ? const_cast<__half *>(p.xu.ptr) : const_cast<__half *>(p.x.ptr), (short)0, (int)(u_last * 2), kBufDword3);
   // XT: piece i of this thread is channel xc[i] of the step, pixels m0 + 8 xg[i] .. + 7
   // (one image: its plane holds a multiple of 8 pixels); byte offset of the piece in step
   // 0, or past the buffer range for pixels past the batch
@@ -165,6 +176,21 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
       return;
     }
     aci[d] = ci;
+    if constexpr (UP) {
+      // a K step below p.cu lies wholly in the upsampled channels (p.cu % BK == 0)
+      if (kt * BK < p.cu) {
+#pragma unroll
+        for (int i = 0; i < A_IT; ++i) {
+          const unsigned off = uoff[i] >= 0 ? (unsigned)((uoff[i] + ci) * 2) : kBufOOB;
+          ra[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ur, off, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < B_IT; ++i)
+          rb[d][i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wr, bsrc[i], kt * BK * 2, 0));
+        advance();
+        return;
+      }
+    }
     const int ky = (int)(((unsigned)tap * kmul) >> 16), kx = tap - ky * p.K;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
@@ -288,17 +314,30 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const ConvParams p, 
 // Tile table: a small CDNA4 choice per op (BN from Cout; BM = 128 pixels).
 int igemm_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
 
+// What the UP build assumes: a 1x1 stride-1 conv on even maps, channels-last x and xu with
+// 16-byte channel pieces, the upsampled channels a whole number of K steps, no ragged tail
+bool upcat_ok(const ConvParams & p)
+{
+  return p.cu > 0 && p.K == 1 && p.S == 1 && p.P == 0 && p.G == 1 && p.H % 2 == 0 && p.W % 2 == 0 &&
+         p.Ho == p.H && p.Wo == p.W && p.cu < p.Cin && p.cu % p.bk == 0 && p.Cin % 8 == 0 && p.cin8 == p.Cin &&
+         !p.xt && !p.pw && !p.halo && !p.res && !p.pipe && !p.wide && !p.s2 && p.x.layout == kNHWC &&
+         p.xu.layout == kNHWC && p.xu.cs % 8 == 0 && p.xu.img % 8 == 0 && p.xu.cs >= p.cu &&
+         (reinterpret_cast<uintptr_t>(p.xu.ptr) & 15) == 0;
+}
+
 template <int WGM, int WGN, int TM, int TN, int BK, int PF, int OCC = 1>
 static void launch_t(const ConvParams & p, hipStream_t s)
 {
   using T = TileShape<32, WGM, WGN, TM, TN>;
   const long M = (long)p.batch * p.Ho * p.Wo;
   if (M >= (1L << 31) || p.K * p.K + 16 >= 65536 / p.K) throw std::runtime_error("implicit-GEMM conv geometry");
+  if (p.cu && !upcat_ok(p)) throw std::runtime_error("implicit-GEMM upsample-concat geometry");
   ConvParams q = p;
   q.dv_hwo = fastdiv_make((unsigned)(p.Ho * p.Wo));
   q.dv_wo = fastdiv_make((unsigned)p.Wo);
   dim3 grid((unsigned)((M + T::BM - 1) / T::BM), (unsigned)((p.Cout + T::BN - 1) / T::BN), (unsigned)p.ksplit);
   if (p.xt) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, 1, true>), grid, dim3(256), 0, s, q);
+  else if (p.cu) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, OCC, false, true>), grid, dim3(256), 0, s, q);
   else if (p.Cin & 7) hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, true>), grid, dim3(256), 0, s, q);
   else hipLaunchKernelGGL((conv_igemm_kernel<WGM, WGN, TM, TN, BK, PF, false, OCC>), grid, dim3(256), 0, s, q);
   if (p.ksplit > 1) {
@@ -383,7 +422,7 @@ int igemm_ksplit(long M, int cout, int kpad)
 // and 32-bit element offsets); every image of a chunk is independent of the others.
 int conv_batch_chunk(const ConvParams & p)
 {
-  const long per = std::max<long>(p.x.img * 2, 1);
+  const long per = std::max<long>(std::max(p.x.img, p.cu ? p.xu.img : 0L) * 2, 1);
   return (int)std::max<long>(1, std::min<long>(p.batch, ((1L << 31) - 1) / per - 1));
 }
 
@@ -394,6 +433,7 @@ ConvParams conv_batch_slice(const ConvParams & p, int b0, int nb)
   q.x.ptr += (long)b0 * p.x.img;
   q.y.ptr += (long)b0 * p.y.img;
   if (q.r.ptr) q.r.ptr += (long)b0 * p.r.img;
+  if (q.cu) q.xu.ptr += (long)b0 * p.xu.img;
   return q;
 }
 
@@ -417,8 +457,9 @@ std::string igemm_launch_tag(const ConvParams & p)
   else if (p.s2)
     snprintf(b, sizeof b, "cfg=%d th=%d tw=%d", p.s2 - 1, p.th, p.tw);
   else
-    snprintf(b, sizeof b, "bn=%d bk=%d ksplit=%d%s%s%s", igemm_bn(p.Cout), p.bk, p.ksplit,
-             igemm_occ4(p) ? " vgpr128" : "", p.xt ? " planar" : "", (p.Cin & 7) ? " cin-ragged" : "");
+    snprintf(b, sizeof b, "bn=%d bk=%d ksplit=%d%s%s%s%s", igemm_bn(p.Cout), p.bk, p.ksplit,
+             igemm_occ4(p) ? " vgpr128" : "", p.xt ? " planar" : "", (p.Cin & 7) ? " cin-ragged" : "",
+             p.cu ? " upsample-concat" : "");
   return b;
 }
 

@@ -212,6 +212,12 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
     }
     return kLaunchIgemm;
   }
+  // a 1x1 conv reading a fused 2x upsample (the executor's upsample-concat fusion): the
+  // implicit GEMM, the one family with that input
+  if (p.cu) {
+    if (!upcat_ok(p)) throw std::runtime_error("upsample-concat input geometry");
+    return kLaunchIgemm;
+  }
   // 1x1 stride 1 with Cout <= 64 on channels-last views: the streaming pointwise kernel of
   // conv_pw.hip when its 32-pixel blocks fill the persistent grid several times over, and
   // where it was measured faster than the implicit GEMM (MI355X, batch 64, kernel trace):

@@ -856,6 +856,56 @@ void Model::plan()
   skip_.assign(nodes_.size(), 0);
   assignViews();
   chooseLayouts();
+  fuseUpsample();
+}
+
+// Upsample-concat fusion (YOLO necks: nn.Upsample(2) -> Concat -> the C2f / C3k2 cv1 1x1):
+// when a 1x1 conv is the only reader of a zero-copy concat whose leading channels are the
+// output of a 2x nearest resize read by nothing else, the conv's implicit GEMM reads those
+// channels from the resize's input at (oy / 2, ox / 2) and the resize is not run, so the
+// upsampled tensor (4x its input) is neither written nor read back.  The other concat inputs
+// stay in the concat root, which the conv reads as before.
+void Model::fuseUpsample()
+{
+  up_src_.assign(nodes_.size(), -1);
+  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_REUSE | IVH_FLAG_NO_FUSE_UPSAMPLE | IVH_FLAG_DIRECT_ONLY)) return;
+  for (size_t k = 0; k < nodes_.size(); ++k) {
+    const PlanNode & n = nodes_[k];
+    if (n.op != "conv1x1" || n.ins.size() < 2 || n.ins[1] == "-") continue;
+    const Tensor & xt = *T_[n.ins[1]];
+    if (xt.kind != Tensor::kAct || xt.root < 0 || xt.producer < 0 || xt.users.size() != 1) continue;
+    const Root & Q = *roots_[xt.root];
+    if (Q.layout != kNHWC || xt.coff != 0 || xt.C != Q.C || xt.dims.size() != 4 || Q.H % 2 || Q.W % 2) continue;
+    const int c = xt.producer;
+    const PlanNode & cn = nodes_[c];
+    if (cn.op != "concat4" || !skip_[c] || cn.ins.empty() || cn.ins[0] == "-") continue;
+    const Tensor & ut = *T_[cn.ins[0]];
+    const int cu = cn.i("ca");
+    if (ut.kind != Tensor::kAct || ut.root != xt.root || ut.coff != 0 || ut.C != cu || ut.producer < 0 ||
+        ut.users.size() != 1 || ut.users[0] != c)
+      continue;
+    const int r = ut.producer;
+    const PlanNode & rn = nodes_[r];
+    if (rn.op != "resize_nn" || skip_[r] || std::max(1, rn.i("S", 2)) != 2 || rn.ins.empty()) continue;
+    const Tensor & at = *T_[rn.ins[0]];
+    if (at.kind != Tensor::kAct || at.root < 0 || roots_[at.root]->layout != kNHWC || at.C != cu ||
+        rn.i("C") != cu || rn.i("H") * 2 != Q.H || rn.i("W") * 2 != Q.W || (long)at.H * at.W != (long)rn.i("H") * rn.i("W") ||
+        at.coff % 8 || roots_[at.root]->cs % 8)
+      continue;
+    // the conv's geometry the implicit GEMM's upsample build needs (upcat_ok at launch)
+    const Tensor & wt = *T_[n.ins[0]];
+    const int cin = (int)wt.dims[1], cout = (int)wt.dims[0];
+    if (cin != Q.C || cin % 8 || cu % igemm_bk(cout, cin) || cu >= cin) continue;
+    // nothing else may read the concat root's upsampled channels
+    bool alone = true;
+    for (const auto & kv : T_) {
+      const Tensor & t = *kv.second;
+      if (&t != &xt && &t != &ut && t.kind == Tensor::kAct && t.root == xt.root && t.coff < cu) alone = false;
+    }
+    if (!alone) continue;
+    up_src_[k] = r;
+    skip_[r] = 1;
+  }
 }
 
 // Views: every activation tensor gets a root; reshape/flatten alias, copy_c is a channel
@@ -1130,6 +1180,13 @@ void Model::allocate()
     const Tensor & yt = *T_[nodes_[nj].outs[0]];
     if (xt.root >= 0 && xt.kind != Tensor::kInit) roots_[xt.root]->last = std::max(roots_[xt.root]->last, nj);
     if (yt.root >= 0) roots_[yt.root]->first = std::min(roots_[yt.root]->first, ni);
+  }
+  // a conv with a fused upsample reads the resize's input at its own node
+  for (int ni = 0; ni < N; ++ni) {
+    const int r = up_src_[ni];
+    if (r < 0) continue;
+    const Tensor & at = *T_[nodes_[r].ins[0]];
+    roots_[at.root]->last = std::max(roots_[at.root]->last, ni);
   }
   // best-fit placement, largest first, on closed [first, last] intervals
   std::vector<int> order;
@@ -1468,6 +1525,11 @@ Launch Model::convLaunch(size_t ni, int batch)
       const Tensor & rt = *T_[n.ins[3]];
       if (rt.numel != yt.numel) fail("residual numel mismatch");
       p.r = view(rt.name, batch);
+    }
+    if (up_src_[ni] >= 0) {
+      const PlanNode & rn = nodes_[up_src_[ni]];
+      p.xu = view(rn.ins[0], batch);
+      p.cu = rn.i("C");
     }
     // single-pixel tensors: NCHW and NHWC coincide; present them channels-last
     auto pix1 = [](View & v, int C) { v.layout = kNHWC; v.cs = (int)round_up(C, 8); };
@@ -1896,6 +1958,8 @@ const Model::LaunchPlan & Model::launches(int batch)
   P.begin.assign(nodes_.size(), 0);
   P.end.assign(nodes_.size(), 0);
   P.covered.assign(nodes_.size(), 0);
+  for (int r : up_src_)
+    if (r >= 0) P.covered[r] = 1;  // the conv reading the resize's input does its work
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     P.begin[ni] = P.L.size();
     if (!skip_[ni] && !P.covered[ni]) emitNode(ni, batch, P.L, P.covered);
@@ -1995,6 +2059,7 @@ void Model::validate(const Launch & l) const
     const ConvParams & p = l.cp;
     const long HW = (long)p.H * p.W, HWo = (long)p.Ho * p.Wo;
     if (p.batch < 1 || p.batch > 65535) throw std::runtime_error("batch out of grid range");
+    if (p.cu && l.kind != Launch::kIgemm) throw std::runtime_error("upsample-concat input outside the implicit GEMM");
     // the resident-weight, pipelined and persistent stride-2 kernels write 4- or 8-channel
     // groups into the view's padding channels
     check(p.y.ptr, 0, vlast(p.y, p.batch, p.Cout + (p.res || p.pipe || p.wide || p.s2 > 2 || p.pw == 1 ? (res_store_width(p) - p.Cout % res_store_width(p)) % res_store_width(p) : 0), HWo), 2,
@@ -2011,6 +2076,10 @@ void Model::validate(const Launch & l) const
       } else {
         if (p.x.layout != kNHWC) throw std::runtime_error("igemm needs channels-last input");
         check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "igemm x");
+      }
+      if (p.cu) {
+        if (!upcat_ok(p)) throw std::runtime_error("igemm upsample-concat geometry");
+        check(p.xu.ptr, 0, vlast(p.xu, p.batch, p.cu, HW / 4), 2, "igemm upsample source");
       }
       const long rows = (long)(p.Cout + igemm_bn(p.Cout) - 1) / igemm_bn(p.Cout) * igemm_bn(p.Cout);
       check(p.w, 0, rows * p.kpad - 1, 2, "igemm w");
@@ -2414,6 +2483,9 @@ bool Model::readTensorF16(const std::string & name, uint16_t * host, int batch)
   auto it = T_.find(name);
   if (it == T_.end()) return false;
   check_batch(batch, max_batch_);
+  if (it->second->producer >= 0 && nodes_[it->second->producer].op == "resize_nn" && skip_[it->second->producer])
+    throw std::runtime_error("tensor " + name + " is not materialised: its upsample is fused into the 1x1 conv reading it "
+                             "(IVH_FLAG_NO_FUSE_UPSAMPLE or IVH_FLAG_NO_REUSE keeps it)");
   HIPCHECK(hipSetDevice(device_));
   HIPCHECK(hipStreamSynchronize(stream_));
   const Tensor & t = *it->second;

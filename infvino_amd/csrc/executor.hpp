@@ -105,6 +105,10 @@ class Model {
   int chanBroadcast(const PlanNode & n) const;
   void assignViews();
   void chooseLayouts();
+  // 1x1 convs reading concat(resize_nn x2 (a), b...): up_src_[ni] = the resize node whose work
+  // conv ni does by reading a directly (that resize emits nothing), else -1
+  void fuseUpsample();
+  std::vector<int> up_src_;
   void allocate();
   void uploadWeights();
   void buildStats();

@@ -99,6 +99,11 @@ struct ConvParams {
   // multiple of 8): each thread loads 8 consecutive pixels of one channel and writes them
   // transposed into the tile's pixel rows in LDS (0: channels-last input)
   int xt = 0;
+  // implicit GEMM of a 1x1 conv over a channel concat whose first cu channels are a 2x
+  // nearest upsample (0: none): those channels are read from xu, channels-last at
+  // (H / 2) x (W / 2), at pixel (oy / 2, ox / 2); channels cu.. from x as usual
+  View xu;
+  int cu = 0;
   // divisions by Ho * Wo and by Wo (set by the implicit-GEMM launcher)
   FastDiv dv_hwo, dv_wo;
 };

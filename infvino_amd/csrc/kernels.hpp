@@ -12,6 +12,7 @@ namespace ivh {
 // conv_mfma.hip
 int igemm_bn(int cout);                    // N tile of the implicit GEMM for a Cout
 int igemm_bk(int cout, int kk);            // K step of a layer with K*K*cin8 = kk (32 / 64)
+bool upcat_ok(const ConvParams & p);      // the implicit GEMM's upsample-concat input applies
 int igemm_kpad(int cout, int kk);          // packed K: kk rounded up to that step
 constexpr int kIgemmBK = 32;               // packed K is always a multiple of this
 constexpr int kIgemmRowPad = 128;          // packed weight rows padded to this multiple

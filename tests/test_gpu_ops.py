@@ -851,3 +851,41 @@ def test_gemm_op(tmp_path, M, N, K, bdims):
         mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(refr[0]))
         print(f"   vs reference-rounding oracle mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
         assert mean_rel < OP_MEAN and max_rel < OP_MAX
+
+
+def _upcat_plan(d, ca, cb, cout, H, W, reuse_a):
+    """concat(resize_nn x2 (a), b) -> 1x1 conv, as a YOLO neck's Upsample / Concat / C2f cv1;
+    a (ca channels at H x W) and b (cb channels at 2H x 2W) are internal channels-last
+    tensors.  reuse_a: a is read again later (the neck's second concat), so it stays live."""
+    def build(pb):
+        x = pb.input("x", [1, cb, 2 * H, 2 * W])
+        b = pb.conv(x, cb, 1, act=pw.ACT_RELU)
+        a = pb.conv(b, ca, 3, 2, act=pw.ACT_SILU)
+        y = pb.conv(pb.concat([pb.upsample(a, 2), b]), cout, 1, act=pw.ACT_SILU)
+        if reuse_a:
+            z = pb.conv(y, ca, 3, 2, act=pw.ACT_SILU)
+            y = pb.conv(pb.concat([z, a]), cout, 1, act=pw.ACT_SILU)
+        return y
+    return _small_plan(d, build)
+
+
+@pytest.mark.parametrize("ca,cb,cout,H,W,batch,reuse_a,fused", [
+    (128, 64, 64, 10, 12, 3, True, True),     # YOLOv8n P3 neck shape class (192 -> 64)
+    (256, 128, 128, 5, 6, 2, False, True),    # P4 neck class (384 -> 128), split-K
+    (64, 40, 48, 7, 5, 5, False, True),       # odd maps, Cout not a tile multiple
+    (64, 32, 32, 20, 20, 1, True, True),      # batch 1
+    (40, 24, 32, 6, 6, 2, False, False),      # 40 upsampled channels: not a whole K step
+])
+def test_upsample_concat_fused(tmp_path, ca, cb, cout, H, W, batch, reuse_a, fused):
+    """The 1x1 conv reads the upsampled channels from the resize's input: same bits as the
+    materialised concat (the same implicit GEMM, the same values in the same LDS rows)."""
+    path = _upcat_plan(tmp_path, ca, cb, cout, H, W, reuse_a)
+    fl = ia.IVH_FLAG_NO_PW  # both runs on the implicit GEMM, which the fused conv always uses
+    tags = _conv_tags(path, batch, fl)
+    assert sum("upsample-concat" in t for t in tags) == (1 if fused else 0), tags
+    assert ("resize_nn" in _kernels(path, batch, fl)) == (not fused)
+    assert not any("upsample-concat" in t for t in _conv_tags(path, batch, fl | ia.IVH_FLAG_NO_FUSE_UPSAMPLE))
+    _, _, got = _run(path, batch, lo=-1.0, flags=fl)
+    _, _, ref = _run(path, batch, lo=-1.0, flags=fl | ia.IVH_FLAG_NO_FUSE_UPSAMPLE)
+    assert np.array_equal(got[0], ref[0])
+    _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=fl)

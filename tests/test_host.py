@@ -530,3 +530,25 @@ def test_host_sanitizers(plans, tmp_path):
     r = subprocess.run([exe] + good + ["--"] + bad, capture_output=True, text=True, env=env, timeout=600)
     print(r.stdout[-2000:], r.stderr[-4000:])
     assert r.returncode == 0 and "0 failures" in r.stdout
+
+
+@pytest.mark.parametrize("name", ["yolov8n-pose", "yolo11n-pose"])
+def test_upsample_concat_fusion(plans, name):
+    """Both neck upsamples (Upsample -> Concat -> the C2f / C3k2 cv1 1x1) fold into their 1x1
+    conv at every batch size; IVH_FLAG_NO_FUSE_UPSAMPLE (and IVH_FLAG_NO_REUSE, which promises
+    readable intermediates) keep the resize launches."""
+    path = plans(name)[0]
+    for flags, fused in ((0, True), (ia.IVH_FLAG_NO_FUSE_UPSAMPLE, False), (ia.IVH_FLAG_NO_REUSE, False)):
+        m = ia.PlanModel(path, 0, 64, DRY | flags)
+        for b in (1, 64):
+            m.run(b)
+            info = [m.nodeInfo(i) for i in range(m.nodeCount())]
+            tags = [m.nodeTag(i) for i in range(m.nodeCount())]
+            resize = [i["kernel"] for i in info if i["op"] == "resize_nn"]
+            assert len(resize) == 2
+            assert resize == (["(fused)"] * 2 if fused else ["resize_nn"] * 2), resize
+            up = [i["desc"] for i, t in zip(info, tags) if "upsample-concat" in t]
+            want = {"yolov8n-pose": ["conv1x1 384x40x40->128x40x40", "conv1x1 192x80x80->64x80x80"],
+                    "yolo11n-pose": ["conv1x1 384x40x40->128x40x40", "conv1x1 256x80x80->64x80x80"]}[name]
+            assert [d.split(" k1")[0] for d in up] == (want if fused else []), up
+        m.close()
