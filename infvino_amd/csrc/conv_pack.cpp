@@ -218,13 +218,16 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
     if (!upcat_ok(p)) throw std::runtime_error("upsample-concat input geometry");
     return kLaunchIgemm;
   }
-  // 1x1 stride 1 with Cout <= 64 on channels-last views: the streaming pointwise kernel of
+  // 1x1 stride 1 with Cout <= 128 on channels-last views: the streaming pointwise kernel of
   // conv_pw.hip when its 32-pixel blocks fill the persistent grid several times over, and
   // where it was measured faster than the implicit GEMM (MI355X, batch 64, kernel trace):
   // every Cout <= 32 (32->32 at 160x160: 37.5 vs 46.4 us, 48->32: 49.2 vs 53.0), Cout <= 64
   // with K <= 96 (64->64 at 80x80: 24.2 vs 25.9, 96->64: 28.8 vs 31.8) or K = 128 at 80x80
   // and up (33.4 vs 35.0).  The implicit GEMM stays faster for 48->64 at 160x160 (99.7 vs
-  // 104.0), 192->64 at 80x80 (44.8 vs 47.3) and 128->64 at 40x40 (12.0 vs 13.3).
+  // 104.0), 192->64 at 80x80 (44.8 vs 47.3) and 128->64 at 40x40 (12.0 vs 13.3).  With
+  // 64 < Cout <= 128 (four 32-channel blocks per wave) only for K <= 96: 96->128 at 80x80
+  // 53.6 -> 50.6 us, while 128->128 and 192->128 at 40x40 are slower (20.2 -> 23.3, 21.1 ->
+  // 23.7 us).
   // 1x1 from channels-last x to NCHW planes (the heads' last convs, whose outputs are graph
   // tensors): the planar-output streaming kernel, measured against the implicit GEMM on
   // MI355X (YOLOv8n-pose heads, batch 64 / 1): 51->51 at 80x80 22.5 -> 18.5 / 5.8 -> 4.6 us,
@@ -238,7 +241,7 @@ int conv_resolve(const ConvSpec & s, const ConvPacking & pk, const void * dev_bl
     return kLaunchIgemm;
   }
   const bool pw_wins = p.Cout <= 32 || (p.cin8 <= 96 && p.cin8 != 48) ||
-                       (p.cin8 > 96 && p.cin8 <= 128 && pw_blocks(p) >= 8192);
+                       (p.Cout <= 64 && p.cin8 > 96 && p.cin8 <= 128 && pw_blocks(p) >= 8192);
   if (p.K == 1 && !(s.flags & IVH_FLAG_NO_PW) && pw_plan(p) && pw_blocks(p) >= kPwMinBlocks && pw_wins) {
     p.pw = 1;
     p.ksplit = 1;

@@ -1,10 +1,10 @@
-// Pointwise (1x1, stride 1) convolution with Cout <= 64 on gfx950 fp16 MFMA, streaming.
+// Pointwise (1x1, stride 1) convolution with Cout <= 128 on gfx950 fp16 MFMA, streaming.
 //
 // Replaces, for the channels-last 1x1 convs of the C2f / C3k2 blocks and the heads, the
 // reference's conv1x1 / gemm kernels (kernels/conv1x1.cl, gemm.cl:468-472, 644-650;
 // dispatch src/PlanModel.cpp:3688-3933):
 //   y[p][co] = act(sum_ci W[co][ci] x[p][ci] + b[co])
-// At Cout <= 64 these layers carry 2-4 bytes of HBM traffic per FLOP: the bound is HBM, and
+// At Cout <= 128 these layers carry 1-4 bytes of HBM traffic per FLOP: the bound is HBM, and
 // the kernel is built to keep the HBM stream full rather than to stage tiles:
 //   * the work-group's weights [32 CB][K] and bias sit in LDS, loaded once per launch;
 //   * every wave is an independent stream over 32-pixel blocks (grid-stride over the
@@ -396,18 +396,21 @@ bool pw_views_ok(const ConvParams & p)
 bool pw_plan(const ConvParams & p)
 {
   const bool act_ok = p.act == kActNone || p.act == kActSiLU || p.act == kActReLU || p.act == kActHSwish;
-  return p.K == 1 && p.S == 1 && p.P == 0 && p.G == 1 && p.H == p.Ho && p.W == p.Wo && act_ok && p.Cout <= 64 &&
+  return p.K == 1 && p.S == 1 && p.P == 0 && p.G == 1 && p.H == p.Ho && p.W == p.Wo && act_ok && p.Cout <= 128 &&
          p.cin8 <= kPwMaxK && p.kpad >= p.cin8 && pw_lds_bytes(p) <= 65536 && pw_views_ok(p);
 }
 
 long pw_blocks(const ConvParams & p) { return ((long)p.batch * p.H * p.W + 31) / 32; }
+
+// 32-channel output blocks per wave: 1, 2 or 4
+int pw_cb(const ConvParams & p) { return p.Cout > 64 ? 4 : (p.Cout > 32 ? 2 : 1); }
 
 // K slices per chunk: 2 for up to 32 input channels, 3 for 48, else 4
 int pw_nsl(const ConvParams & p) { return p.cin8 <= 32 ? 2 : (p.cin8 == 48 ? 3 : 4); }
 
 size_t pw_lds_bytes(const ConvParams & p)
 {
-  const int cb = p.Cout > 32 ? 2 : 1, kc = 16 * pw_nsl(p), nch = (p.cin8 + kc - 1) / kc;
+  const int cb = pw_cb(p), kc = 16 * pw_nsl(p), nch = (p.cin8 + kc - 1) / kc;
   return (size_t)cb * 32 * (kc * nch + 8) * 2 + (size_t)cb * 32 * 4;
 }
 
@@ -545,7 +548,8 @@ void launch_conv_pw(const ConvParams & p, hipStream_t s)
     else launch_pwt_xt<false>(p, g, s);
     return;
   }
-  if (p.Cout > 32) launch_pw_cb<2>(p, g, s);
+  if (p.Cout > 64) launch_pw_cb<4>(p, g, s);
+  else if (p.Cout > 32) launch_pw_cb<2>(p, g, s);
   else launch_pw_cb<1>(p, g, s);
 }
 

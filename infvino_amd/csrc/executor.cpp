@@ -2138,7 +2138,7 @@ void Model::validate(const Launch & l) const
         check(p.w, 0, (long)(p.Cout - 1) * p.kpad + p.cin8 - 1, 2, "planar pointwise w");
         if (!p.xt) check(p.x.ptr, 0, vlast(p.x, p.batch, p.cin8, HW), 2, "planar pointwise x");
       } else if (p.pw) {
-        if (p.K != 1 || p.S != 1 || p.P != 0 || p.G != 1 || p.H != p.Ho || p.W != p.Wo || p.Cout > 64 || p.Cout < 1 ||
+        if (p.K != 1 || p.S != 1 || p.P != 0 || p.G != 1 || p.H != p.Ho || p.W != p.Wo || p.Cout > 128 || p.Cout < 1 ||
             p.cin8 > 512 || p.kpad < p.cin8 || p.ksplit != 1 || p.halo || p.res || p.pipe || p.s2 || p.xt ||
             !pw_views_ok(p) || pw_lds_bytes(p) > 65536 ||
             (p.act != kActNone && p.act != kActSiLU && p.act != kActReLU && p.act != kActHSwish))

@@ -83,7 +83,7 @@ long pair_tiles(int H, int W, int batch, int th, int tw);
 // weights / bias / act of conv 2, th x tw); both weights in the 32-channel halo packing
 void launch_conv_pair(const ConvParams & a, const ConvParams & b, hipStream_t s);
 
-// conv_pw.hip: 1x1 stride-1 convs with Cout <= 64 on channels-last views (streaming)
+// conv_pw.hip: 1x1 stride-1 convs with Cout <= 128 on channels-last views (streaming)
 bool pw_views_ok(const ConvParams & p);
 bool pw_plan(const ConvParams & p);         // eligible (shape, activation, views, LDS)
 long pw_blocks(const ConvParams & p);       // 32-pixel blocks of the batch

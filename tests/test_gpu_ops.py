@@ -447,6 +447,8 @@ def test_conv3x3_s2_persistent_no_act(tmp_path):
     (64, 56, 80, 80, 6, pw.ACT_SILU),      # Cout 56 (ragged second 32-channel block)
     (51, 48, 80, 80, 6, pw.ACT_SILU),      # Cin 51: the last 8-channel piece masked past Cin
     (64, 64, 40, 40, 24, pw.ACT_NONE),     # no activation
+    (96, 128, 80, 80, 6, pw.ACT_SILU),     # four 32-channel blocks per wave (YOLO11n C3k2 cv2 at 80x80)
+    (64, 100, 80, 80, 6, pw.ACT_RELU),     # Cout 100: ragged fourth block
 ])
 def test_conv1x1_streaming(tmp_path, cin, cout, H, W, batch, act):
     """1x1 convs through the streaming pointwise kernel of conv_pw.hip vs the oracle and vs
