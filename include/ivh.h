@@ -76,6 +76,10 @@ extern "C" {
 #define IVH_FLAG_NO_FUSE_UPSAMPLE 0x100000u /* run a 2x resize_nn whose output only feeds a
                                                concat read by one 1x1 conv, instead of that
                                                conv reading the resize's input directly */
+#define IVH_FLAG_NO_FUSE_SIBLINGS 0x200000u /* run sibling 3x3 convs that read the same
+                                               tensor (a Pose head's branches) one by one
+                                               instead of as one conv over all their output
+                                               channels */
 #define IVH_FLAG_NO_PW 0x20000u   /* 1x1 convs never use the streaming pointwise kernels */
 #define IVH_FLAG_PIPE_ANY 0x4000u /* 3x3 stride-1 convs use the DMA-pipelined kernel wherever it
                                      applies (Cin >= 32, any grid size), not only where it is

@@ -43,6 +43,7 @@ IVH_FLAG_NO_PW = 0x20000
 IVH_FLAG_NO_WIDE = 0x40000
 IVH_FLAG_NO_PINGPONG = 0x80000
 IVH_FLAG_NO_FUSE_UPSAMPLE = 0x100000
+IVH_FLAG_NO_FUSE_SIBLINGS = 0x200000
 
 # every symbol include/ivh.h declares, with (restype, argtypes)
 _vp, _i, _u32, _sz, _d = C.c_void_p, C.c_int, C.c_uint32, C.c_size_t, C.c_double

@@ -157,6 +157,7 @@ Model::Model(const std::string & plan_path, int device, int max_batch, uint32_t 
     fuseAttention();
   }
   findPairs();
+  findSiblings();
   plan();
   if (!dry_) HIPCHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   allocate();
@@ -943,6 +944,24 @@ void Model::assignViews()
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     PlanNode & n = nodes_[ni];
     Tensor & out = *T_[n.outs[0]];
+    if (!sib_[ni].empty()) {  // merged siblings: their outputs are channel views of one root
+      auto r = std::make_unique<Root>();
+      r->H = out.H;
+      r->W = out.W;
+      r->C = 0;
+      for (int j : sib_[ni]) r->C += T_[nodes_[j].outs[0]]->C;
+      r->numel = (long)r->C * r->H * r->W;
+      const int rid = (int)roots_.size();
+      roots_.push_back(std::move(r));
+      int off = 0;
+      for (int j : sib_[ni]) {
+        Tensor & t = *T_[nodes_[j].outs[0]];
+        t.root = rid;
+        t.coff = off;
+        t.eoff = (long)off * t.H * t.W;
+        off += t.C;
+      }
+    }
     if (n.op == "reshape" || n.op == "flatten") {
       const Tensor & src = *T_[n.ins.at(0)];
       if (src.numel != out.numel) throw std::runtime_error("reshape numel mismatch: " + out.name);
@@ -1285,15 +1304,34 @@ void Model::uploadWeights()
     const PlanNode & n = nodes_[ni];
     const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
     if (!(is1 || is3 || isg) || skip_[ni]) continue;
+    if (sib_lead_[ni] >= 0 && sib_lead_[ni] != (int)ni) continue;  // packed with its lead
     const std::string wname = is1 ? n.ins.at(0) : n.ins.at(1);
     const Tensor & wt = *T_[wname];
     if (wt.kind != Tensor::kInit) throw std::runtime_error("conv weight is not an init: " + wname);
-    const std::vector<uint16_t> & W = host[wname];
+    const std::vector<uint16_t> * Wp = &host[wname];
     ConvSpec cs;
     cs.Cout = (int)wt.dims.at(0);
+    // merged siblings: the members' weights and biases concatenated over output channels
+    std::vector<uint16_t> Wm, Bm;
+    if (!sib_[ni].empty()) {
+      cs.Cout = 0;
+      for (int j : sib_[ni]) {
+        const PlanNode & m = nodes_[j];
+        const Tensor & mw = *T_[m.ins.at(1)];
+        const std::vector<uint16_t> & hw = host.at(m.ins.at(1));
+        const std::vector<uint16_t> & hb = host.at(m.ins.at(2));
+        if (mw.numel != (long)mw.dims[0] * wt.dims[1] * 9 || (long)hb.size() < mw.dims[0])
+          throw std::runtime_error("merged sibling conv weights: " + m.outs[0]);
+        Wm.insert(Wm.end(), hw.begin(), hw.end());
+        Bm.insert(Bm.end(), hb.begin(), hb.begin() + mw.dims[0]);
+        cs.Cout += (int)mw.dims[0];
+      }
+      Wp = &Wm;
+    }
+    const std::vector<uint16_t> & W = *Wp;
     cs.K = is1 ? 1 : (is3 ? 3 : n.i("K", 3));
     cs.G = isg ? n.i("G", 1) : 1;
-    const int cin_g = (int)(wt.numel / ((long)cs.Cout * cs.K * cs.K));
+    const int cin_g = (int)(wt.numel / ((long)wt.dims.at(0) * cs.K * cs.K));
     const Tensor & x = *T_[is1 ? n.ins.at(1) : n.ins.at(0)];
     cs.Cin = is1 ? (int)wt.dims.at(1) : cin_g * cs.G;
     if (is1) {
@@ -1311,7 +1349,7 @@ void Model::uploadWeights()
     cs.has_bias = bname != "-";
     const uint16_t * B = nullptr;
     if (cs.has_bias) {
-      const auto & Bv = host.at(bname);
+      const auto & Bv = sib_[ni].empty() ? host.at(bname) : Bm;
       if ((long)Bv.size() < cs.Cout) throw std::runtime_error("bias too short: " + bname);
       B = Bv.data();
     }
@@ -1436,6 +1474,76 @@ void Model::findPairs()
   }
 }
 
+// Sibling merge: 3x3 convs that read the same tensor with the same stride, pad and
+// activation (a Pose head's box, class and keypoint branches each start with one) run as one
+// conv over the concatenated output channels, so x is read once and the MFMA tiles are
+// fuller.  Each member's output becomes a channel view of one root (assignViews), whose
+// readers must therefore all be convs; members with Cout % 8 != 0 are allowed only last, so
+// every view starts on a 16-byte boundary.
+void Model::findSiblings()
+{
+  sib_.assign(nodes_.size(), {});
+  sib_lead_.assign(nodes_.size(), -1);
+  if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_SIBLINGS | IVH_FLAG_NCHW_ONLY | IVH_FLAG_DIRECT_ONLY)) return;
+  std::map<std::string, std::vector<int>> readers;
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    for (size_t k = 0; k < nodes_[i].ins.size(); ++k)
+      if (nodes_[i].ins[k] != "-") readers[nodes_[i].ins[k]].push_back((int)i);
+  std::set<std::string> outs(outputs_.begin(), outputs_.end());
+  std::vector<char> paired(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i)
+    if (pair_next_[i] >= 0) paired[i] = paired[pair_next_[i]] = 1;
+  auto member_ok = [&](size_t j) {
+    const PlanNode & n = nodes_[j];
+    if (n.op != "conv3x3" || paired[j] || n.ins.size() < 3 || n.outs.size() != 1 || (n.ins.size() > 3 && n.ins[3] != "-"))
+      return false;
+    const Tensor & x = *T_.at(n.ins[0]);
+    const Tensor & w = *T_.at(n.ins[1]);
+    const Tensor & y = *T_.at(n.outs[0]);
+    if (x.kind != Tensor::kAct || w.kind != Tensor::kInit || w.dims.size() != 4 || w.dims[1] != x.C ||
+        y.kind != Tensor::kAct || y.dims.size() != 4 || y.C != w.dims[0] || outs.count(y.name) || n.ins[2] == "-")
+      return false;
+    // every reader of the output is a conv reading it as its input
+    const auto it = readers.find(y.name);
+    if (it == readers.end()) return false;
+    for (int u : it->second) {
+      const PlanNode & un = nodes_[u];
+      const bool conv_in = ((un.op == "conv3x3" || un.op == "conv_general") && un.ins[0] == y.name &&
+                            std::count(un.ins.begin(), un.ins.end(), y.name) == 1) ||
+                           (un.op == "conv1x1" && un.ins.size() > 1 && un.ins[1] == y.name &&
+                            std::count(un.ins.begin(), un.ins.end(), y.name) == 1);
+      if (!conv_in) return false;
+    }
+    return true;
+  };
+  std::vector<char> taken(nodes_.size(), 0);
+  for (size_t i = 0; i < nodes_.size(); ++i) {
+    if (taken[i] || !member_ok(i)) continue;
+    const PlanNode & a = nodes_[i];
+    std::vector<int> g{(int)i};
+    for (int j : readers[a.ins[0]]) {
+      if (j <= (int)i || taken[j] || !member_ok(j)) continue;
+      const PlanNode & b = nodes_[j];
+      if (b.ins[0] != a.ins[0] || b.i("stride", 1) != a.i("stride", 1) || b.i("pad", 1) != a.i("pad", 1) ||
+          b.i("act") != a.i("act") || b.i("Hout") != a.i("Hout") || b.i("Wout") != a.i("Wout"))
+        continue;
+      g.push_back(j);
+    }
+    if (g.size() < 2) continue;
+    // channel order: 8-aligned members first (node order), then at most one ragged one
+    std::vector<int> even, odd;
+    for (int j : g) (T_.at(nodes_[j].outs[0])->C % 8 ? odd : even).push_back(j);
+    if (odd.size() > 1) odd.resize(1);
+    if (even.empty() || even.size() + odd.size() < 2) continue;
+    even.insert(even.end(), odd.begin(), odd.end());
+    for (int j : even) {
+      taken[j] = 1;
+      sib_lead_[j] = (int)i;
+    }
+    sib_[i] = even;
+  }
+}
+
 bool Model::pairLaunch(size_t ni, int batch, Launch & L)
 {
   const int nj = pair_next_[ni];
@@ -1493,6 +1601,14 @@ Launch Model::convLaunch(size_t ni, int batch)
     ConvParams & p = L.cp;
     p.batch = batch;
     p.Cout = (int)wt.dims[0];
+    // merged siblings: all members' channels, written from channel 0 of their shared root
+    const Tensor * ymerged = nullptr;
+    if (!sib_[ni].empty()) {
+      p.Cout = 0;
+      for (int j : sib_[ni]) p.Cout += T_[nodes_[j].outs[0]]->C;
+      ymerged = T_[nodes_[sib_[ni][0]].outs[0]].get();
+      if (ymerged->coff != 0 || roots_.at(ymerged->root)->C != p.Cout) fail("merged sibling root");
+    }
     if (is1) {
       p.Cin = (int)wt.dims[1];
       const long N = xt.numel / std::max(p.Cin, 1);
@@ -1510,16 +1626,19 @@ Launch Model::convLaunch(size_t ni, int batch)
       p.Ho = n.i("Hout"); p.Wo = n.i("Wout");
       if (p.Ho != (p.H + 2 * p.P - p.K) / p.S + 1 || p.Wo != (p.W + 2 * p.P - p.K) / p.S + 1)
         fail("Hout/Wout inconsistent with input geometry");
-      if (wt.numel != (long)p.Cout * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
+      if (wt.numel != (ymerged ? wt.dims[0] : (long)p.Cout) * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
     }
     if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
-    if (yt.numel != (long)p.Cout * p.Ho * p.Wo) fail("output numel mismatch");
+    const Tensor & yv = ymerged ? *ymerged : yt;
+    if (ymerged ? (long)p.Cout * yv.H * yv.W != roots_.at(yv.root)->numel || yv.H != p.Ho || yv.W != p.Wo
+                : yt.numel != (long)p.Cout * p.Ho * p.Wo)
+      fail("output numel mismatch");
     p.act = n.i("act");
     p.x = view(xt.name, batch);
-    p.y = view(yt.name, batch);
-    if (p.y.layout == kNHWC && yt.kind != Tensor::kInit) {
-      const Root & yr = *roots_.at(yt.root);
-      if (yt.coff + p.Cout == yr.C) p.ypad = yr.cs - yr.C;
+    p.y = view(yv.name, batch);
+    if (p.y.layout == kNHWC && yv.kind != Tensor::kInit) {
+      const Root & yr = *roots_.at(yv.root);
+      if (yv.coff + p.Cout == yr.C) p.ypad = yr.cs - yr.C;
     }
     if (has(3)) {
       const Tensor & rt = *T_[n.ins[3]];
@@ -1960,6 +2079,8 @@ const Model::LaunchPlan & Model::launches(int batch)
   P.covered.assign(nodes_.size(), 0);
   for (int r : up_src_)
     if (r >= 0) P.covered[r] = 1;  // the conv reading the resize's input does its work
+  for (size_t ni = 0; ni < nodes_.size(); ++ni)
+    if (sib_lead_[ni] >= 0 && sib_lead_[ni] != (int)ni) P.covered[ni] = 1;  // in its lead's launch
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     P.begin[ni] = P.L.size();
     if (!skip_[ni] && !P.covered[ni]) emitNode(ni, batch, P.L, P.covered);
@@ -2552,7 +2673,8 @@ std::string Model::nodeTag(int i)
   const LaunchPlan & P = launches(labelBatch());
   if (P.begin.at(i) == P.end.at(i)) return k;
   const Launch & l = P.L[P.begin[i]];
-  if (l.kind == Launch::kIgemm) return k + " " + igemm_launch_tag(l.cp);
+  if (l.kind == Launch::kIgemm)
+    return k + " " + igemm_launch_tag(l.cp) + (sib_.at(i).empty() ? "" : " siblings=" + std::to_string(sib_[i].size()) + " cout=" + std::to_string(l.cp.Cout));
   if (l.kind == Launch::kDw) return k + " " + dw_launch_tag(l.cp);
   if (l.kind == Launch::kPair)
     return k + " th=" + std::to_string(l.cp.th) + " tw=" + std::to_string(l.cp.tw) + " tiles=" +

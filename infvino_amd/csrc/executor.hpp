@@ -125,6 +125,13 @@ class Model {
   // when node ni is the first conv of a pair, else -1 (decided at load, before allocate)
   void findPairs();
   std::vector<int> pair_next_;
+  // sibling 3x3 convs (the heads' cv2 / cv3 / cv4 first convs read the same x): one launch
+  // with the output channels of all of them, whose outputs are channel views of one root.
+  // sib_[lead] = the members in channel order (the lead is the first in node order), empty
+  // otherwise; sib_lead_[ni] = the lead of node ni's group, or -1
+  void findSiblings();
+  std::vector<std::vector<int>> sib_;
+  std::vector<int> sib_lead_;
   // the launch of a conv node (conv1x1 / conv3x3 / conv_general) at a batch size
   Launch convLaunch(size_t ni, int batch);
   // node ni and its pair partner as one kPair launch; false when a view does not suit it

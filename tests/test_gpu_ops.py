@@ -891,3 +891,38 @@ def test_upsample_concat_fused(tmp_path, ca, cb, cout, H, W, batch, reuse_a, fus
     _, _, ref = _run(path, batch, lo=-1.0, flags=fl | ia.IVH_FLAG_NO_FUSE_UPSAMPLE)
     assert np.array_equal(got[0], ref[0])
     _check_f32(path, batch, lo=-1.0, ref_mode=False, flags=fl)
+
+
+def _head_plan(d, cin, H, W, widths=(51, 64, 64)):
+    """A Pose head level: three branches whose first 3x3 convs read the same x (here the
+    keypoint branch, 51 channels, comes first in node order as in the written plans), each
+    followed by its own 3x3 conv; the three branch outputs concatenated."""
+    def build(pb):
+        x = pb.conv(pb.input("x", [1, cin, H, W]), cin, 1, act=pw.ACT_SILU)
+        firsts = [pb.conv(x, c, 3, 1, act=pw.ACT_SILU) for c in widths]
+        return pb.concat([pb.conv(f, c, 3, 1, act=pw.ACT_SILU) for f, c in zip(firsts, widths)])
+    return _small_plan(d, build)
+
+
+@pytest.mark.parametrize("cin,H,W,batch,widths", [
+    (64, 20, 24, 3, (51, 64, 64)),     # P3 class: the resident-weight ping-pong kernel, 3 channel blocks
+    (128, 12, 10, 4, (51, 64, 64)),    # P4 class
+    (256, 6, 5, 2, (51, 64, 64)),      # P5 class
+    (256, 20, 20, 64, (51, 64, 64)),   # P5 at batch 64: the wide-layer kernel, 2 x 128 channels
+    (128, 16, 16, 8, (51, 64)),        # YOLO11n: box and keypoint branches only
+])
+def test_sibling_convs_merged(tmp_path, cin, H, W, batch, widths):
+    """Sibling 3x3 convs on one input run as one conv over all their output channels, each
+    branch reading its channel view of the merged output: oracle bar, and the merged run
+    against the branches run one by one."""
+    path = _head_plan(tmp_path, cin, H, W, widths)
+    tags = _conv_tags(path, batch)
+    assert sum(f"siblings={len(widths)} cout={sum(widths)}" in t for t in tags) == 1, tags
+    assert not any("siblings" in t for t in _conv_tags(path, batch, ia.IVH_FLAG_NO_FUSE_SIBLINGS))
+    kinds = _kernels(path, batch)
+    assert kinds.count("(fused)") == len(widths) - 1, kinds
+    got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
+    _, _, sep = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_FUSE_SIBLINGS)
+    mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(sep[0]))
+    print(f"   merged vs separate mean_rel={mean_rel:.2e} max_rel={max_rel:.2e}")
+    assert mean_rel < 1e-3 and max_rel < 5e-3

@@ -60,8 +60,9 @@ def test_kernel_choice_yolov8(plans):
     64 < Cout <= 256, the DMA-pipelined kernel for the other Cin > 64 convs on the 40x40 maps
     (enough items for its persistent grid), the fused pair kernel for the three
     32-channel bottlenecks at 80x80 and the 16-channel one at 160x160 (their second conv then
-    launches nothing) and the stride-1 LDS-patch kernel for the rest."""
-    m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
+    launches nothing) and the stride-1 LDS-patch kernel for the rest.  Per conv shape, so with
+    the heads' sibling convs run apart (their merged launches: test_sibling_conv_merge)."""
+    m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY | ia.IVH_FLAG_NO_FUSE_SIBLINGS)
     m.run(64)
     info = [m.nodeInfo(i) for i in range(m.nodeCount())]
     by = {i["desc"]: i["kernel"] for i in info}
@@ -415,8 +416,9 @@ def test_launch_plans_per_batch(plans):
 def test_labels_follow_last_batch(plans):
     """Kernel labels describe the batch of the last run: YOLOv8n-pose at 640 splits K at
     batch 1 (grids too small to fill the chip) and not at batch 64, and the pipelined 3x3
-    kernel runs only at batch 64."""
-    m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY)
+    kernel runs only at batch 64 (on the heads' 128 -> 64 / 51 convs, run apart here: merged they
+    take the wide-layer kernel)."""
+    m = ia.PlanModel(plans("yolov8n-pose")[0], 0, 64, DRY | ia.IVH_FLAG_NO_FUSE_SIBLINGS)
     m.run(64)
     k64 = [m.nodeInfo(i)["kernel"] for i in range(m.nodeCount())]
     t64 = [m.nodeTag(i) for i in range(m.nodeCount())]
@@ -552,3 +554,23 @@ def test_upsample_concat_fusion(plans, name):
                     "yolo11n-pose": ["conv1x1 384x40x40->128x40x40", "conv1x1 256x80x80->64x80x80"]}[name]
             assert [d.split(" k1")[0] for d in up] == (want if fused else []), up
         m.close()
+
+
+def test_sibling_conv_merge(plans):
+    """The Pose heads' first 3x3 convs per level (YOLOv8n: box, class and keypoint branches,
+    64 + 64 + 51 channels; YOLO11n: box and keypoint, 64 + 51, its class branch starting with
+    a depthwise conv) run as one conv per level; IVH_FLAG_NO_FUSE_SIBLINGS runs them apart."""
+    for name, per_level in (("yolov8n-pose", "siblings=3 cout=179"), ("yolo11n-pose", "siblings=2 cout=115")):
+        for flags, merged in ((0, True), (ia.IVH_FLAG_NO_FUSE_SIBLINGS, False)):
+            m = ia.PlanModel(plans(name)[0], 0, 64, DRY | flags)
+            for b in (1, 64):
+                m.run(b)
+                tags = [m.nodeTag(i) for i in range(m.nodeCount())]
+                assert sum(per_level in t for t in tags) == (3 if merged else 0), (name, b, flags)
+                assert not any("siblings" in t and per_level not in t for t in tags)
+                if merged and b == 64:
+                    # P3 (64 in): the resident-weight ping-pong kernel over the merged channel
+                    # blocks; P4 / P5 (128 / 256 in): the wide-layer kernel
+                    kinds = [t.split()[0] for t in tags if per_level in t]
+                    assert kinds == ["conv_res", "conv_wide", "conv_wide"], kinds
+            m.close()
