@@ -479,7 +479,8 @@ def main():
                     help="launch node by node instead of replaying the captured HIP graph")
     ap.add_argument("--layer", default="conv3x3s2_16to32_320", help="sweep layer (or config1) for --phase layer")
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
-                    help="extra ivh_create flags for --phase layer (e.g. 0x200: no resident-weight kernel)")
+                    help="extra ivh_create flags for --phase layer and --phase throughput (e.g. 0x200: no "
+                         "resident-weight kernel, 0x300000: no upsample-concat / sibling-conv fusion)")
     ap.add_argument("--phase", default="all", choices=["all", "throughput", "calib", "sweep", "layer", "hbm", "gemm",
                                                        "attention"],
                     help="throughput: only the batch-64 timed steps (for counter runs); calib: a known-size "
@@ -524,7 +525,7 @@ def main():
 
     # ---- throughput: K graph replays queued back to back, synchronised at both ends
     gflag = ia.IVH_FLAG_NO_GRAPH if args.no_graph else 0
-    m = ia.PlanModel(path, 0, B, ia.IVH_FLAG_ASYNC | gflag)
+    m = ia.PlanModel(path, 0, B, ia.IVH_FLAG_ASYNC | gflag | (args.flags if args.phase == "throughput" else 0))
     m.setInput(x, B)
     for _ in range(args.warmup):
         m.run(B)

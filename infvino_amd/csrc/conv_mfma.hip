@@ -68,10 +68,12 @@ __global__ void __launch_bounds__(256, OCC) conv_igemm_kernel(const ConvParams p
   const int wm = wave % WGM, wn = wave / WGM;
   const int HWo = p.Ho * p.Wo;
   const unsigned M = (unsigned)p.batch * HWo;  // below 2^31 (the launcher's batch chunks)
-  // XCD-aware order over (pixel tile, channel tile, K slice), pixel tiles fastest
+  // XCD-aware order over (channel tile, pixel tile, K slice), channel tiles fastest: the
+  // channel tiles of one pixel tile, which gather the same input, run together on one XCD and
+  // share its L2, and neighbouring pixel tiles (sharing input rows) follow on the same XCD
   const int lin = xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
                            gridDim.x * gridDim.y * gridDim.z);
-  const int bx = lin % gridDim.x, by = (lin / gridDim.x) % gridDim.y, bz = lin / (gridDim.x * gridDim.y);
+  const int by = lin % gridDim.y, bx = (lin / gridDim.y) % gridDim.x, bz = lin / (gridDim.x * gridDim.y);
   const unsigned m0 = (unsigned)bx * BM;
   const int n0 = by * BN;
   const int kc = tid % KC, r0 = tid / KC;
