@@ -97,6 +97,11 @@ MODEL_LAYERS = [
     ("conv3x3s2_128to128_40", 128, 128, 40, 40, 3, 2),
     ("conv1x1_384to128_40", 384, 128, 40, 40, 1, 1),
     ("conv1x1_128to64_80", 128, 64, 80, 80, 1, 1),
+    # a Pose head level: the box / class / keypoint branches' first 3x3 convs (64 + 64 + 51
+    # channels from one input), which run as one merged conv
+    ("heads_64_80", 64, 179, 80, 80, 3, 1),
+    ("heads_128_40", 128, 179, 40, 40, 3, 1),
+    ("heads_256_20", 256, 179, 20, 20, 3, 1),
 ]
 
 
@@ -118,6 +123,9 @@ def sweep_plan(pw, d, name):
         if name.startswith("pair"):
             t = pb.conv(x, cout, 3, 1)
             y = pb.conv(t, cout, 3, 1, res=x)
+        elif name.startswith("heads"):
+            # keypoint branch first, as in the written plans; each branch output read by a conv
+            y = pb.concat([pb.conv(pb.conv(x, c, 3, 1), 16, 1) for c in (51, 64, 64)])
         else:
             y = pb.conv(x, cout, k, s)
         pb.output(pb.unary(y, pw.UN_RELU))
@@ -447,19 +455,20 @@ def model_lines(ia, pw, specs, steps, warmup):
 
 def measured_traffic(node_desc, batch):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc
-    summary (profiles/traffic_dominant_kernel.md), when it was measured on this node."""
+    summary (profiles/traffic_dominant_kernel.md: node / batch / hbm_bytes_per_launch
+    records), when it was measured on this node at this batch."""
     path = os.path.join(ROOT, "profiles", "traffic_dominant_kernel.md")
     if not os.path.exists(path):
         return None
-    node = bytes_ = b = None
+    node = b = None
     for line in open(path):
         if line.startswith("node:"):
-            node = line.split(":", 1)[1].strip()
+            node, b = line.split(":", 1)[1].strip(), None
         elif line.startswith("batch:"):
             b = int(line.split(":", 1)[1])
-        elif line.startswith("hbm_bytes_per_launch:"):
-            bytes_ = float(line.split(":", 1)[1])
-    return bytes_ if (node == node_desc and b == batch) else None
+        elif line.startswith("hbm_bytes_per_launch:") and node == node_desc and b == batch:
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def main():
