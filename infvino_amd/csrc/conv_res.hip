@@ -462,11 +462,13 @@ __global__ void __launch_bounds__(256 * NGRP, 1) conv3x3s1_pp_kernel(const ConvP
   const float inv_tw = __builtin_amdgcn_rcpf((float)TW), inv_pw = __builtin_amdgcn_rcpf((float)PW);
 
   const long x_last = (long)(p.batch - 1) * p.x.img + ((long)p.H * p.W - 1) * p.x.cs + p.cin8;
+  // a grouped launch: this channel block's input channels start y * xg channels into x
+  const __half * const xp = p.x.ptr + (long)blockIdx.y * p.xg;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<__half *>(p.x.ptr), (short)0, (int)(x_last * 2), kBufDword3);
+      const_cast<__half *>(xp), (short)0, (int)(x_last * 2), kBufDword3);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<__half *>(p.w + (long)n0 * p.kpad), (short)0, BN * p.kpad * 2, kBufDword3);
-  const unsigned long long xaddr = reinterpret_cast<unsigned long long>(p.x.ptr);
+  const unsigned long long xaddr = reinterpret_cast<unsigned long long>(xp);
   const pp_u4 xrs = {(unsigned)xaddr, (unsigned)(xaddr >> 32) & 0xffffu, (unsigned)(x_last * 2), (unsigned)kBufDword3};
 
   // ---- prologue: weights into LDS by DMA (slot s = row s / 73, piece s % 73; piece 72 is
@@ -952,6 +954,7 @@ static void launch_pp(const ConvParams & p, hipStream_t s)
 
 void launch_conv_res(const ConvParams & p, hipStream_t s)
 {
+  if (p.xg && p.res != 4) throw std::runtime_error("grouped resident-weight conv outside the ping-pong kernel");
   const int bc = conv_batch_chunk(p);
   if (bc < p.batch) {
     for (int b0 = 0; b0 < p.batch; b0 += bc) launch_conv_res(conv_batch_slice(p, b0, std::min(bc, p.batch - b0)), s);

@@ -1307,11 +1307,10 @@ void Model::uploadWeights()
     weight_bytes_ += round_up((long)bytes, 256);
     return d;
   };
-  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+  // one conv's packing; merged: the members of its sibling group together
+  auto pack_conv = [&](size_t ni, bool merged) -> Packed {
     const PlanNode & n = nodes_[ni];
     const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
-    if (!(is1 || is3 || isg) || skip_[ni]) continue;
-    if (sib_lead_[ni] >= 0 && sib_lead_[ni] != (int)ni) continue;  // packed with its lead
     const std::string wname = is1 ? n.ins.at(0) : n.ins.at(1);
     const Tensor & wt = *T_[wname];
     if (wt.kind != Tensor::kInit) throw std::runtime_error("conv weight is not an init: " + wname);
@@ -1320,7 +1319,7 @@ void Model::uploadWeights()
     cs.Cout = (int)wt.dims.at(0);
     // merged siblings: the members' weights and biases concatenated over output channels
     std::vector<uint16_t> Wm, Bm;
-    if (!sib_[ni].empty()) {
+    if (merged) {
       cs.Cout = 0;
       for (int j : sib_[ni]) {
         const PlanNode & m = nodes_[j];
@@ -1356,7 +1355,7 @@ void Model::uploadWeights()
     cs.has_bias = bname != "-";
     const uint16_t * B = nullptr;
     if (cs.has_bias) {
-      const auto & Bv = sib_[ni].empty() ? host.at(bname) : Bm;
+      const auto & Bv = merged ? Bm : host.at(bname);
       if ((long)Bv.size() < cs.Cout) throw std::runtime_error("bias too short: " + bname);
       B = Bv.data();
     }
@@ -1375,7 +1374,19 @@ void Model::uploadWeights()
     std::vector<uint8_t> blob;
     conv_pack(cs, pk.pk, W.data(), B, blob);
     pk.dev = upload(blob.data(), blob.size());
-    packed_[ni] = pk;
+    return pk;
+  };
+  packed_grp_.assign(nodes_.size(), Packed{});
+  for (size_t ni = 0; ni < nodes_.size(); ++ni) {
+    const std::string & op = nodes_[ni].op;
+    if (!(op == "conv1x1" || op == "conv3x3" || op == "conv_general") || skip_[ni]) continue;
+    const int lead = sib_lead_[ni];
+    if (lead >= 0 && lead != (int)ni && !sib_grouped_[lead]) continue;  // packed with its lead
+    const bool grouped_lead = !sib_[ni].empty() && sib_grouped_[ni];
+    packed_[ni] = pack_conv(ni, !sib_[ni].empty() && !grouped_lead);
+    // a grouped lead also keeps its own packing (and its members theirs): at a batch whose
+    // grouped launch does not get the ping-pong kernel they run one by one
+    if (grouped_lead) packed_grp_[ni] = pack_conv(ni, true);
   }
   // split-K workspace: the largest need over every node and every batch size, so launch
   // lists and captured graphs of different batch sizes share one fixed buffer
@@ -1491,6 +1502,8 @@ void Model::findSiblings()
 {
   sib_.assign(nodes_.size(), {});
   sib_lead_.assign(nodes_.size(), -1);
+  sib_grouped_.assign(nodes_.size(), 0);
+  sib_x_.assign(nodes_.size(), std::string());
   if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_SIBLINGS | IVH_FLAG_NCHW_ONLY | IVH_FLAG_DIRECT_ONLY)) return;
   std::map<std::string, std::vector<int>> readers;
   for (size_t i = 0; i < nodes_.size(); ++i)
@@ -1549,6 +1562,39 @@ void Model::findSiblings()
     }
     sib_[i] = even;
   }
+  // Grouped siblings: the merged members' own next convs (3x3 stride 1, 64 -> 64, each the
+  // one reader of its member's output) read consecutive 64-channel views of the merged root;
+  // as a grouped conv on the ping-pong kernel (channel block y reads input channels 64 y ..)
+  // they are one launch.  The members' outputs must be whole 64-channel blocks from channel 0.
+  if (flags_ & (IVH_FLAG_NO_RESIDENT | IVH_FLAG_NO_PINGPONG | IVH_FLAG_PIPE_ANY)) return;
+  const size_t n_first = nodes_.size();
+  for (size_t i = 0; i < n_first; ++i) {
+    if (sib_[i].empty() || sib_grouped_[i]) continue;
+    std::vector<int> tw;
+    int off = 0;
+    for (int m : sib_[i]) {
+      const Tensor & t = *T_.at(nodes_[m].outs[0]);
+      const auto it = readers.find(t.name);
+      if (t.C != 64 || off != 64 * (int)tw.size() || it == readers.end() || it->second.size() != 1) break;
+      const int r = it->second[0];
+      const PlanNode & rn = nodes_[r];
+      if (taken[r] || !member_ok(r) || rn.ins[0] != t.name || rn.i("stride", 1) != 1 || rn.i("pad", 1) != 1 ||
+          T_.at(rn.ins[1])->dims != std::vector<int64_t>{64, 64, 3, 3} || rn.i("Hout") != t.H || rn.i("Wout") != t.W ||
+          (!tw.empty() && rn.i("act") != nodes_[tw[0]].i("act")))
+        break;
+      tw.push_back(r);
+      off += t.C;
+    }
+    if (tw.size() < 2) continue;
+    const int lead = *std::min_element(tw.begin(), tw.end());
+    for (int r : tw) {
+      taken[r] = 1;
+      sib_lead_[r] = lead;
+    }
+    sib_[lead] = tw;
+    sib_grouped_[lead] = 1;
+    sib_x_[lead] = nodes_[sib_[i][0]].outs[0];
+  }
 }
 
 bool Model::pairLaunch(size_t ni, int batch, Launch & L)
@@ -1593,7 +1639,7 @@ bool Model::pairLaunch(size_t ni, int batch, Launch & L)
   return true;
 }
 
-Launch Model::convLaunch(size_t ni, int batch)
+Launch Model::convLaunch(size_t ni, int batch, bool grouped)
 {
   const PlanNode & n = nodes_[ni];
   const Tensor & yt = *T_[n.outs[0]];
@@ -1601,7 +1647,7 @@ Launch Model::convLaunch(size_t ni, int batch)
   auto fail = [&](const std::string & m) { throw std::runtime_error("node " + n.op + " -> " + yt.name + ": " + m); };
   const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
   {
-    const Packed & pk = packed_[ni];
+    const Packed & pk = grouped ? packed_grp_.at(ni) : packed_[ni];
     const Tensor & wt = *T_[is1 ? n.ins[0] : n.ins[1]];
     const Tensor & xt = *T_[is1 ? n.ins[1] : n.ins[0]];
     Launch L;
@@ -1610,7 +1656,7 @@ Launch Model::convLaunch(size_t ni, int batch)
     p.Cout = (int)wt.dims[0];
     // merged siblings: all members' channels, written from channel 0 of their shared root
     const Tensor * ymerged = nullptr;
-    if (!sib_[ni].empty()) {
+    if (!sib_[ni].empty() && (grouped || !sib_grouped_[ni])) {
       p.Cout = 0;
       for (int j : sib_[ni]) p.Cout += T_[nodes_[j].outs[0]]->C;
       ymerged = T_[nodes_[sib_[ni][0]].outs[0]].get();
@@ -1641,7 +1687,8 @@ Launch Model::convLaunch(size_t ni, int batch)
                 : yt.numel != (long)p.Cout * p.Ho * p.Wo)
       fail("output numel mismatch");
     p.act = n.i("act");
-    p.x = view(xt.name, batch);
+    p.x = view(grouped ? sib_x_[ni] : xt.name, batch);
+    if (grouped) p.xg = 64;
     p.y = view(yv.name, batch);
     if (p.y.layout == kNHWC && yv.kind != Tensor::kInit) {
       const Root & yr = *roots_.at(yv.root);
@@ -1777,6 +1824,17 @@ void Model::emitNode(size_t ni, int batch, std::vector<Launch> & out, std::vecto
   }
   const bool is1 = n.op == "conv1x1", is3 = n.op == "conv3x3", isg = n.op == "conv_general";
   if (is1 || is3 || isg) {
+    // grouped siblings: one launch when it gets the ping-pong kernel (the one family with a
+    // grouped input), else every member launches by itself
+    if (!sib_[ni].empty() && sib_grouped_[ni]) {
+      Launch G = convLaunch(ni, batch, true);
+      if (G.kind == Launch::kIgemm && G.cp.res == 4) {
+        out.push_back(G);
+        for (int j : sib_[ni])
+          if (j != (int)ni) covered[j] = 1;
+        return;
+      }
+    }
     if (pair_next_[ni] >= 0) {
       Launch P;
       if (pairLaunch(ni, batch, P)) {
@@ -2086,8 +2144,8 @@ const Model::LaunchPlan & Model::launches(int batch)
   P.covered.assign(nodes_.size(), 0);
   for (int r : up_src_)
     if (r >= 0) P.covered[r] = 1;  // the conv reading the resize's input does its work
-  for (size_t ni = 0; ni < nodes_.size(); ++ni)
-    if (sib_lead_[ni] >= 0 && sib_lead_[ni] != (int)ni) P.covered[ni] = 1;  // in its lead's launch
+  for (size_t ni = 0; ni < nodes_.size(); ++ni)  // in its lead's launch (grouped: emitNode decides)
+    if (sib_lead_[ni] >= 0 && sib_lead_[ni] != (int)ni && !sib_grouped_[sib_lead_[ni]]) P.covered[ni] = 1;
   for (size_t ni = 0; ni < nodes_.size(); ++ni) {
     P.begin[ni] = P.L.size();
     if (!skip_[ni] && !P.covered[ni]) emitNode(ni, batch, P.L, P.covered);
@@ -2234,6 +2292,10 @@ void Model::validate(const Launch & l) const
         if ((long)p.batch * (p.H + 1) >= (1L << 22) || p.W >= (1 << 22)) throw std::runtime_error("resident-weight geometry too large");
         const long bn = res_bn(cfg), nrows = (p.Cout + bn - 1) / bn * bn;
         check(p.w, 0, nrows * p.kpad - 1, 2, "resident-weight w");
+        if (p.xg) {  // grouped: block y reads input channels 64 y .. 64 y + 63
+          if (cfg != 3 || p.xg != 64 || p.Cin != 64 || p.cin8 != 64) throw std::runtime_error("grouped conv geometry");
+          check(p.x.ptr, 0, vlast(p.x, p.batch, (long)p.xg * (nrows / bn - 1) + p.cin8, HW), 2, "grouped conv x");
+        }
         if (res_grid_x(p, cfg) < 1 || res_grid_x(p, cfg) > 65535) throw std::runtime_error("resident-weight grid");
       }
       if (p.pipe) {
@@ -2681,7 +2743,10 @@ std::string Model::nodeTag(int i)
   if (P.begin.at(i) == P.end.at(i)) return k;
   const Launch & l = P.L[P.begin[i]];
   if (l.kind == Launch::kIgemm)
-    return k + " " + igemm_launch_tag(l.cp) + (sib_.at(i).empty() ? "" : " siblings=" + std::to_string(sib_[i].size()) + " cout=" + std::to_string(l.cp.Cout));
+    return k + " " + igemm_launch_tag(l.cp) +
+           (sib_.at(i).empty() || (sib_grouped_[i] && !l.cp.xg)
+                ? ""
+                : (sib_grouped_[i] ? " groups=" : " siblings=") + std::to_string(sib_[i].size()) + " cout=" + std::to_string(l.cp.Cout));
   if (l.kind == Launch::kDw) return k + " " + dw_launch_tag(l.cp);
   if (l.kind == Launch::kPair)
     return k + " th=" + std::to_string(l.cp.th) + " tw=" + std::to_string(l.cp.tw) + " tiles=" +
@@ -2773,13 +2838,14 @@ void Model::buildStats()
       s.bytes -= 2.0 * 3 * at.numel;
     }
     if (sib_[ni].empty()) continue;
-    // merged siblings: x once, every member's output; the lead carries the whole launch
+    // merged siblings: x once (grouped: each member's own input), every member's output; the
+    // lead carries the whole launch
     int cout = 0;
     for (int j : sib_[ni]) {
       if (j != (int)ni) {
         NodeStat & m = stats_[j];
         s.flops += m.flops;
-        s.bytes += 2.0 * T_[nodes_[j].outs[0]]->numel;
+        s.bytes += 2.0 * T_[nodes_[j].outs[0]]->numel + (sib_grouped_[ni] ? 2.0 * T_[nodes_[j].ins[0]]->numel : 0.0);
         m.flops = m.bytes = 0;
       }
       cout += T_[nodes_[j].outs[0]]->C;
@@ -2787,7 +2853,7 @@ void Model::buildStats()
     const auto arrow = s.desc.find("->"), x = s.desc.find('x', arrow);
     if (arrow != std::string::npos && x != std::string::npos)
       s.desc = s.desc.substr(0, arrow + 2) + std::to_string(cout) + s.desc.substr(x) + " (" +
-               std::to_string(sib_[ni].size()) + " siblings)";
+               std::to_string(sib_[ni].size()) + (sib_grouped_[ni] ? " groups)" : " siblings)");
   }
 }
 

@@ -132,8 +132,14 @@ class Model {
   void findSiblings();
   std::vector<std::vector<int>> sib_;
   std::vector<int> sib_lead_;
+  // grouped siblings: 3x3 convs 64 -> 64 whose inputs are consecutive 64-channel views of one
+  // merged root (the branches' second convs) run as one grouped launch; sib_x_[lead] = the
+  // tensor of the first group's input
+  std::vector<char> sib_grouped_;
+  std::vector<std::string> sib_x_;
   // the launch of a conv node (conv1x1 / conv3x3 / conv_general) at a batch size
-  Launch convLaunch(size_t ni, int batch);
+  // grouped: a grouped-siblings lead's one launch for all its members (packed_grp_)
+  Launch convLaunch(size_t ni, int batch, bool grouped = false);
   // node ni and its pair partner as one kPair launch; false when a view does not suit it
   bool pairLaunch(size_t ni, int batch, Launch & L);
   void validate(const Launch & l) const;
@@ -167,6 +173,7 @@ class Model {
     void * dev = nullptr;  // device copy of the packed operand blob
   };
   std::vector<Packed> packed_;              // per node
+  std::vector<Packed> packed_grp_;          // grouped-siblings leads: the members' weights together
   float * ws_ = nullptr;                    // split-K partials
   size_t ws_floats_ = 0;
 

@@ -104,6 +104,9 @@ struct ConvParams {
   // (H / 2) x (W / 2), at pixel (oy / 2, ox / 2); channels cu.. from x as usual
   View xu;
   int cu = 0;
+  // grouped launch (the resident-weight ping-pong kernel): output channel block y (64
+  // channels) reads input channels y * xg .. y * xg + Cin - 1 of x (0: every block reads 0..)
+  int xg = 0;
   // divisions by Ho * Wo and by Wo (set by the implicit-GEMM launcher)
   FastDiv dv_hwo, dv_wo;
 };

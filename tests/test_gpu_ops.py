@@ -896,11 +896,12 @@ def test_upsample_concat_fused(tmp_path, ca, cb, cout, H, W, batch, reuse_a, fus
 def _head_plan(d, cin, H, W, widths=(51, 64, 64)):
     """A Pose head level: three branches whose first 3x3 convs read the same x (here the
     keypoint branch, 51 channels, comes first in node order as in the written plans), each
-    followed by its own 3x3 conv; the three branch outputs concatenated."""
+    followed by its own 3x3 conv and a 1x1 conv; the three branch outputs concatenated."""
     def build(pb):
         x = pb.conv(pb.input("x", [1, cin, H, W]), cin, 1, act=pw.ACT_SILU)
         firsts = [pb.conv(x, c, 3, 1, act=pw.ACT_SILU) for c in widths]
-        return pb.concat([pb.conv(f, c, 3, 1, act=pw.ACT_SILU) for f, c in zip(firsts, widths)])
+        seconds = [pb.conv(f, c, 3, 1, act=pw.ACT_SILU) for f, c in zip(firsts, widths)]
+        return pb.concat([pb.conv(t, 16, 1, act=pw.ACT_NONE) for t in seconds])
     return _small_plan(d, build)
 
 
@@ -919,8 +920,12 @@ def test_sibling_convs_merged(tmp_path, cin, H, W, batch, widths):
     tags = _conv_tags(path, batch)
     assert sum(f"siblings={len(widths)} cout={sum(widths)}" in t for t in tags) == 1, tags
     assert not any("siblings" in t for t in _conv_tags(path, batch, ia.IVH_FLAG_NO_FUSE_SIBLINGS))
+    # the 64-channel branches' second convs read consecutive 64-channel views of the merged
+    # root: one grouped launch on the ping-pong kernel
+    grouped = widths.count(64) >= 2
+    assert sum("groups=2 cout=128" in t for t in tags) == (1 if grouped else 0), tags
     kinds = _kernels(path, batch)
-    assert kinds.count("(fused)") == len(widths) - 1, kinds
+    assert kinds.count("(fused)") == len(widths) - 1 + (1 if grouped else 0), kinds
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
     _, _, sep = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_FUSE_SIBLINGS)
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(sep[0]))

@@ -573,4 +573,9 @@ def test_sibling_conv_merge(plans):
                     # blocks; P4 / P5 (128 / 256 in): the wide-layer kernel
                     kinds = [t.split()[0] for t in tags if per_level in t]
                     assert kinds == ["conv_res", "conv_wide", "conv_wide"], kinds
+                # YOLOv8n: the box and class branches' second convs (64 -> 64 on consecutive
+                # 64-channel views) as one grouped ping-pong launch per level
+                grouped = [t for t in tags if "groups=2 cout=128" in t]
+                assert len(grouped) == (3 if merged and name == "yolov8n-pose" else 0), (name, b, grouped)
+                assert all(t.startswith("conv_res cfg=3") for t in grouped)
             m.close()
