@@ -1318,19 +1318,30 @@ void Model::uploadWeights()
     ConvSpec cs;
     cs.Cout = (int)wt.dims.at(0);
     // merged siblings: the members' weights and biases concatenated over output channels
+    // (grouped: each member's input channels zero-padded to 64; the last member's rows padded
+    // with zero rows up to the launch's output channels)
     std::vector<uint16_t> Wm, Bm;
+    const bool grp = merged && sib_grouped_[ni];
+    const int mcin = grp ? 64 : (int)wt.dims.at(1);
     if (merged) {
       cs.Cout = 0;
-      for (int j : sib_[ni]) {
-        const PlanNode & m = nodes_[j];
+      for (size_t k = 0; k < sib_[ni].size(); ++k) {
+        const PlanNode & m = nodes_[sib_[ni][k]];
         const Tensor & mw = *T_[m.ins.at(1)];
         const std::vector<uint16_t> & hw = host.at(m.ins.at(1));
         const std::vector<uint16_t> & hb = host.at(m.ins.at(2));
-        if (mw.numel != (long)mw.dims[0] * wt.dims[1] * 9 || (long)hb.size() < mw.dims[0])
+        const int co = (int)mw.dims[0], ci = (int)mw.dims[1];
+        if (mw.dims.size() != 4 || mw.numel != (long)co * ci * 9 || ci > mcin || (!grp && ci != mcin) ||
+            (long)hb.size() < co)
           throw std::runtime_error("merged sibling conv weights: " + m.outs[0]);
-        Wm.insert(Wm.end(), hw.begin(), hw.end());
-        Bm.insert(Bm.end(), hb.begin(), hb.begin() + mw.dims[0]);
-        cs.Cout += (int)mw.dims[0];
+        const int rows = k + 1 == sib_[ni].size() ? sib_cout_[ni] - cs.Cout : co;
+        if (rows < co) throw std::runtime_error("merged sibling conv rows: " + m.outs[0]);
+        for (int r = 0; r < rows; ++r) {
+          for (int c = 0; c < mcin; ++c)
+            for (int t = 0; t < 9; ++t) Wm.push_back(r < co && c < ci ? hw[((size_t)r * ci + c) * 9 + t] : 0);
+          Bm.push_back(r < co ? hb[r] : 0);
+        }
+        cs.Cout += rows;
       }
       Wp = &Wm;
     }
@@ -1339,7 +1350,7 @@ void Model::uploadWeights()
     cs.G = isg ? n.i("G", 1) : 1;
     const int cin_g = (int)(wt.numel / ((long)wt.dims.at(0) * cs.K * cs.K));
     const Tensor & x = *T_[is1 ? n.ins.at(1) : n.ins.at(0)];
-    cs.Cin = is1 ? (int)wt.dims.at(1) : cin_g * cs.G;
+    cs.Cin = is1 ? (int)wt.dims.at(1) : (grp ? mcin : cin_g * cs.G);
     if (is1) {
       const long N = x.numel / std::max(cs.Cin, 1);
       if (x.dims.size() == 4 && (long)x.H * x.W == N && x.C == cs.Cin) { cs.H = x.H; cs.W = x.W; }
@@ -1504,6 +1515,7 @@ void Model::findSiblings()
   sib_lead_.assign(nodes_.size(), -1);
   sib_grouped_.assign(nodes_.size(), 0);
   sib_x_.assign(nodes_.size(), std::string());
+  sib_cout_.assign(nodes_.size(), 0);
   if (flags_ & (IVH_FLAG_NO_FUSE | IVH_FLAG_NO_FUSE_SIBLINGS | IVH_FLAG_NCHW_ONLY | IVH_FLAG_DIRECT_ONLY)) return;
   std::map<std::string, std::vector<int>> readers;
   for (size_t i = 0; i < nodes_.size(); ++i)
@@ -1561,6 +1573,16 @@ void Model::findSiblings()
       sib_lead_[j] = (int)i;
     }
     sib_[i] = even;
+    int sum = 0;
+    bool blocks = true;
+    for (size_t k = 0; k < even.size(); ++k) {
+      const int c = T_.at(nodes_[even[k]].outs[0])->C;
+      sum += c;
+      if (k + 1 < even.size() ? c % 64 != 0 : c > 64) blocks = false;
+    }
+    const int act = a.i("act");
+    const bool act0 = act == kActNone || act == kActSiLU || act == kActReLU || act == kActHSwish;  // act(0) = 0
+    sib_cout_[i] = blocks && act0 ? 64 * (int)even.size() : sum;
   }
   // Grouped siblings: the merged members' own next convs (3x3 stride 1, 64 -> 64, each the
   // one reader of its member's output) read consecutive 64-channel views of the merged root;
@@ -1570,20 +1592,29 @@ void Model::findSiblings()
   const size_t n_first = nodes_.size();
   for (size_t i = 0; i < n_first; ++i) {
     if (sib_[i].empty() || sib_grouped_[i]) continue;
+    // the last member's output may be narrower than 64 channels when the merge writes its
+    // padding channels (zeros): its next conv then runs as a 64-channel group of zero-padded
+    // weights
+    const bool padded = sib_cout_[i] == 64 * (int)sib_[i].size();
     std::vector<int> tw;
-    int off = 0;
-    for (int m : sib_[i]) {
-      const Tensor & t = *T_.at(nodes_[m].outs[0]);
+    int off = 0, cout = 0;
+    for (size_t k = 0; k < sib_[i].size(); ++k) {
+      const Tensor & t = *T_.at(nodes_[sib_[i][k]].outs[0]);
+      const bool last = k + 1 == sib_[i].size();
       const auto it = readers.find(t.name);
-      if (t.C != 64 || off != 64 * (int)tw.size() || it == readers.end() || it->second.size() != 1) break;
+      if (!(t.C == 64 || (last && padded && t.C < 64)) || off != 64 * (int)tw.size() || it == readers.end() ||
+          it->second.size() != 1)
+        break;
       const int r = it->second[0];
       const PlanNode & rn = nodes_[r];
+      const auto & wd = T_.at(rn.ins[1])->dims;
       if (taken[r] || !member_ok(r) || rn.ins[0] != t.name || rn.i("stride", 1) != 1 || rn.i("pad", 1) != 1 ||
-          T_.at(rn.ins[1])->dims != std::vector<int64_t>{64, 64, 3, 3} || rn.i("Hout") != t.H || rn.i("Wout") != t.W ||
-          (!tw.empty() && rn.i("act") != nodes_[tw[0]].i("act")))
+          wd.size() != 4 || wd[1] != t.C || wd[2] != 3 || wd[3] != 3 || wd[0] > 64 || (!last && wd[0] != 64) ||
+          rn.i("Hout") != t.H || rn.i("Wout") != t.W || (!tw.empty() && rn.i("act") != nodes_[tw[0]].i("act")))
         break;
       tw.push_back(r);
-      off += t.C;
+      off += 64;
+      cout += (int)wd[0];
     }
     if (tw.size() < 2) continue;
     const int lead = *std::min_element(tw.begin(), tw.end());
@@ -1594,6 +1625,7 @@ void Model::findSiblings()
     sib_[lead] = tw;
     sib_grouped_[lead] = 1;
     sib_x_[lead] = nodes_[sib_[i][0]].outs[0];
+    sib_cout_[lead] = cout;
   }
 }
 
@@ -1657,10 +1689,10 @@ Launch Model::convLaunch(size_t ni, int batch, bool grouped)
     // merged siblings: all members' channels, written from channel 0 of their shared root
     const Tensor * ymerged = nullptr;
     if (!sib_[ni].empty() && (grouped || !sib_grouped_[ni])) {
-      p.Cout = 0;
-      for (int j : sib_[ni]) p.Cout += T_[nodes_[j].outs[0]]->C;
+      p.Cout = sib_cout_[ni];
       ymerged = T_[nodes_[sib_[ni][0]].outs[0]].get();
-      if (ymerged->coff != 0 || roots_.at(ymerged->root)->C != p.Cout) fail("merged sibling root");
+      const Root & mr = *roots_.at(ymerged->root);
+      if (ymerged->coff != 0 || p.Cout < mr.C || p.Cout > (mr.layout == kNHWC ? mr.cs : mr.C)) fail("merged sibling root");
     }
     if (is1) {
       p.Cin = (int)wt.dims[1];
@@ -1671,7 +1703,8 @@ Launch Model::convLaunch(size_t ni, int batch, bool grouped)
       p.K = 1; p.S = 1; p.P = 0; p.G = 1;
       p.Ho = p.H; p.Wo = p.W;
     } else {
-      p.Cin = xt.C; p.H = xt.H; p.W = xt.W;
+      p.Cin = grouped ? 64 : xt.C;
+      p.H = xt.H; p.W = xt.W;
       p.K = is3 ? 3 : n.i("K", 3);
       p.S = is3 ? n.i("stride", 1) : n.i("S", 1);
       p.P = is3 ? n.i("pad", 1) : n.i("P", 1);
@@ -1679,12 +1712,11 @@ Launch Model::convLaunch(size_t ni, int batch, bool grouped)
       p.Ho = n.i("Hout"); p.Wo = n.i("Wout");
       if (p.Ho != (p.H + 2 * p.P - p.K) / p.S + 1 || p.Wo != (p.W + 2 * p.P - p.K) / p.S + 1)
         fail("Hout/Wout inconsistent with input geometry");
-      if (wt.numel != (ymerged ? wt.dims[0] : (long)p.Cout) * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
+      if (!ymerged && wt.numel != (long)p.Cout * (p.Cin / p.G) * p.K * p.K) fail("weight shape mismatch");
     }
     if (p.G < 1 || p.Cin % p.G || p.Cout % p.G) fail("bad groups");
     const Tensor & yv = ymerged ? *ymerged : yt;
-    if (ymerged ? (long)p.Cout * yv.H * yv.W != roots_.at(yv.root)->numel || yv.H != p.Ho || yv.W != p.Wo
-                : yt.numel != (long)p.Cout * p.Ho * p.Wo)
+    if (ymerged ? yv.H != p.Ho || yv.W != p.Wo : yt.numel != (long)p.Cout * p.Ho * p.Wo)
       fail("output numel mismatch");
     p.act = n.i("act");
     p.x = view(grouped ? sib_x_[ni] : xt.name, batch);

@@ -137,6 +137,10 @@ class Model {
   // tensor of the first group's input
   std::vector<char> sib_grouped_;
   std::vector<std::string> sib_x_;
+  // the launch's output channels: the members' sum, or for a merge whose members but the last
+  // are whole 64-channel blocks 64 per member (the last member's padding channels written as
+  // act(0) = 0 by zero weight rows, so a grouped launch may read them as its last group)
+  std::vector<int> sib_cout_;
   // the launch of a conv node (conv1x1 / conv3x3 / conv_general) at a batch size
   // grouped: a grouped-siblings lead's one launch for all its members (packed_grp_)
   Launch convLaunch(size_t ni, int batch, bool grouped = false);

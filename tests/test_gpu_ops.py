@@ -918,14 +918,15 @@ def test_sibling_convs_merged(tmp_path, cin, H, W, batch, widths):
     against the branches run one by one."""
     path = _head_plan(tmp_path, cin, H, W, widths)
     tags = _conv_tags(path, batch)
-    assert sum(f"siblings={len(widths)} cout={sum(widths)}" in t for t in tags) == 1, tags
-    assert not any("siblings" in t for t in _conv_tags(path, batch, ia.IVH_FLAG_NO_FUSE_SIBLINGS))
-    # the 64-channel branches' second convs read consecutive 64-channel views of the merged
-    # root: one grouped launch on the ping-pong kernel
-    grouped = widths.count(64) >= 2
-    assert sum("groups=2 cout=128" in t for t in tags) == (1 if grouped else 0), tags
+    # the merge writes 64 channels per branch (the keypoint branch's 51 padded with zero rows),
+    # and the branches' second convs, reading consecutive 64-channel views of it, run as one
+    # grouped launch on the ping-pong kernel (the keypoint group's weights zero-padded)
+    n = len(widths)
+    assert sum(f"siblings={n} cout={64 * n}" in t for t in tags) == 1, tags
+    assert sum(f"groups={n} cout={sum(widths)}" in t for t in tags) == 1, tags
+    assert not any("siblings" in t or "groups" in t for t in _conv_tags(path, batch, ia.IVH_FLAG_NO_FUSE_SIBLINGS))
     kinds = _kernels(path, batch)
-    assert kinds.count("(fused)") == len(widths) - 1 + (1 if grouped else 0), kinds
+    assert kinds.count("(fused)") == 2 * (n - 1), kinds
     got = _check_f32(path, batch, lo=-1.0, ref_mode=False)
     _, _, sep = _run(path, batch, lo=-1.0, flags=ia.IVH_FLAG_NO_FUSE_SIBLINGS)
     mean_rel, max_rel, _, _ = O.rel_errors(O.h2f(got[0]), O.h2f(sep[0]))

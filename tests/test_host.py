@@ -558,9 +558,11 @@ def test_upsample_concat_fusion(plans, name):
 
 def test_sibling_conv_merge(plans):
     """The Pose heads' first 3x3 convs per level (YOLOv8n: box, class and keypoint branches,
-    64 + 64 + 51 channels; YOLO11n: box and keypoint, 64 + 51, its class branch starting with
-    a depthwise conv) run as one conv per level; IVH_FLAG_NO_FUSE_SIBLINGS runs them apart."""
-    for name, per_level in (("yolov8n-pose", "siblings=3 cout=179"), ("yolo11n-pose", "siblings=2 cout=115")):
+    64 + 64 + 51 channels, written as 3 x 64; YOLO11n: box and keypoint, 64 + 51 as 2 x 64, its
+    class branch starting with a depthwise conv) run as one conv per level, their second convs
+    as one grouped launch; IVH_FLAG_NO_FUSE_SIBLINGS runs them apart."""
+    for name, per_level, groups in (("yolov8n-pose", "siblings=3 cout=192", "groups=3 cout=179"),
+                                    ("yolo11n-pose", "siblings=2 cout=128", "groups=2 cout=115")):
         for flags, merged in ((0, True), (ia.IVH_FLAG_NO_FUSE_SIBLINGS, False)):
             m = ia.PlanModel(plans(name)[0], 0, 64, DRY | flags)
             for b in (1, 64):
@@ -573,9 +575,10 @@ def test_sibling_conv_merge(plans):
                     # blocks; P4 / P5 (128 / 256 in): the wide-layer kernel
                     kinds = [t.split()[0] for t in tags if per_level in t]
                     assert kinds == ["conv_res", "conv_wide", "conv_wide"], kinds
-                # YOLOv8n: the box and class branches' second convs (64 -> 64 on consecutive
-                # 64-channel views) as one grouped ping-pong launch per level
-                grouped = [t for t in tags if "groups=2 cout=128" in t]
-                assert len(grouped) == (3 if merged and name == "yolov8n-pose" else 0), (name, b, grouped)
+                # the branches' second convs (on consecutive 64-channel views of the merged
+                # root, the keypoint branch's 51 channels zero-padded) as one grouped ping-pong
+                # launch per level
+                grouped = [t for t in tags if groups in t]
+                assert len(grouped) == (3 if merged else 0), (name, b, grouped)
                 assert all(t.startswith("conv_res cfg=3") for t in grouped)
             m.close()
