@@ -102,6 +102,8 @@ MODEL_LAYERS = [
     ("heads_64_80", 64, 179, 80, 80, 3, 1),
     ("heads_128_40", 128, 179, 40, 40, 3, 1),
     ("heads_256_20", 256, 179, 20, 20, 3, 1),
+    # the same with each branch's second 3x3 conv, which run as one grouped launch
+    ("heads2_64_80", 64, 179, 80, 80, 3, 1),
 ]
 
 
@@ -123,6 +125,9 @@ def sweep_plan(pw, d, name):
         if name.startswith("pair"):
             t = pb.conv(x, cout, 3, 1)
             y = pb.conv(t, cout, 3, 1, res=x)
+        elif name.startswith("heads2"):
+            # first and second 3x3 convs of each branch, then a 1x1 conv
+            y = pb.concat([pb.conv(pb.conv(pb.conv(x, c, 3, 1), c, 3, 1), 16, 1) for c in (51, 64, 64)])
         elif name.startswith("heads"):
             # keypoint branch first, as in the written plans; each branch output read by a conv
             y = pb.concat([pb.conv(pb.conv(x, c, 3, 1), 16, 1) for c in (51, 64, 64)])

@@ -2886,6 +2886,12 @@ void Model::buildStats()
     if (arrow != std::string::npos && x != std::string::npos)
       s.desc = s.desc.substr(0, arrow + 2) + std::to_string(cout) + s.desc.substr(x) + " (" +
                std::to_string(sib_[ni].size()) + (sib_grouped_[ni] ? " groups)" : " siblings)");
+    if (sib_grouped_[ni]) {  // a grouped conv: 64 input channels per group
+      const auto sp = s.desc.find(' '), xi = s.desc.find('x', sp), g1 = s.desc.find(" g1 ");
+      if (sp != std::string::npos && xi != std::string::npos && g1 != std::string::npos)
+        s.desc = s.desc.substr(0, sp + 1) + std::to_string(64 * sib_[ni].size()) + s.desc.substr(xi, g1 + 2 - xi) +
+                 std::to_string(sib_[ni].size()) + s.desc.substr(g1 + 3);
+    }
   }
 }
 
